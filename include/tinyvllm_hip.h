@@ -1,0 +1,201 @@
+/*
+ * tinyvllm_hip.h -- C ABI of the gfx950 (MI355X) kernels behind tiny-vLLM's
+ * decode token loop.
+ *
+ * Every entry point takes plain device pointers, element counts, element
+ * strides and the hipStream_t to launch on (pass torch's current stream so
+ * the launch is ordered with, and capturable into, the caller's graph).
+ * None of them allocates, synchronises or reads device memory on the host.
+ *
+ * Return value: 0 on success; a negative TVLLM_E* code otherwise, with a
+ * human-readable message available from tvllm_last_error() (thread-local).
+ * Argument checks mirror the TORCH_CHECK contracts of the reference's host
+ * functions; value validity (slot ranges, block ids) is the caller's job, as
+ * in the reference, where it is validated on the CPU before launch.
+ *
+ * Element types: TVLLM_BF16 / TVLLM_F16 for every op; TVLLM_F32 is also
+ * accepted by the row-wise pointwise ops (rms_norm, silu_and_mul), like the
+ * reference's pointwise.cu dispatch.
+ */
+#ifndef TINYVLLM_HIP_H
+#define TINYVLLM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tvllm_stream_t; /* == hipStream_t */
+
+enum tvllm_dtype { TVLLM_BF16 = 0, TVLLM_F16 = 1, TVLLM_F32 = 2 };
+
+enum tvllm_status {
+    TVLLM_OK = 0,
+    TVLLM_EINVAL = -1,   /* shape / stride / dtype contract violated  */
+    TVLLM_ELAUNCH = -2,  /* hipLaunchKernel (or hipGetLastError) failed */
+};
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* tvllm_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int tvllm_abi_version(void);
+
+/* Scatter K/V rows into the paged cache: cache[slot[t]] = key[t] (bit copy).
+ * slot == -1 skips the row (graph padding).
+ * key/value: [tokens, kv_heads, head_dim] with the given element strides
+ * (last stride must be 1); caches: contiguous [num_slots, kv_heads, head_dim].
+ * Replaces: torch.ops.tinyvllm_cuda.store_kv
+ *           (reference tinyvllm/kernels/kv_store.cu:101-232, wrapper
+ *            tinyvllm/kernels/kv_store.py:10-30). */
+int tvllm_store_kv(const void* key, const void* value,
+                   int64_t key_token_stride, int64_t key_head_stride,
+                   int64_t value_token_stride, int64_t value_head_stride,
+                   void* key_cache, void* value_cache,
+                   const int64_t* slots, int64_t num_tokens,
+                   int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
+                   int dtype, tvllm_stream_t stream);
+
+/* Bytes of device workspace tvllm_paged_decode needs for this geometry
+ * (split-K partial results). 0 means no workspace is needed.
+ * max_context_len bounds the context of any row (the engine's
+ * max_model_len); it only sizes the split count, never the grid's validity. */
+int64_t tvllm_paged_decode_workspace_size(int64_t num_rows, int64_t num_heads,
+                                          int64_t num_kv_heads,
+                                          int64_t head_dim,
+                                          int64_t max_context_len,
+                                          int64_t block_size);
+
+/* Single-query paged attention for decode rows.
+ * For r < num_rows, h < num_heads:
+ *   out[rows[r], h] = softmax_t(scale * q[rows[r], h] . k_t) @ v_t,
+ *   t < lengths[r], token t at slot blocks[offsets[r] + t / bs] * bs + t % bs
+ *   of KV head h / (num_heads / num_kv_heads). lengths[r] == 0 -> zeros.
+ * q, out: [*, num_heads, head_dim] with element strides (last == 1).
+ * k_cache, v_cache: contiguous [num_slots, num_kv_heads, head_dim].
+ * rows, offsets (num_rows + 1), lengths, blocks: int64 device vectors.
+ * workspace: >= tvllm_paged_decode_workspace_size(...) bytes (may be NULL
+ * when that size is 0). head_dim must be 64 or 128.
+ * Replaces: torch.ops.tinyvllm_cuda.paged_decode
+ *           (reference tinyvllm/kernels/paged_decode.cu:469-669, wrapper
+ *            tinyvllm/kernels/paged_decode.py:10-32). */
+int tvllm_paged_decode(const void* q, int64_t q_token_stride,
+                       int64_t q_head_stride, const void* k_cache,
+                       const void* v_cache, void* out,
+                       int64_t out_token_stride, int64_t out_head_stride,
+                       const int64_t* rows, const int64_t* blocks,
+                       const int64_t* offsets, const int64_t* lengths,
+                       int64_t num_rows, int64_t num_heads,
+                       int64_t num_kv_heads, int64_t head_dim,
+                       int64_t num_slots, int64_t block_size,
+                       int64_t max_context_len, float scale,
+                       void* workspace, int64_t workspace_bytes,
+                       int dtype, tvllm_stream_t stream);
+
+/* RMSNorm over rows of width `width`, optionally after a residual add:
+ *   x = residual ? round(x + residual) : x
+ *   out = round(round(x * rsqrt(mean(x^2) + eps)) * weight)
+ *   residual_out = x            (only when residual != NULL)
+ * Input rows: count = tokens * heads; row (t, h) starts at
+ * t * token_stride + h * head_stride (heads == 1, head_stride == 0 for 2-D).
+ * residual rows: t * residual_stride. out / residual_out: dense [count, width].
+ * Replaces: torch.ops.tinyvllm_cuda.rms_norm / add_rms_norm
+ *           (reference tinyvllm/kernels/pointwise.cu:549-616). */
+int tvllm_rms_norm(const void* input, int64_t tokens, int64_t heads,
+                   int64_t width, int64_t token_stride, int64_t head_stride,
+                   const void* weight, const void* residual,
+                   int64_t residual_stride, void* out, void* residual_out,
+                   float eps, int dtype, tvllm_stream_t stream);
+
+/* out[r, c] = round(round(silu(x[r, c])) * x[r, c + width / 2]) for rows
+ * laid out like tvllm_rms_norm's input; out is dense [count, width / 2].
+ * Replaces: torch.ops.tinyvllm_cuda.silu_and_mul
+ *           (reference tinyvllm/kernels/pointwise.cu:619-680). */
+int tvllm_silu_and_mul(const void* input, int64_t tokens, int64_t heads,
+                       int64_t width, int64_t token_stride,
+                       int64_t head_stride, void* out, int dtype,
+                       tvllm_stream_t stream);
+
+/* Per-head Q/K RMSNorm followed by half-split RoPE, with every rounding
+ * point of the reference expression:
+ *   n = round(round(x * inv_rms) * w);
+ *   o1 = round(round(n1 * cos) - round(n2 * sin));
+ *   o2 = round(round(n2 * cos) + round(n1 * sin)).
+ * q: [tokens, num_heads, head_dim], k: [tokens, num_kv_heads, head_dim],
+ * element strides, last stride 1. cos/sin: contiguous [tokens, head_dim/2].
+ * q_out, k_out: dense [tokens, heads, head_dim].
+ * Fused KV write (not in the reference, which runs store_kv afterwards):
+ * when key_cache != NULL, the rotated K row and the V row
+ * (v: [tokens, num_kv_heads, head_dim] with the given strides) are also
+ * written to key_cache/value_cache[slots[t]] (slot -1 skips); k_out may then
+ * be NULL.
+ * Replaces: torch.ops.tinyvllm_cuda.qk_norm_rope
+ *           (reference tinyvllm/kernels/pointwise.cu:453-546) and, when
+ *           fused, the following store_kv (runtime/attention.py:219-233). */
+int tvllm_qk_norm_rope(const void* q, int64_t q_token_stride,
+                       int64_t q_head_stride, const void* k,
+                       int64_t k_token_stride, int64_t k_head_stride,
+                       const void* q_weight, const void* k_weight,
+                       const void* cos, const void* sin, int64_t tokens,
+                       int64_t num_heads, int64_t num_kv_heads,
+                       int64_t head_dim, float q_eps, float k_eps,
+                       void* q_out, void* k_out,
+                       const void* v, int64_t v_token_stride,
+                       int64_t v_head_stride, void* key_cache,
+                       void* value_cache, const int64_t* slots,
+                       int64_t num_slots, int dtype, tvllm_stream_t stream);
+
+/* Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
+ * (row stride row_stride elements). NaN compares greater than any number,
+ * as torch.argmax does.
+ * Replaces: logits.argmax(dim=-1) in TorchSampler.sample
+ *           (reference tinyvllm/sampling.py:42-43). */
+int tvllm_argmax(const void* logits, int64_t rows, int64_t vocab,
+                 int64_t row_stride, int64_t* out, int dtype,
+                 tvllm_stream_t stream);
+
+/* Temperature / top-k / top-p sampling by the exponential race:
+ *   s = (logit - max) / temperature;  keep the top_k largest (0 = all);
+ *   keep the smallest prefix of the descending order whose probability
+ *   mass exceeds top_p (ties broken by lower index);
+ *   out[r] = argmax_{kept i} p_i / E_i,  E_i ~ Exp(1) from a counter-based
+ *   Philox4x32-10 stream keyed by (seeds[r], counters[r], i).
+ * temperature > 0. workspace: tvllm_sample_workspace_size(rows, vocab).
+ * Replaces: TorchSampler._sample_batch (reference tinyvllm/sampling.py:75-164);
+ *           the noise stream differs from torch.Generator's. */
+int64_t tvllm_sample_workspace_size(int64_t rows, int64_t vocab);
+int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
+                 int64_t row_stride, const float* temperature,
+                 const int64_t* top_k, const float* top_p,
+                 const int64_t* seeds, const int64_t* counters,
+                 int64_t* out, void* workspace, int64_t workspace_bytes,
+                 int dtype, tvllm_stream_t stream);
+
+/* Causal paged attention for multi-token query rows (chunked prefill).
+ * Item i owns query tokens q[q_offsets[i] : q_offsets[i+1]], the last
+ * `query_len` of its `context_lens[i]` tokens (lower-right causal mask:
+ * query j of the item sees tokens t <= context_lens[i] - query_len + j).
+ * K/V of all context tokens (including this chunk's, already written)
+ * come from the paged cache through blocks/block_offsets as in
+ * tvllm_paged_decode. Items with q_offsets[i+1] - q_offsets[i] <= 0 are
+ * skipped. max_query_len bounds every item's query length (grid size).
+ * Replaces: CudaAttention._attend's per-row gather + SDPA for rows with
+ * history (reference tinyvllm/runtime/attention.py:102-151, 235-285). */
+int tvllm_paged_prefill(const void* q, int64_t q_token_stride,
+                        int64_t q_head_stride, const void* k_cache,
+                        const void* v_cache, void* out,
+                        int64_t out_token_stride, int64_t out_head_stride,
+                        const int64_t* q_offsets, const int64_t* blocks,
+                        const int64_t* block_offsets,
+                        const int64_t* context_lens, int64_t num_items,
+                        int64_t max_query_len, int64_t num_heads,
+                        int64_t num_kv_heads, int64_t head_dim,
+                        int64_t num_slots, int64_t block_size, float scale,
+                        int dtype, tvllm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TINYVLLM_HIP_H */

@@ -1,0 +1,63 @@
+"""The C-ABI library loads (no GPU needed) and exports every declared symbol."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tinyvllm_hip.h"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"\b(tvllm_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declares_the_bound_entry_points():
+    from tinyvllm.kernels._extension import EXPORTED_SYMBOLS
+
+    assert declared_symbols() == set(EXPORTED_SYMBOLS)
+
+
+def test_library_loads_and_exports_every_symbol():
+    from tinyvllm.kernels._extension import LIBRARY_PATH, load_kernels
+
+    if not LIBRARY_PATH.exists():
+        pytest.fail("libtinyvllm_hip.so is not built (run __graft_entry__.build())")
+    lib = load_kernels()
+    for name in sorted(declared_symbols()):
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+    assert lib.tvllm_abi_version() == 1
+    assert lib.tvllm_last_error() == b""
+
+
+def test_argument_errors_surface_without_touching_a_gpu():
+    """Contract violations are rejected on the host before any launch."""
+    from tinyvllm.kernels._extension import check, load_kernels
+
+    lib = load_kernels()
+    status = lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
+                                4, 8, 128, 64, 7, None)
+    assert status == -1
+    with pytest.raises(RuntimeError, match="float16 or bfloat16"):
+        check(status)
+    status = lib.tvllm_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None,
+                                    None, None, 1, 6, 4, 128, 64, 16, 64, 1.0,
+                                    None, 0, 0, None)
+    with pytest.raises(RuntimeError, match="GQA"):
+        check(status)
+    # Zero-sized work is a no-op that never dereferences pointers.
+    assert lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
+                              0, 8, 128, 64, 0, None) == 0
+
+
+def test_decode_workspace_sizes():
+    from tinyvllm.kernels._extension import load_kernels
+
+    lib = load_kernels()
+    # 8B shape at bs64: 512 (row, kv-head) units -> 4 splits of a 4096 context.
+    assert lib.tvllm_paged_decode_workspace_size(64, 32, 8, 128, 4096, 16) == \
+        64 * 32 * 4 * 130 * 4
+    # Enough rows to fill the chip on their own: no split, no workspace.
+    assert lib.tvllm_paged_decode_workspace_size(512, 32, 8, 128, 4096, 16) == 0

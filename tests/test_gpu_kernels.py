@@ -1,0 +1,333 @@
+"""HIP kernels vs the CPU oracle on identical seeded inputs (C1/C2 recipes).
+
+Integer/byte work (KV writes, slot indexing, argmax indices) must be
+bit-exact; floating-point outputs must meet max abs err <= 2e-2 and mean
+relative (L1) error <= 1e-3 against the oracle rounded to the same dtype.
+"""
+import math
+
+import pytest
+import torch
+
+from helpers import assert_bf16_close, paged_decode_case
+from oracle import attention as OA
+from oracle import paged_kv as OK
+from oracle import pointwise as OP
+
+pytestmark = pytest.mark.gpu
+
+
+def _Cache(k, v, block_size):
+    """A one-layer PagedKVCache wrapping existing K/V tensors."""
+    from tinyvllm.paged_kv import PagedKVCache
+
+    cache = PagedKVCache.__new__(PagedKVCache)
+    cache.key, cache.value = k[None], v[None]
+    cache.num_layers, cache.block_size = 1, block_size
+    cache.num_slots, cache.num_kv_heads, cache.head_dim = k.shape
+    cache.num_blocks = cache.num_slots // block_size
+    cache.device, cache.dtype = k.device, k.dtype
+    return cache
+
+
+# ------------------------------------------------------------------ store_kv --
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("strided", [False, True])
+def test_store_kv_bit_exact_with_padding(device, dtype, strided):
+    from tinyvllm.kernels.kv_store import store_kv
+
+    g = torch.Generator().manual_seed(11)
+    tokens, hkv, d, slots_total = 256, 8, 128, 16384
+    qkv = torch.randn(tokens, (16 + 2 * hkv) * d, generator=g).to(dtype)
+    if strided:  # K/V as views of a packed QKV projection output
+        k = qkv[:, 16 * d:(16 + hkv) * d].view(tokens, hkv, d)
+        v = qkv[:, (16 + hkv) * d:].view(tokens, hkv, d)
+    else:
+        k = qkv[:, :hkv * d].reshape(tokens, hkv, d).contiguous()
+        v = qkv[:, hkv * d:2 * hkv * d].reshape(tokens, hkv, d).contiguous()
+    slots = torch.randperm(slots_total, generator=g)[:tokens]
+    slots[::7] = -1
+    kc = torch.full((slots_total, hkv, d), 1.5).to(dtype)
+    vc = torch.full((slots_total, hkv, d), -2.5).to(dtype)
+    ek, ev = kc.clone(), vc.clone()
+    OK.kv_write(ek, ev, slots, k.contiguous(), v.contiguous())
+    cache = _Cache(kc.to(device), vc.to(device), 16)
+    if strided:
+        dq = qkv.to(device)
+        dk = dq[:, 16 * d:(16 + hkv) * d].view(tokens, hkv, d)
+        dv = dq[:, (16 + hkv) * d:].view(tokens, hkv, d)
+    else:
+        dk, dv = k.to(device), v.to(device)
+    store_kv(cache, 0, slots.to(device), dk, dv)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.key[0].cpu().view(torch.int16), ek.view(torch.int16))
+    assert torch.equal(cache.value[0].cpu().view(torch.int16), ev.view(torch.int16))
+
+
+# -------------------------------------------------------------- paged decode --
+
+def _run_decode(case, device, max_context_len=None):
+    from tinyvllm.kernels.paged_decode import paged_decode_attention
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    cache = _Cache(case["k"].to(device), case["v"].to(device), case["block_size"])
+    meta = SingleQueryMetadata(
+        case["rows"].to(device), case["blocks"].to(device), case["offsets"].to(device),
+        case["lengths"].to(device), max_context_len,
+    )
+    q = case["q"].to(device)
+    out = torch.full_like(q, 7.0)
+    paged_decode_attention(q, cache, 0, meta, out, scale=case["scale"])
+    torch.cuda.synchronize()
+    expect = torch.full_like(case["q"], 7.0)
+    OA.decode_attention(case["q"], case["k"], case["v"], case["rows"], case["blocks"],
+                        case["offsets"], case["lengths"], case["block_size"],
+                        case["scale"], expect)
+    return out.cpu(), expect
+
+
+def test_decode_c1_qwen3_0p6b_shapes(device):
+    case = paged_decode_case(seed=0, batch=8, heads=16, kv_heads=8)
+    out, expect = _run_decode(case, device, max_context_len=1024)
+    assert_bf16_close(out, expect)
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(8, 8), (16, 8), (32, 8), (40, 8), (64, 8), (64, 4)])
+@pytest.mark.parametrize("max_ctx", [None, 2048])
+def test_decode_gqa_groups_and_splits(device, heads, kv_heads, max_ctx):
+    case = paged_decode_case(seed=heads + kv_heads, batch=5, heads=heads, kv_heads=kv_heads,
+                             pool_blocks=512, min_len=1, max_len=1500)
+    out, expect = _run_decode(case, device, max_context_len=max_ctx)
+    assert_bf16_close(out, expect)
+
+
+def test_decode_edge_lengths_and_padding_rows(device):
+    lengths = [0, 1, 15, 16, 17, 63, 64, 65, 0, 1000]
+    case = paged_decode_case(seed=9, batch=len(lengths), heads=32, kv_heads=8,
+                             pool_blocks=256, lengths=lengths)
+    out, expect = _run_decode(case, device, max_context_len=1024)
+    assert (out[0] == 0).all() and (out[8] == 0).all()
+    assert_bf16_close(out, expect)
+
+
+def test_decode_selected_rows_and_strided_q(device):
+    """query_rows picks rows of a larger token axis; Q is a strided view."""
+    case = paged_decode_case(seed=12, batch=4, heads=32, kv_heads=8, pool_blocks=256,
+                             max_len=700)
+    wide = torch.randn(10, 48, 128).to(torch.bfloat16)
+    q = wide[:, :32]
+    rows = torch.tensor([7, 2, 9, 0])
+    from tinyvllm.kernels.paged_decode import paged_decode_attention
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    cache = _Cache(case["k"].to(device), case["v"].to(device), 16)
+    meta = SingleQueryMetadata(rows.to(device), case["blocks"].to(device),
+                               case["offsets"].to(device), case["lengths"].to(device), 800)
+    out = torch.full((10, 32, 128), 3.0, dtype=torch.bfloat16, device=device)
+    paged_decode_attention(q.to(device), cache, 0, meta, out, scale=case["scale"])
+    expect = torch.full((10, 32, 128), 3.0).to(torch.bfloat16)
+    OA.decode_attention(q, case["k"], case["v"], rows, case["blocks"], case["offsets"],
+                        case["lengths"], 16, case["scale"], expect)
+    assert_bf16_close(out.cpu(), expect)
+
+
+@pytest.mark.parametrize("head_dim,block_size", [(64, 16), (128, 5), (256, 8)])
+def test_decode_generic_shapes(device, head_dim, block_size):
+    case = paged_decode_case(seed=head_dim + block_size, batch=3, heads=4, kv_heads=2,
+                             head_dim=head_dim, block_size=block_size, pool_blocks=300,
+                             max_len=400)
+    out, expect = _run_decode(case, device)
+    assert_bf16_close(out, expect)
+
+
+def test_decode_fp16(device):
+    case = paged_decode_case(seed=21, batch=6, heads=32, kv_heads=8, pool_blocks=512,
+                             dtype=torch.float16)
+    out, expect = _run_decode(case, device, max_context_len=1024)
+    assert_bf16_close(out, expect)
+
+
+# ------------------------------------------------------------- prefill attn --
+
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 8)])
+def test_prefill_chunks_with_history(device, heads, kv_heads):
+    from tinyvllm.kernels.paged_prefill import paged_prefill_attention
+    from tinyvllm.runtime.contracts import MultiQueryMetadata
+
+    g = torch.Generator().manual_seed(31)
+    d, bs, pool = 128, 16, 512
+    # (context, query_len): fresh prompt, chunk with history, short tail, 1-token
+    items = [(70, 70), (600, 128), (513, 1), (300, 45), (1024, 512)]
+    k = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(pool, generator=g).tolist()
+    blocks, boff, qoff = [], [0], [0]
+    for ctx, ql in items:
+        n = math.ceil(ctx / bs)
+        blocks += perm[boff[-1]:boff[-1] + n]
+        boff.append(boff[-1] + n)
+        qoff.append(qoff[-1] + ql)
+    q = torch.randn(qoff[-1], heads, d, generator=g).to(torch.bfloat16)
+    meta_cpu = [torch.tensor(x) for x in (qoff, blocks, boff, [c for c, _ in items])]
+    expect = torch.zeros_like(q)
+    OA.prefill_attention(q, k, v, *meta_cpu, bs, d ** -0.5, expect)
+    cache = _Cache(k.to(device), v.to(device), bs)
+    meta = MultiQueryMetadata(*(t.to(device) for t in meta_cpu),
+                              max_query_len=max(ql for _, ql in items))
+    out = torch.zeros(q.shape, dtype=q.dtype, device=device)
+    paged_prefill_attention(q.to(device), cache, 0, meta, out, scale=d ** -0.5)
+    torch.cuda.synchronize()
+    # P is rounded to bf16 for the MFMA P.V product: allow that on top.
+    assert_bf16_close(out.cpu(), expect, mean_rel=2e-3)
+
+
+# ----------------------------------------------------------------- pointwise --
+
+def _c2_inputs(dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(2)
+    t = 256
+    return dict(
+        x=torch.randn(t, 1024, generator=g).to(dtype),
+        res=torch.randn(t, 1024, generator=g).to(dtype),
+        w=(1 + 0.02 * torch.randn(1024, generator=g)).to(dtype),
+        qkv=torch.randn(t, (16 + 16) * 128, generator=g).to(dtype),
+        qw=(1 + 0.02 * torch.randn(128, generator=g)).to(dtype),
+        kw=(1 + 0.02 * torch.randn(128, generator=g)).to(dtype),
+        pos=torch.randint(0, 2048, (t,), generator=g),
+        gu=torch.randn(t, 6144, generator=g).to(dtype),
+        slots=torch.randperm(16384, generator=g)[:t],
+    )
+
+
+@pytest.mark.parametrize("width", [1024, 4096, 5120, 128, 100, 20000])
+def test_rms_norm_and_add(device, width):
+    from tinyvllm.kernels.pointwise import add_rms_norm, rms_norm
+
+    g = torch.Generator().manual_seed(width)
+    x = torch.randn(37, width, generator=g).to(torch.bfloat16)
+    r = torch.randn(37, width, generator=g).to(torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(width, generator=g)).to(torch.bfloat16)
+    y = rms_norm(x.to(device), w.to(device))
+    assert_bf16_close(y.cpu(), OP.rms_norm(x, w))
+    y2, merged = add_rms_norm(x.to(device), r.to(device), w.to(device))
+    ey, em = OP.add_rms_norm(x, r, w)
+    assert torch.equal(merged.cpu(), em)  # the rounded sum is exact
+    assert_bf16_close(y2.cpu(), ey)
+
+
+def test_rms_norm_3d_strided_and_fp32(device):
+    from tinyvllm.kernels.pointwise import rms_norm
+
+    base = torch.randn(9, 6, 128)
+    x = base[:, 1:5]  # [9, 4, 128] with head stride 128, token stride 768
+    w = 1 + 0.02 * torch.randn(128)
+    y = rms_norm(x.to(device), w.to(device))
+    assert torch.allclose(y.cpu(), OP.rms_norm(x, w), atol=1e-5, rtol=1e-5)
+    xb, wb = x.to(torch.bfloat16), w.to(torch.bfloat16)
+    assert_bf16_close(rms_norm(xb.to(device), wb.to(device)).cpu(), OP.rms_norm(xb, wb))
+
+
+def test_silu_and_mul_c2(device):
+    from tinyvllm.kernels.pointwise import silu_and_mul
+
+    c = _c2_inputs()
+    y = silu_and_mul(c["gu"].to(device))
+    assert_bf16_close(y.cpu(), OP.silu_and_mul(c["gu"]))
+    odd = torch.randn(5, 2 * 37).to(torch.bfloat16)
+    assert_bf16_close(silu_and_mul(odd.to(device)).cpu(), OP.silu_and_mul(odd))
+
+
+def test_qk_norm_rope_c2_and_fused_kv_write(device):
+    from tinyvllm.kernels.pointwise import qk_norm_rope, qk_norm_rope_store
+
+    c = _c2_inputs()
+    t, hq, hkv, d = 256, 16, 8, 128
+    qkv = c["qkv"]
+    q = qkv[:, :hq * d].view(t, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    cos, sin = OP.rope_tables(c["pos"], d, 1e6, torch.bfloat16)
+    eq, ek = OP.qk_norm_rope(q, k, c["qw"], c["kw"], cos, sin)
+    dq = qkv.to(device)
+    gq = dq[:, :hq * d].view(t, hq, d)
+    gk = dq[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    gv = dq[:, (hq + hkv) * d:].view(t, hkv, d)
+    args = (c["qw"].to(device), c["kw"].to(device), cos.to(device), sin.to(device))
+    oq, ok = qk_norm_rope(gq, gk, *args)
+    assert_bf16_close(oq.cpu(), eq)
+    assert_bf16_close(ok.cpu(), ek)
+    # Fused write: same Q bits, and the cache holds exactly the K/V rows the
+    # unfused path produces (bit-exact), untouched elsewhere and at slot -1.
+    slots = c["slots"].clone()
+    slots[5] = -1
+    kc = torch.full((16384, hkv, d), 9.0, dtype=torch.bfloat16, device=device)
+    vc = torch.full((16384, hkv, d), -9.0, dtype=torch.bfloat16, device=device)
+    fq, fk = qk_norm_rope_store(gq, gk, gv, *args, 1e-6, 1e-6, kc, vc, slots.to(device),
+                                key_out=True)
+    assert torch.equal(fq, oq) and torch.equal(fk, ok)
+    ekc = torch.full((16384, hkv, d), 9.0).to(torch.bfloat16)
+    evc = torch.full((16384, hkv, d), -9.0).to(torch.bfloat16)
+    OK.kv_write(ekc, evc, slots, ok.cpu(), v.contiguous())
+    assert torch.equal(kc.cpu().view(torch.int16), ekc.view(torch.int16))
+    assert torch.equal(vc.cpu().view(torch.int16), evc.view(torch.int16))
+
+
+# ------------------------------------------------------------------ sampling --
+
+def test_argmax_exact_with_ties_and_nan(device):
+    from tinyvllm.kernels.sampling import argmax
+
+    g = torch.Generator().manual_seed(4)
+    logits = torch.randn(64, 151936, generator=g).to(torch.bfloat16)
+    logits[3, 100] = logits[3, 90000] = 50.0      # tie -> lower index
+    logits[5, 151935] = 60.0                       # last element
+    assert torch.equal(argmax(logits.to(device)).cpu(), logits.float().argmax(-1))
+    odd = torch.randn(3, 1001).float()
+    odd[1, 7] = float("nan")
+    assert argmax(odd.to(device)).cpu().tolist() == [int(odd[0].argmax()), 7, int(odd[2].argmax())]
+
+
+def test_sample_greedy_rows_and_degenerate_filters(device):
+    from tinyvllm.kernels.sampling import sample
+
+    g = torch.Generator().manual_seed(5)
+    rows, vocab = 6, 50000
+    logits = torch.randn(rows, vocab, generator=g).to(torch.bfloat16)
+    temp = torch.tensor([0.0, 0.8, 1.0, 0.5, 1.2, 0.9])
+    top_k = torch.tensor([0, 1, 0, 0, 1, 0])
+    top_p = torch.tensor([1.0, 1.0, 1e-7, 1.0, 0.3, 1e-6])
+    seeds = torch.arange(rows) * 17
+    counters = torch.zeros(rows, dtype=torch.long)
+    out = sample(*(x.to(device) for x in (logits, temp, top_k, top_p, seeds, counters))).cpu()
+    best = logits.float().argmax(-1)
+    for r in (0, 1, 2, 4, 5):  # greedy, top-k 1, tiny top-p all reduce to argmax
+        assert out[r] == best[r], r
+
+
+def test_sample_stays_in_kept_set_and_follows_softmax(device):
+    from oracle.sampling import kept_set
+    from tinyvllm.kernels.sampling import sample
+
+    g = torch.Generator().manual_seed(6)
+    vocab = 4096
+    row = (torch.randn(vocab, generator=g) * 3).to(torch.bfloat16)
+    cases = [(1.0, 0, 0.9), (0.7, 50, 1.0), (1.3, 200, 0.8), (1.0, 0, 1.0)]
+    n = 256
+    for temp, k, p in cases:
+        keep = kept_set(row.float(), temp, k, p)
+        logits = row[None].expand(n, vocab).contiguous()
+        out = sample(logits.to(device), torch.full((n,), temp).to(device),
+                     torch.full((n,), k).to(device), torch.full((n,), p).to(device),
+                     torch.full((n,), 1234).to(device), torch.arange(n).to(device)).cpu()
+        assert keep[out.numpy()].all(), (temp, k, p)
+    # Frequencies over a 3-token distribution (temperature 1, no filters).
+    probs = torch.tensor([0.5, 0.3, 0.2])
+    n = 8192
+    logits = torch.log(probs)[None].expand(n, 3).contiguous()
+    out = sample(logits.to(device), torch.ones(n, device=device),
+                 torch.zeros(n, dtype=torch.long, device=device),
+                 torch.ones(n, device=device), torch.full((n,), 99, device=device),
+                 torch.arange(n, device=device)).cpu()
+    freq = torch.bincount(out, minlength=3).float() / n
+    assert torch.allclose(freq, probs, atol=0.03), freq

@@ -1,0 +1,531 @@
+// Paged single-query (decode) attention for gfx950.
+//
+// Semantics follow the reference kernel tinyvllm/kernels/paged_decode.cu:92-466
+// (host contract :469-669): for decode row r and query head h,
+//   out[rows[r], h] = sum_t softmax_t(scale * q . k_t) v_t,  t < lengths[r],
+// token t lives at slot blocks[offsets[r] + t / bs] * bs + t % bs, KV head
+// h / (Hq / Hkv); zero-length rows produce zeros (reference :130-135).
+// Unlike the reference kernel, which rounds the PV weights to the storage
+// type (:332-333), the weights stay fp32 here: the PV product runs on the
+// VALU where that costs nothing, and the result then tracks the reference's
+// torch path (SDPAAttention, fp32 softmax) to well under one bf16 ulp.
+//
+// MI355X design (head_dim 128, the fast path):
+//  * one wave64 workgroup per (row, KV head, split): the G = Hq/Hkv query
+//    heads of a KV head share every K/V byte it loads, so the cache is read
+//    once per KV head instead of once per query head;
+//  * split-K: the row's pages are cut into `splits` equal page ranges so that
+//    rows x KV heads x splits fills the 256 CUs; a merge kernel combines the
+//    (max, sum, unnormalised output) partials with the usual LSE rescale;
+//  * Q.K^T on the matrix cores: per 16-token tile, 4 MFMA 16x16x32 steps with
+//    A = K rows (natural cache layout, 64 contiguous bytes per lane quad),
+//    B = the G query rows zero-padded to 16 columns;
+//  * P.V on the VALU: lane l holds 8 head dims of the token that the MFMA
+//    result row (l / 16) describes, so each lane's weights are a DPP
+//    row-broadcast of the score lane of its own 16-lane row - no LDS at all;
+//  * 64 tokens per iteration: 16 K and 16 V 16-byte loads per lane in flight
+//    (32 KiB per wave) before any arithmetic waits on them.
+#include "common.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace tvllm {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x32(const U16x8& a, const U16x8& b,
+                                              f32x4 c) {
+    if constexpr (std::is_same_v<T, __bf16>) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+            0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+            0, 0);
+    }
+}
+
+// Broadcast lane (row_base + G) of every 16-lane row to the whole row.
+template <int G>
+__device__ __forceinline__ float row_bcast(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                           0x150 + G, 0xf, 0xf, false));
+}
+
+template <int L>
+__device__ __forceinline__ float read_lane(float v) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), L));
+}
+
+__device__ __forceinline__ uint32_t shfl_u32(uint32_t v, int src) {
+    return static_cast<uint32_t>(__shfl(static_cast<int>(v), src, 64));
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <typename T>
+struct DecodeArgs {
+    const T* q;
+    int64_t qts, qhs;
+    const U16x8* k;  // cache rows in 16-byte units
+    const U16x8* v;
+    T* out;
+    int64_t ots, ohs;
+    const int64_t* rows;
+    const int64_t* blocks;
+    const int64_t* offsets;
+    const int64_t* lengths;
+    int heads, kv_heads, group, block_size, splits;
+    float scale_log2;  // softmax scale * log2(e): scores live in base 2
+    float* part_o;     // [rows, heads, splits, 128] unnormalised outputs
+    float* part_ml;    // [rows, heads, splits, 2] (running max, sum)
+};
+
+// GP: group size rounded up to a power of two (<= 16); SPLIT: write partials.
+template <typename T, int GP, bool SPLIT>
+__global__ void __launch_bounds__(64)
+paged_decode_d128(DecodeArgs<T> a) {
+    constexpr int D = 128;
+    constexpr int ROW16 = D / 8;  // 16-byte units per cache row of one head
+    const int lane = threadIdx.x;
+    const int quad = lane >> 4;   // 16-lane row of the wave
+    const int col = lane & 15;
+
+    const int id = blockIdx.x;
+    const int split = id % a.splits;
+    const int unit = id / a.splits;
+    const int kvh = unit % a.kv_heads;
+    const int r = unit / a.kv_heads;
+    const int h0 = kvh * a.group;
+
+    const int64_t row = a.rows[r];
+    const int64_t length = a.lengths[r];
+    const int bs = a.block_size;
+    const int64_t pages = (length + bs - 1) / bs;
+    const int64_t per_split = (pages + a.splits - 1) / a.splits;
+    const int64_t p_begin = int64_t(split) * per_split;
+    const int64_t p_end = min(pages, p_begin + per_split);
+    const int64_t t_begin = p_begin * bs;
+    const int64_t t_end = min(length, p_end * bs);
+
+    if (t_begin >= t_end) {
+        if constexpr (SPLIT) {
+            if (lane < a.group) {
+                float* ml = a.part_ml + ((int64_t(r) * a.heads + h0 + lane) * a.splits + split) * 2;
+                ml[0] = -INFINITY;
+                ml[1] = 0.f;
+            }
+        } else {
+            // Zero-length row: zeros, without touching Q, tables or KV.
+            for (int g = 0; g < a.group; ++g) {
+                T* o = a.out + row * a.ots + (h0 + g) * a.ohs;
+                for (int d = lane; d < D; d += 64) o[d] = static_cast<T>(0.f);
+            }
+        }
+        return;
+    }
+
+    const int64_t table = a.offsets[r];
+
+    // B operand: query head g = col (zero beyond the group), dims c*32 + quad*8.
+    U16x8 qb[4];
+    {
+        const bool has = col < a.group;
+        const T* qrow = a.q + row * a.qts + (h0 + (has ? col : 0)) * a.qhs + quad * 8;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if (has) {
+                qb[c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
+            } else {
+                qb[c].w[0] = qb[c].w[1] = qb[c].w[2] = qb[c].w[3] = 0u;
+            }
+        }
+    }
+
+    float acc[GP][8];
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    float m_run = -INFINITY;  // running max (base-2 units), per score lane
+    float l_run = 0.f;        // this lane's share of the denominator
+
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += 64) {
+        // Lane x resolves the cache row of chunk token t0 + x (clamped to the
+        // last valid token so that masked lanes still read mapped memory).
+        uint32_t my_row;
+        {
+            const int64_t t = min(t0 + lane, t_end - 1);
+            const int64_t page = t / bs;
+            const int64_t slot = a.blocks[table + page] * bs + (t - page * bs);
+            my_row = static_cast<uint32_t>((slot * a.kv_heads + kvh) * ROW16);
+        }
+
+        U16x8 kreg[4][4];  // [tile][k-slice]: token 16*tile + col
+        U16x8 vreg[4][4];  // [tile][i]:       token 16*tile + 4*quad + i
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t kr = shfl_u32(my_row, 16 * j + col);
+            const U16x8* kp = a.k + kr + quad;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kreg[j][c] = kp[c * 4];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t vr = shfl_u32(my_row, 16 * j + 4 * quad + i);
+                vreg[j][i] = a.v[vr + col];
+            }
+        }
+
+        // Scores: s[j][i] = token 16j + 4*quad + i, query head col.
+        float s[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(kreg[j][c], qb[c], d);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t t = t0 + 16 * j + 4 * quad + i;
+                s[j][i] = t < t_end ? d[i] * a.scale_log2 : -INFINITY;
+            }
+        }
+
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[j][i]);
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        const float m_new = fmaxf(m_run, cmax);
+        const float alpha = exp2f(m_run - m_new);
+        m_run = m_new;
+
+        float pw[4][4];
+        float psum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = exp2f(s[j][i] - m_new);
+                psum += p;
+                pw[j][i] = p;
+            }
+        l_run = l_run * alpha + psum;
+
+        static_for<0, GP>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            const float ag = read_lane<g>(alpha);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
+        });
+
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float vv[8];
+                unpack8<T>(vreg[j][i], vv);
+                static_for<0, GP>([&](auto gc) {
+                    constexpr int g = decltype(gc)::value;
+                    const float p = row_bcast<g>(pw[j][i]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vv[e], acc[g][e]);
+                });
+            }
+        }
+    }
+
+    // Combine the four 16-lane rows (disjoint token subsets).
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            acc[g][e] += __shfl_xor(acc[g][e], 16, 64);
+            acc[g][e] += __shfl_xor(acc[g][e], 32, 64);
+        }
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+
+    if constexpr (SPLIT) {
+        static_for<0, GP>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            if (g < a.group && quad == 0) {
+                float4* po = reinterpret_cast<float4*>(
+                    a.part_o + ((int64_t(r) * a.heads + h0 + g) * a.splits + split) * D +
+                    col * 8);
+                po[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+                po[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+            }
+        });
+        if (lane < a.group) {
+            float* ml = a.part_ml + ((int64_t(r) * a.heads + h0 + lane) * a.splits + split) * 2;
+            ml[0] = m_run;
+            ml[1] = l_run;
+        }
+    } else {
+        static_for<0, GP>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            const float denom = read_lane<g>(l_run);
+            if (g < a.group && quad == 0) {
+                U16x8 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    o.w[e] = pack2<T>(acc[g][2 * e] / denom, acc[g][2 * e + 1] / denom);
+                *reinterpret_cast<U16x8*>(a.out + row * a.ots + (h0 + g) * a.ohs + col * 8) = o;
+            }
+        });
+    }
+}
+
+// Merge split partials: out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
+template <typename T>
+__global__ void __launch_bounds__(64)
+paged_decode_merge(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                   T* __restrict__ out, const int64_t* __restrict__ rows,
+                   int64_t ots, int64_t ohs, int heads, int splits, int head_dim) {
+    const int id = blockIdx.x;
+    const int r = id / heads;
+    const int h = id - r * heads;
+    const int64_t base = (int64_t(r) * heads + h) * splits;
+    float mx = -INFINITY;
+    for (int s = 0; s < splits; ++s) mx = fmaxf(mx, part_ml[(base + s) * 2]);
+    T* o = out + rows[r] * ots + h * ohs;
+    if (mx == -INFINITY) {
+        for (int d = threadIdx.x; d < head_dim; d += 64) o[d] = static_cast<T>(0.f);
+        return;
+    }
+    float denom = 0.f;
+    for (int s = 0; s < splits; ++s) {
+        const float m = part_ml[(base + s) * 2];
+        if (m != -INFINITY) denom += exp2f(m - mx) * part_ml[(base + s) * 2 + 1];
+    }
+    for (int d = threadIdx.x; d < head_dim; d += 64) {
+        float num = 0.f;
+        for (int s = 0; s < splits; ++s) {
+            const float m = part_ml[(base + s) * 2];
+            if (m != -INFINITY) num += exp2f(m - mx) * part_o[(base + s) * head_dim + d];
+        }
+        o[d] = static_cast<T>(num / denom);
+    }
+}
+
+// Any head_dim <= 256 and any group: one wave per (row, query head), one
+// token at a time. Used for shapes the MFMA path does not cover.
+template <typename T>
+__global__ void __launch_bounds__(64)
+paged_decode_generic(const T* __restrict__ q, int64_t qts, int64_t qhs,
+                     const T* __restrict__ k, const T* __restrict__ v,
+                     T* __restrict__ out, int64_t ots, int64_t ohs,
+                     const int64_t* __restrict__ rows,
+                     const int64_t* __restrict__ blocks,
+                     const int64_t* __restrict__ offsets,
+                     const int64_t* __restrict__ lengths, int heads, int kv_heads,
+                     int head_dim, int block_size, float scale_log2) {
+    const int lane = threadIdx.x;
+    const int r = blockIdx.x / heads;
+    const int h = blockIdx.x - r * heads;
+    const int kvh = h / (heads / kv_heads);
+    const int64_t row = rows[r];
+    const int64_t length = lengths[r];
+    T* o = out + row * ots + h * ohs;
+    if (length == 0) {
+        for (int d = lane; d < head_dim; d += 64) o[d] = static_cast<T>(0.f);
+        return;
+    }
+    float qv[4], acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = lane + 64 * i;
+        qv[i] = d < head_dim ? to_f<T>(q[row * qts + h * qhs + d]) : 0.f;
+        acc[i] = 0.f;
+    }
+    const int64_t table = offsets[r];
+    float m = -INFINITY, l = 0.f;
+    for (int64_t t = 0; t < length; ++t) {
+        const int64_t page = t / block_size;
+        const int64_t slot = blocks[table + page] * block_size + (t - page * block_size);
+        const int64_t base = (slot * kv_heads + kvh) * head_dim;
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = lane + 64 * i;
+            if (d < head_dim) dot = fmaf(qv[i], to_f<T>(k[base + d]), dot);
+        }
+        const float sc = wave_sum(dot) * scale_log2;
+        const float mn = fmaxf(m, sc);
+        const float alpha = exp2f(m - mn);
+        const float p = exp2f(sc - mn);
+        l = l * alpha + p;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = lane + 64 * i;
+            if (d < head_dim) acc[i] = fmaf(p, to_f<T>(v[base + d]), acc[i] * alpha);
+        }
+        m = mn;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = lane + 64 * i;
+        if (d < head_dim) o[d] = static_cast<T>(acc[i] / l);
+    }
+}
+
+// Workgroups the split heuristic aims for: 8 per CU on 256 CUs keeps every
+// SIMD busy with two resident waves and leaves room for tail imbalance.
+constexpr int64_t kTargetGroups = 2048;
+constexpr int64_t kMaxSplits = 64;
+
+int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
+                      int64_t block_size) {
+    const int64_t units = rows * kv_heads;
+    if (units <= 0) return 1;
+    int64_t s = (kTargetGroups + units - 1) / units;
+    const int64_t max_pages = (max_context + block_size - 1) / block_size;
+    // Each split should own at least one full 64-token iteration.
+    const int64_t by_tokens = (max_context + 63) / 64;
+    s = std::min(s, std::min(max_pages, by_tokens));
+    s = std::min(s, kMaxSplits);
+    return std::max<int64_t>(s, 1);
+}
+
+bool fast_path(int64_t head_dim, int64_t group, const void* q, int64_t qts,
+               int64_t qhs, const void* out, int64_t ots, int64_t ohs,
+               const void* k, const void* v, int64_t num_slots, int64_t kv_heads) {
+    return head_dim == 128 && group <= 16 && aligned16(q) && qts % 8 == 0 &&
+           qhs % 8 == 0 && aligned16(out) && ots % 8 == 0 && ohs % 8 == 0 &&
+           aligned16(k) && aligned16(v) &&
+           num_slots * kv_heads * (head_dim / 8) <= int64_t(UINT32_MAX);
+}
+
+}  // namespace
+}  // namespace tvllm
+
+using namespace tvllm;
+
+extern "C" int64_t tvllm_paged_decode_workspace_size(int64_t num_rows,
+                                                     int64_t num_heads,
+                                                     int64_t num_kv_heads,
+                                                     int64_t head_dim,
+                                                     int64_t max_context_len,
+                                                     int64_t block_size) {
+    if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || head_dim != 128)
+        return 0;
+    const int64_t s = choose_splits(num_rows, num_kv_heads, max_context_len, block_size);
+    if (s <= 1) return 0;
+    return num_rows * num_heads * s * (head_dim + 2) * int64_t(sizeof(float));
+}
+
+extern "C" int tvllm_paged_decode(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride,
+    const void* k_cache, const void* v_cache, void* out, int64_t out_token_stride,
+    int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
+    const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
+    int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
+    int64_t block_size, int64_t max_context_len, float scale, void* workspace,
+    int64_t workspace_bytes, int dtype, tvllm_stream_t stream) {
+    TVLLM_CHECK(head_dim > 0 && head_dim <= 256 && num_heads > 0 && num_kv_heads > 0,
+                "paged_decode: invalid attention head geometry");
+    TVLLM_CHECK(num_heads % num_kv_heads == 0 && block_size > 0 &&
+                    block_size <= INT32_MAX && num_slots % block_size == 0,
+                "paged_decode: invalid GQA or block geometry");
+    TVLLM_CHECK(num_rows >= 0 && num_rows <= INT32_MAX / num_heads,
+                "paged_decode: decode grid is too large");
+    TVLLM_CHECK(max_context_len > 0, "paged_decode: max_context_len must be positive");
+    if (num_rows == 0) return TVLLM_OK;
+    TVLLM_CHECK(q && k_cache && v_cache && out && rows && blocks && offsets && lengths,
+                "paged_decode: null pointer");
+    const int64_t group = num_heads / num_kv_heads;
+    hipStream_t s = as_hip(stream);
+    const float scale_log2 = scale * kLog2e;
+
+    return dispatch_half(dtype, [&]<int DT>() {
+        using T = typename Elem<DT>::T;
+        if (!fast_path(head_dim, group, q, q_token_stride, q_head_stride, out,
+                       out_token_stride, out_head_stride, k_cache, v_cache,
+                       num_slots, num_kv_heads)) {
+            paged_decode_generic<T><<<int(num_rows * num_heads), 64, 0, s>>>(
+                static_cast<const T*>(q), q_token_stride, q_head_stride,
+                static_cast<const T*>(k_cache), static_cast<const T*>(v_cache),
+                static_cast<T*>(out), out_token_stride, out_head_stride, rows,
+                blocks, offsets, lengths, int(num_heads), int(num_kv_heads),
+                int(head_dim), int(block_size), scale_log2);
+            return launch_status("paged_decode");
+        }
+        const int64_t splits =
+            choose_splits(num_rows, num_kv_heads, max_context_len, block_size);
+        const int64_t need = splits > 1
+            ? num_rows * num_heads * splits * (head_dim + 2) * int64_t(sizeof(float))
+            : 0;
+        TVLLM_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                    "paged_decode: workspace of %lld bytes required, %lld given",
+                    (long long)need, (long long)workspace_bytes);
+        TVLLM_CHECK(need == 0 || aligned16(workspace),
+                    "paged_decode: workspace must be 16-byte aligned");
+        const int64_t grid = num_rows * num_kv_heads * splits;
+        TVLLM_CHECK(grid <= INT32_MAX, "paged_decode: decode grid is too large");
+
+        DecodeArgs<T> args;
+        args.q = static_cast<const T*>(q);
+        args.qts = q_token_stride;
+        args.qhs = q_head_stride;
+        args.k = static_cast<const U16x8*>(k_cache);
+        args.v = static_cast<const U16x8*>(v_cache);
+        args.out = static_cast<T*>(out);
+        args.ots = out_token_stride;
+        args.ohs = out_head_stride;
+        args.rows = rows;
+        args.blocks = blocks;
+        args.offsets = offsets;
+        args.lengths = lengths;
+        args.heads = int(num_heads);
+        args.kv_heads = int(num_kv_heads);
+        args.group = int(group);
+        args.block_size = int(block_size);
+        args.splits = int(splits);
+        args.scale_log2 = scale_log2;
+        args.part_o = static_cast<float*>(workspace);
+        args.part_ml = need ? args.part_o + num_rows * num_heads * splits * head_dim
+                            : nullptr;
+
+#define TVLLM_DEC(GP)                                                          \
+    do {                                                                       \
+        if (splits > 1)                                                        \
+            paged_decode_d128<T, GP, true><<<int(grid), 64, 0, s>>>(args);     \
+        else                                                                   \
+            paged_decode_d128<T, GP, false><<<int(grid), 64, 0, s>>>(args);    \
+    } while (0)
+        if (group <= 1) TVLLM_DEC(1);
+        else if (group <= 2) TVLLM_DEC(2);
+        else if (group <= 4) TVLLM_DEC(4);
+        else if (group <= 8) TVLLM_DEC(8);
+        else TVLLM_DEC(16);
+#undef TVLLM_DEC
+        int st = launch_status("paged_decode");
+        if (st != TVLLM_OK || splits <= 1) return st;
+        paged_decode_merge<T><<<int(num_rows * num_heads), 64, 0, s>>>(
+            args.part_o, args.part_ml, static_cast<T*>(out), rows,
+            out_token_stride, out_head_stride, int(num_heads), int(splits),
+            int(head_dim));
+        return launch_status("paged_decode merge");
+    });
+}

@@ -1,0 +1,411 @@
+// Row-wise pointwise kernels of the Qwen3 layer: RMSNorm (+ residual add),
+// SiLU(gate) * up, and per-head Q/K RMSNorm + half-split RoPE with an
+// optional fused slot-mapped KV-cache write.
+//
+// Rounding points follow the reference kernels, which restate the PyTorch
+// expressions (tinyvllm/kernels/pointwise.cu:95-116 rotate_pair, :128-214
+// rms_norm_kernel, :260-321 silu_and_mul, :325-450 qk_norm_rope_kernel):
+//   add:      x = round(x + residual)
+//   rmsnorm:  y = round(round(x * rsqrt(mean_fp32(x^2) + eps)) * w)
+//   silu:     o = round(round(g / (1 + exp(-g))) * u)
+//   rope:     o1 = round(round(n1*c) - round(n2*s)); o2 = round(round(n2*c) + round(n1*s))
+// All arithmetic is fp32 with contraction disabled at compile time, so each
+// product and sum is rounded exactly where the expression says.
+//
+// Mapping: every row is owned by one wave64 (narrow rows) or one 256-thread
+// workgroup (wide rows); a row is held in registers between the reduction
+// and the write, so the input is read once.
+#include "common.h"
+
+namespace tvllm {
+namespace {
+
+// ------------------------------------------------------------ RMSNorm ----
+
+// Loads 8 consecutive elements (16B vector when possible).
+template <typename T, bool VEC>
+__device__ __forceinline__ void load8(const T* p, int valid, float (&v)[8]) {
+    if constexpr (VEC && sizeof(T) == 2) {
+        if (valid >= 8) {
+            U16x8 raw = *reinterpret_cast<const U16x8*>(p);
+            unpack8<T>(raw, v);
+            return;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = i < valid ? to_f<T>(p[i]) : 0.f;
+}
+
+template <typename T, bool VEC>
+__device__ __forceinline__ void store8(T* p, int valid, const float (&v)[8]) {
+    if constexpr (VEC && sizeof(T) == 2) {
+        if (valid >= 8) {
+            U16x8 raw;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) raw.w[i] = pack2<T>(v[2 * i], v[2 * i + 1]);
+            *reinterpret_cast<U16x8*>(p) = raw;
+            return;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (i < valid) p[i] = static_cast<T>(v[i]);
+}
+
+// TPR threads per row (64 = one wave, or 256 = one workgroup); NV chunks of
+// 8 elements per thread are kept in registers (width <= TPR * 8 * NV).
+template <typename T, int TPR, int NV, bool RESIDUAL, bool VEC>
+__global__ void __launch_bounds__(256)
+rms_norm_kernel(const T* __restrict__ x, int64_t rows, int64_t heads, int width,
+                int64_t token_stride, int64_t head_stride,
+                const T* __restrict__ weight, const T* __restrict__ residual,
+                int64_t residual_stride, T* __restrict__ out,
+                T* __restrict__ residual_out, float eps) {
+    constexpr int RPB = 256 / TPR;  // rows per block
+    const int sub = threadIdx.x / TPR;
+    const int t = threadIdx.x % TPR;
+    const int64_t row = int64_t(blockIdx.x) * RPB + sub;
+    const bool active = row < rows;
+
+    const int64_t r = active ? row : 0;
+    const int64_t tok = r / heads;
+    const T* src = x + tok * token_stride + (r - tok * heads) * head_stride;
+    const T* res = RESIDUAL ? residual + tok * residual_stride : nullptr;
+
+    float v[NV][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int c = (n * TPR + t) * 8;
+        const int valid = active ? min(8, width - c) : 0;
+        load8<T, VEC>(src + c, valid, v[n]);
+        if constexpr (RESIDUAL) {
+            float rv[8];
+            load8<T, VEC>(res + c, valid, rv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[n][i] = rnd<T>(v[n][i] + rv[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += v[n][i] * v[n][i];
+    }
+    ss = wave_sum(ss);
+    if constexpr (TPR > 64) {
+        __shared__ float partial[4];
+        if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    }
+    if (!active) return;
+    const float inv = rsqrtf(ss * (1.0f / float(width)) + eps);
+
+    T* dst = out + row * int64_t(width);
+    T* rdst = RESIDUAL ? residual_out + row * int64_t(width) : nullptr;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int c = (n * TPR + t) * 8;
+        const int valid = min(8, width - c);
+        if (valid <= 0) continue;
+        float w[8], y[8];
+        load8<T, VEC>(weight + c, valid, w);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = rnd<T>(rnd<T>(v[n][i] * inv) * w[i]);
+        store8<T, VEC>(dst + c, valid, y);
+        if constexpr (RESIDUAL) store8<T, VEC>(rdst + c, valid, v[n]);
+    }
+}
+
+// Wide rows that do not fit in registers: two passes over the (cached) row.
+template <typename T, bool RESIDUAL>
+__global__ void __launch_bounds__(256)
+rms_norm_wide_kernel(const T* __restrict__ x, int64_t rows, int64_t heads,
+                     int width, int64_t token_stride, int64_t head_stride,
+                     const T* __restrict__ weight, const T* __restrict__ residual,
+                     int64_t residual_stride, T* __restrict__ out,
+                     T* __restrict__ residual_out, float eps) {
+    const int64_t row = blockIdx.x;
+    const int64_t tok = row / heads;
+    const T* src = x + tok * token_stride + (row - tok * heads) * head_stride;
+    const T* res = RESIDUAL ? residual + tok * residual_stride : nullptr;
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < width; c += 256) {
+        float a = to_f<T>(src[c]);
+        if constexpr (RESIDUAL) a = rnd<T>(a + to_f<T>(res[c]));
+        ss += a * a;
+    }
+    ss = wave_sum(ss);
+    __shared__ float partial[4];
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inv = rsqrtf(ss * (1.0f / float(width)) + eps);
+    for (int c = threadIdx.x; c < width; c += 256) {
+        float a = to_f<T>(src[c]);
+        if constexpr (RESIDUAL) {
+            a = rnd<T>(a + to_f<T>(res[c]));
+            residual_out[row * width + c] = static_cast<T>(a);
+        }
+        out[row * width + c] =
+            static_cast<T>(rnd<T>(a * inv) * to_f<T>(weight[c]));
+    }
+}
+
+template <typename T, bool RESIDUAL>
+int launch_rms(const void* x, int64_t rows, int64_t heads, int width,
+               int64_t ts, int64_t hs, const void* w, const void* res,
+               int64_t rs, void* out, void* rout, float eps, hipStream_t s) {
+    const T* xp = static_cast<const T*>(x);
+    const T* wp = static_cast<const T*>(w);
+    const T* rp = static_cast<const T*>(res);
+    T* op = static_cast<T*>(out);
+    T* rop = static_cast<T*>(rout);
+    const bool vec = sizeof(T) == 2 && width % 8 == 0 && ts % 8 == 0 &&
+                     hs % 8 == 0 && (!RESIDUAL || rs % 8 == 0) && aligned16(x) &&
+                     aligned16(w) && aligned16(out) &&
+                     (!RESIDUAL || (aligned16(res) && aligned16(rout)));
+    const int chunks = (width + 7) / 8;
+#define TVLLM_RMS(TPR, NV, V)                                                   \
+    rms_norm_kernel<T, TPR, NV, RESIDUAL, V>                                    \
+        <<<int((rows + 256 / TPR - 1) / (256 / TPR)), 256, 0, s>>>(              \
+            xp, rows, heads, width, ts, hs, wp, rp, rs, op, rop, eps)
+#define TVLLM_RMS_V(TPR, NV) \
+    do { if (vec) TVLLM_RMS(TPR, NV, true); else TVLLM_RMS(TPR, NV, false); } while (0)
+    if (chunks <= 64) TVLLM_RMS_V(64, 1);
+    else if (chunks <= 128) TVLLM_RMS_V(64, 2);
+    else if (chunks <= 256) TVLLM_RMS_V(256, 1);
+    else if (chunks <= 512) TVLLM_RMS_V(256, 2);
+    else if (chunks <= 1024) TVLLM_RMS_V(256, 4);
+    else
+        rms_norm_wide_kernel<T, RESIDUAL><<<int(rows), 256, 0, s>>>(
+            xp, rows, heads, width, ts, hs, wp, rp, rs, op, rop, eps);
+#undef TVLLM_RMS_V
+#undef TVLLM_RMS
+    return launch_status(RESIDUAL ? "add_rms_norm" : "rms_norm");
+}
+
+// --------------------------------------------------------- SiLU * up ----
+
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(256)
+silu_mul_kernel(const T* __restrict__ x, int64_t rows, int64_t heads, int half,
+                int64_t token_stride, int64_t head_stride, T* __restrict__ out,
+                int chunks_per_row) {
+    const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t row = idx / chunks_per_row;
+    if (row >= rows) return;
+    const int c = int(idx - row * chunks_per_row) * 8;
+    const int valid = min(8, half - c);
+    const int64_t tok = row / heads;
+    const T* src = x + tok * token_stride + (row - tok * heads) * head_stride;
+    float g[8], u[8], y[8];
+    load8<T, VEC>(src + c, valid, g);
+    load8<T, VEC>(src + half + c, valid, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float act = rnd<T>(g[i] / (1.0f + expf(-g[i])));
+        y[i] = act * u[i];
+    }
+    store8<T, VEC>(out + row * int64_t(half) + c, valid, y);
+}
+
+// ------------------------------------------------- QK norm + RoPE + KV ----
+
+// One wave per (token, head) row. Rows [0, T*Hq) are query heads, rows
+// [T*Hq, T*(Hq+Hkv)) key heads; a key-row wave also copies the matching V
+// row into the cache when the KV write is fused. Lane l owns the rotation
+// pairs (d, d + D/2) for d = l, l + 64, ...; NP pairs per lane.
+template <typename T, int NP>
+__global__ void __launch_bounds__(256)
+qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
+                    const T* __restrict__ k, int64_t kts, int64_t khs,
+                    const T* __restrict__ qw, const T* __restrict__ kw,
+                    const T* __restrict__ cos_t, const T* __restrict__ sin_t,
+                    int64_t tokens, int heads, int kv_heads, int head_dim,
+                    float q_eps, float k_eps, T* __restrict__ q_out,
+                    T* __restrict__ k_out, const T* __restrict__ v, int64_t vts,
+                    int64_t vhs, T* __restrict__ key_cache,
+                    T* __restrict__ value_cache,
+                    const int64_t* __restrict__ slots) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t q_rows = tokens * heads;
+    if (row >= q_rows + tokens * kv_heads) return;
+
+    const bool is_q = row < q_rows;
+    const int64_t r = is_q ? row : row - q_rows;
+    const int nh = is_q ? heads : kv_heads;
+    const int64_t tok = r / nh;
+    const int h = int(r - tok * nh);
+    const T* src = is_q ? q + tok * qts + h * qhs : k + tok * kts + h * khs;
+    const T* w = is_q ? qw : kw;
+    const float eps = is_q ? q_eps : k_eps;
+    const int half = head_dim / 2;
+
+    float x1[NP], x2[NP];
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int d = lane + 64 * p;
+        const bool ok = d < half;
+        x1[p] = ok ? to_f<T>(src[d]) : 0.f;
+        x2[p] = ok ? to_f<T>(src[d + half]) : 0.f;
+        ss += x1[p] * x1[p];
+        ss += x2[p] * x2[p];
+    }
+    ss = wave_sum(ss);
+    const float inv = rsqrtf(ss * (1.0f / float(head_dim)) + eps);
+
+    int64_t slot = -1;
+    T* dst;
+    if (is_q) {
+        dst = q_out + r * head_dim;
+    } else if (key_cache != nullptr) {
+        slot = slots[tok];
+        dst = slot >= 0 ? key_cache + (slot * kv_heads + h) * head_dim : nullptr;
+    } else {
+        dst = k_out + r * head_dim;
+    }
+    // With the fused write, a dense K copy is still produced if requested.
+    T* dense_k = (!is_q && key_cache != nullptr && k_out != nullptr)
+                     ? k_out + r * head_dim : nullptr;
+
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int d = lane + 64 * p;
+        if (d >= half) continue;
+        const float n1 = rnd<T>(rnd<T>(x1[p] * inv) * to_f<T>(w[d]));
+        const float n2 = rnd<T>(rnd<T>(x2[p] * inv) * to_f<T>(w[d + half]));
+        const float c = to_f<T>(cos_t[tok * half + d]);
+        const float s = to_f<T>(sin_t[tok * half + d]);
+        const float o1 = rnd<T>(n1 * c) - rnd<T>(n2 * s);
+        const float o2 = rnd<T>(n2 * c) + rnd<T>(n1 * s);
+        if (dst != nullptr) {
+            dst[d] = static_cast<T>(o1);
+            dst[d + half] = static_cast<T>(o2);
+        }
+        if (dense_k != nullptr) {
+            dense_k[d] = static_cast<T>(o1);
+            dense_k[d + half] = static_cast<T>(o2);
+        }
+    }
+
+    if (!is_q && key_cache != nullptr && slot >= 0) {
+        const T* vsrc = v + tok * vts + h * vhs;
+        T* vdst = value_cache + (slot * kv_heads + h) * head_dim;
+        for (int d = lane; d < head_dim; d += 64) vdst[d] = vsrc[d];
+    }
+}
+
+}  // namespace
+}  // namespace tvllm
+
+using namespace tvllm;
+
+extern "C" int tvllm_rms_norm(const void* input, int64_t tokens, int64_t heads,
+                              int64_t width, int64_t token_stride,
+                              int64_t head_stride, const void* weight,
+                              const void* residual, int64_t residual_stride,
+                              void* out, void* residual_out, float eps, int dtype,
+                              tvllm_stream_t stream) {
+    TVLLM_CHECK(tokens >= 0 && heads > 0 && width > 0,
+                "rms_norm: rows must have positive width");
+    TVLLM_CHECK(width <= INT32_MAX - 127 && tokens * heads <= INT32_MAX,
+                "rms_norm: RMSNorm dimensions exceed index range");
+    TVLLM_CHECK(residual == nullptr || heads == 1,
+                "add_rms_norm: residual requires a 2D input");
+    TVLLM_CHECK(residual == nullptr || residual_out != nullptr,
+                "add_rms_norm: residual_out is required");
+    const int64_t rows = tokens * heads;
+    if (rows == 0) return TVLLM_OK;
+    TVLLM_CHECK(input && weight && out, "rms_norm: null pointer");
+    hipStream_t s = as_hip(stream);
+    return dispatch_float(dtype, [&]<int DT>() {
+        using T = typename Elem<DT>::T;
+        if (residual)
+            return launch_rms<T, true>(input, rows, heads, int(width), token_stride,
+                                       head_stride, weight, residual,
+                                       residual_stride, out, residual_out, eps, s);
+        return launch_rms<T, false>(input, rows, heads, int(width), token_stride,
+                                    head_stride, weight, nullptr, 0, out, nullptr,
+                                    eps, s);
+    });
+}
+
+extern "C" int tvllm_silu_and_mul(const void* input, int64_t tokens,
+                                  int64_t heads, int64_t width,
+                                  int64_t token_stride, int64_t head_stride,
+                                  void* out, int dtype, tvllm_stream_t stream) {
+    TVLLM_CHECK(tokens >= 0 && heads > 0 && width > 0,
+                "silu_and_mul: rows must have positive width");
+    TVLLM_CHECK(width % 2 == 0, "silu_and_mul: SiLU input width must be even");
+    TVLLM_CHECK(width <= INT32_MAX - 16, "silu_and_mul: width too large");
+    const int64_t rows = tokens * heads;
+    if (rows == 0) return TVLLM_OK;
+    TVLLM_CHECK(input && out, "silu_and_mul: null pointer");
+    const int half = int(width / 2);
+    const int chunks = (half + 7) / 8;
+    const int64_t total = rows * chunks;
+    TVLLM_CHECK((total + 255) / 256 <= INT32_MAX, "silu_and_mul: too many rows");
+    hipStream_t s = as_hip(stream);
+    return dispatch_float(dtype, [&]<int DT>() {
+        using T = typename Elem<DT>::T;
+        const bool vec = sizeof(T) == 2 && half % 8 == 0 && token_stride % 8 == 0 &&
+                         head_stride % 8 == 0 && aligned16(input) && aligned16(out);
+        const int blocks = int((total + 255) / 256);
+        if (vec)
+            silu_mul_kernel<T, true><<<blocks, 256, 0, s>>>(
+                static_cast<const T*>(input), rows, heads, half, token_stride,
+                head_stride, static_cast<T*>(out), chunks);
+        else
+            silu_mul_kernel<T, false><<<blocks, 256, 0, s>>>(
+                static_cast<const T*>(input), rows, heads, half, token_stride,
+                head_stride, static_cast<T*>(out), chunks);
+        return launch_status("silu_and_mul");
+    });
+}
+
+extern "C" int tvllm_qk_norm_rope(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k,
+    int64_t k_token_stride, int64_t k_head_stride, const void* q_weight,
+    const void* k_weight, const void* cos, const void* sin, int64_t tokens,
+    int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, float q_eps,
+    float k_eps, void* q_out, void* k_out, const void* v, int64_t v_token_stride,
+    int64_t v_head_stride, void* key_cache, void* value_cache,
+    const int64_t* slots, int64_t num_slots, int dtype, tvllm_stream_t stream) {
+    TVLLM_CHECK(tokens >= 0 && num_heads > 0 && num_kv_heads > 0,
+                "qk_norm_rope: Q/K must have positive head counts");
+    TVLLM_CHECK(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 1024,
+                "qk_norm_rope: RoPE input must have an even head_dim <= 1024");
+    TVLLM_CHECK(tokens * (num_heads + num_kv_heads) <= INT32_MAX * int64_t(4),
+                "qk_norm_rope: Q/K RMSNorm dimensions exceed index range");
+    const bool fused = key_cache != nullptr;
+    TVLLM_CHECK(!fused || (value_cache && v && slots && key_cache != value_cache),
+                "qk_norm_rope: fused KV write needs v, value_cache and slots");
+    TVLLM_CHECK(fused || k_out != nullptr, "qk_norm_rope: k_out is required");
+    TVLLM_CHECK(!fused || tokens <= num_slots, "qk_norm_rope: too many KV rows");
+    const int64_t rows = tokens * (num_heads + num_kv_heads);
+    if (rows == 0) return TVLLM_OK;
+    TVLLM_CHECK(q && k && q_weight && k_weight && cos && sin && q_out,
+                "qk_norm_rope: null pointer");
+    hipStream_t s = as_hip(stream);
+    return dispatch_half(dtype, [&]<int DT>() {
+        using T = typename Elem<DT>::T;
+        const int blocks = int((rows + 3) / 4);
+        const int half = int(head_dim / 2);
+#define TVLLM_QKR(NP)                                                            \
+    qk_norm_rope_kernel<T, NP><<<blocks, 256, 0, s>>>(                           \
+        static_cast<const T*>(q), q_token_stride, q_head_stride,                 \
+        static_cast<const T*>(k), k_token_stride, k_head_stride,                 \
+        static_cast<const T*>(q_weight), static_cast<const T*>(k_weight),        \
+        static_cast<const T*>(cos), static_cast<const T*>(sin), tokens,          \
+        int(num_heads), int(num_kv_heads), int(head_dim), q_eps, k_eps,          \
+        static_cast<T*>(q_out), static_cast<T*>(k_out),                          \
+        static_cast<const T*>(v), v_token_stride, v_head_stride,                 \
+        static_cast<T*>(key_cache), static_cast<T*>(value_cache), slots)
+        if (half <= 64) TVLLM_QKR(1);
+        else if (half <= 128) TVLLM_QKR(2);
+        else if (half <= 256) TVLLM_QKR(4);
+        else TVLLM_QKR(8);
+#undef TVLLM_QKR
+        return launch_status("qk_norm_rope");
+    });
+}

@@ -1,0 +1,381 @@
+// Token sampling over [rows, vocab] logits: greedy argmax, and temperature /
+// top-k / top-p sampling by the exponential race.
+//
+// Reference behaviour: tinyvllm/sampling.py:21-72 (TorchSampler.sample:
+// greedy rows use logits.argmax) and :75-164 (_sample_batch):
+//   s = (logit.float() - rowmax) / T; optional top-k; stable descending sort;
+//   softmax; drop every token whose preceding cumulative probability exceeds
+//   top_p (the first token crossing top_p is kept); choice = argmax p / E,
+//   E ~ Exp(1).
+//
+// MI355X design: one 1024-thread workgroup per row, no sort. The kept set is
+// found by radix selection over an order-preserving 32-bit key of s (four
+// 8-bit digit passes, histograms in LDS), weighting each token by its
+// probability mass in 2^-40 fixed point so the sums are exact and
+// deterministic; ties on s are resolved by token index (three more passes),
+// which is exactly the stable sort's order. The noise is a counter-based
+// Philox4x32-10 stream (Salmon et al., SC'11) keyed by the request seed and
+// its sample counter, so a step is reproducible and graph-capturable.
+#include "common.h"
+
+namespace tvllm {
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+
+template <typename T>
+__device__ __forceinline__ float load_logit(const T* row, int64_t i) {
+    return to_f<T>(row[i]);
+}
+
+// Better = larger value; NaN beats numbers; ties go to the lower index.
+__device__ __forceinline__ bool better(float a, int64_t ia, float b, int64_t ib) {
+    const bool na = a != a, nb = b != b;
+    if (na || nb) return na && (!nb || ia < ib);
+    return a > b || (a == b && ia < ib);
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, int64_t& idx) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int64_t oi = __shfl_xor(idx, off, 64);
+        if (better(ov, oi, v, idx)) { v = ov; idx = oi; }
+    }
+}
+
+// Block-wide argmax; every thread gets the result.
+__device__ void block_argmax(float& v, int64_t& idx) {
+    __shared__ float sv[kWaves];
+    __shared__ int64_t si[kWaves];
+    wave_argmax(v, idx);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[w] = v; si[w] = idx; }
+    __syncthreads();
+    v = sv[0];
+    idx = si[0];
+    for (int i = 1; i < kWaves; ++i)
+        if (better(sv[i], si[i], v, idx)) { v = sv[i]; idx = si[i]; }
+    __syncthreads();
+}
+
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+argmax_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride,
+              int64_t* __restrict__ out) {
+    const T* row = logits + int64_t(blockIdx.x) * stride;
+    float best = -INFINITY;
+    int64_t bi = INT64_MAX;
+    if constexpr (VEC) {
+        const int64_t nvec = vocab / 8;
+        const U16x8* rv = reinterpret_cast<const U16x8*>(row);
+        for (int64_t c = threadIdx.x; c < nvec; c += kThreads) {
+            float x[8];
+            unpack8<T>(rv[c], x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (better(x[e], c * 8 + e, best, bi)) { best = x[e]; bi = c * 8 + e; }
+        }
+        for (int64_t i = nvec * 8 + threadIdx.x; i < vocab; i += kThreads) {
+            const float x = load_logit(row, i);
+            if (better(x, i, best, bi)) { best = x; bi = i; }
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
+            const float x = load_logit(row, i);
+            if (better(x, i, best, bi)) { best = x; bi = i; }
+        }
+    }
+    block_argmax(best, bi);
+    if (threadIdx.x == 0) out[blockIdx.x] = bi;
+}
+
+// ------------------------------------------------------------ sampling ----
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as
+// easy as 1, 2, 3", SC'11): 10 rounds of the 4x32 multiply-xor bijection.
+__device__ __forceinline__ uint4 philox4x32_10(uint4 ctr, uint2 key) {
+    constexpr uint32_t kM0 = 0xD2511F53u, kM1 = 0xCD9E8D57u;
+    constexpr uint32_t kW0 = 0x9E3779B9u, kW1 = 0xBB67AE85u;
+#pragma unroll
+    for (int round = 0; round < 10; ++round) {
+        const uint32_t hi0 = __umulhi(kM0, ctr.x), lo0 = kM0 * ctr.x;
+        const uint32_t hi1 = __umulhi(kM1, ctr.z), lo1 = kM1 * ctr.z;
+        ctr = make_uint4(hi1 ^ ctr.y ^ key.x, lo1, hi0 ^ ctr.w ^ key.y, lo0);
+        key.x += kW0;
+        key.y += kW1;
+    }
+    return ctr;
+}
+
+// Order-preserving map float -> uint32 (larger float, larger key).
+__device__ __forceinline__ uint32_t fkey(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+constexpr double kMassScale = 1099511627776.0;  // 2^40 fixed point
+
+struct RowCtx {
+    float mx;     // row max of the logits
+    float temp;   // temperature
+};
+
+template <typename T>
+__device__ __forceinline__ float score_of(const T* row, int64_t i, const RowCtx& c) {
+    return (load_logit(row, i) - c.mx) / c.temp;
+}
+
+__device__ __forceinline__ uint64_t mass_of(float s) {
+    return static_cast<uint64_t>(static_cast<double>(expf(s)) * kMassScale);
+}
+
+// Selection result: kept = key > k or (key == k and index <= idx).
+struct Cut {
+    uint32_t key;
+    int64_t idx;
+    bool all;  // total weight never exceeds the target: keep everything
+};
+
+__device__ __forceinline__ bool kept(const Cut& c, uint32_t key, int64_t i) {
+    return c.all || key > c.key || (key == c.key && i <= c.idx);
+}
+
+// Finds the first element, in (key descending, index ascending) order among
+// elements with in(i), whose inclusive cumulative weight exceeds `target`.
+// weight(i) is 1 (MASS = false) or the fixed-point probability mass.
+template <typename T, bool MASS, typename In>
+__device__ Cut radix_cut(const T* row, int64_t vocab, const RowCtx& ctx,
+                         uint64_t target, In&& in) {
+    __shared__ uint64_t hist[256];
+    __shared__ uint32_t s_prefix;
+    __shared__ uint64_t s_above;
+    __shared__ int s_found;
+    uint32_t prefix = 0;
+    uint64_t above = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = threadIdx.x; b < 256; b += kThreads) hist[b] = 0;
+        __syncthreads();
+        for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
+            if (!in(i)) continue;
+            const float s = score_of(row, i, ctx);
+            const uint32_t k = fkey(s);
+            if (shift < 24 && ((k ^ prefix) >> (shift + 8)) != 0) continue;
+            atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(k >> shift) & 255]),
+                      static_cast<unsigned long long>(MASS ? mass_of(s) : 1));
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t cum = above;
+            int found = -1;
+            for (int b = 255; b >= 0; --b) {
+                if (cum + hist[b] > target) { found = b; break; }
+                cum += hist[b];
+            }
+            s_found = found;
+            s_prefix = found >= 0 ? prefix | (uint32_t(found) << shift) : prefix;
+            s_above = cum;
+        }
+        __syncthreads();
+        if (s_found < 0) {
+            Cut c{0u, 0, true};
+            __syncthreads();
+            return c;
+        }
+        prefix = s_prefix;
+        above = s_above;
+        __syncthreads();
+    }
+    // prefix is the boundary key; every tie there has the same weight w.
+    // The boundary is the j-th tie in index order, j = (target - above) / w.
+    uint64_t w = 1;
+    if constexpr (MASS) {
+        w = 0;
+        // All ties share s, hence the same mass; recompute from any of them.
+        __shared__ uint64_t s_w;
+        if (threadIdx.x == 0) s_w = 0;
+        __syncthreads();
+        for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
+            if (!in(i)) continue;
+            const float s = score_of(row, i, ctx);
+            if (fkey(s) == prefix) { s_w = mass_of(s); break; }
+        }
+        __syncthreads();
+        w = s_w;
+        __syncthreads();
+    }
+    const uint64_t j = w ? (target - above) / w : 0;
+    // Ascending radix select of the j-th tie index (indices < 2^24).
+    __shared__ uint32_t ihist[256];
+    __shared__ uint32_t s_iprefix;
+    __shared__ uint64_t s_ibelow;
+    uint32_t iprefix = 0;
+    uint64_t below = 0;
+    for (int shift = 16; shift >= 0; shift -= 8) {
+        for (int b = threadIdx.x; b < 256; b += kThreads) ihist[b] = 0;
+        __syncthreads();
+        for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
+            if (!in(i)) continue;
+            const uint32_t ui = static_cast<uint32_t>(i);
+            if (shift < 16 && ((ui ^ iprefix) >> (shift + 8)) != 0) continue;
+            if (fkey(score_of(row, i, ctx)) != prefix) continue;
+            atomicAdd(&ihist[(ui >> shift) & 255], 1u);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t cum = below;
+            int found = 255;
+            for (int b = 0; b < 256; ++b) {
+                if (cum + ihist[b] > j) { found = b; break; }
+                cum += ihist[b];
+            }
+            s_iprefix = iprefix | (uint32_t(found) << shift);
+            s_ibelow = cum;
+        }
+        __syncthreads();
+        iprefix = s_iprefix;
+        below = s_ibelow;
+        __syncthreads();
+    }
+    return Cut{prefix, static_cast<int64_t>(iprefix), false};
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+sample_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride,
+              const float* __restrict__ temperature, const int64_t* __restrict__ top_k,
+              const float* __restrict__ top_p, const int64_t* __restrict__ seeds,
+              const int64_t* __restrict__ counters, int64_t* __restrict__ out) {
+    const int r = blockIdx.x;
+    const T* row = logits + int64_t(r) * stride;
+
+    // Row max (also the greedy answer).
+    float best = -INFINITY;
+    int64_t bi = INT64_MAX;
+    for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
+        const float x = load_logit(row, i);
+        if (better(x, i, best, bi)) { best = x; bi = i; }
+    }
+    block_argmax(best, bi);
+    const float temp = temperature[r];
+    if (!(temp > 0.f)) {
+        if (threadIdx.x == 0) out[r] = bi;
+        return;
+    }
+    const RowCtx ctx{best, temp};
+    const int64_t k = top_k[r];
+    const float p = top_p[r];
+
+    Cut kcut{0u, 0, true};
+    if (k > 0 && k < vocab) {
+        kcut = radix_cut<T, false>(row, vocab, ctx, uint64_t(k - 1),
+                                   [](int64_t) { return true; });
+    }
+    auto in_k = [&](int64_t i) {
+        return kcut.all || kept(kcut, fkey(score_of(row, i, ctx)), i);
+    };
+
+    Cut pcut{0u, 0, true};
+    if (p < 1.f) {
+        // Z = total mass of the top-k candidates (the softmax denominator).
+        __shared__ unsigned long long s_z;
+        if (threadIdx.x == 0) s_z = 0;
+        __syncthreads();
+        unsigned long long z = 0;
+        for (int64_t i = threadIdx.x; i < vocab; i += kThreads)
+            if (in_k(i)) z += mass_of(score_of(row, i, ctx));
+        atomicAdd(&s_z, z);
+        __syncthreads();
+        const uint64_t target = static_cast<uint64_t>(static_cast<double>(p) *
+                                                      static_cast<double>(s_z));
+        pcut = radix_cut<T, true>(row, vocab, ctx, target, in_k);
+    }
+
+    // Exponential race over the kept set: argmax s_i - log(E_i).
+    const uint2 key = make_uint2(static_cast<uint32_t>(seeds[r]),
+                                 static_cast<uint32_t>(uint64_t(seeds[r]) >> 32));
+    const uint64_t step = static_cast<uint64_t>(counters[r]);
+    float bv = -INFINITY;
+    int64_t bidx = INT64_MAX;
+    for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
+        const float s = score_of(row, i, ctx);
+        const uint32_t kk = fkey(s);
+        if (!kcut.all && !kept(kcut, kk, i)) continue;
+        if (!pcut.all && !kept(pcut, kk, i)) continue;
+        const uint4 rnd4 = philox4x32_10(
+            make_uint4(static_cast<uint32_t>(i >> 2), static_cast<uint32_t>(i >> 34),
+                       static_cast<uint32_t>(step), static_cast<uint32_t>(step >> 32)),
+            key);
+        const int lane4 = int(i & 3);
+        const uint32_t bits = lane4 == 0 ? rnd4.x : lane4 == 1 ? rnd4.y
+                            : lane4 == 2 ? rnd4.z : rnd4.w;
+        const float u = (float(bits >> 8) + 0.5f) * (1.0f / 16777216.0f);
+        const float e = -logf(u);
+        const float g = s - logf(e);
+        if (better(g, i, bv, bidx)) { bv = g; bidx = i; }
+    }
+    block_argmax(bv, bidx);
+    if (threadIdx.x == 0) out[r] = bidx;
+}
+
+}  // namespace
+}  // namespace tvllm
+
+using namespace tvllm;
+
+extern "C" int tvllm_argmax(const void* logits, int64_t rows, int64_t vocab,
+                            int64_t row_stride, int64_t* out, int dtype,
+                            tvllm_stream_t stream) {
+    TVLLM_CHECK(rows >= 0 && vocab > 0 && row_stride >= vocab,
+                "argmax: invalid logits geometry");
+    TVLLM_CHECK(rows <= INT32_MAX, "argmax: too many rows");
+    if (rows == 0) return TVLLM_OK;
+    TVLLM_CHECK(logits && out, "argmax: null pointer");
+    hipStream_t s = as_hip(stream);
+    return dispatch_float(dtype, [&]<int DT>() {
+        using T = typename Elem<DT>::T;
+        const bool vec = row_stride % 8 == 0 && aligned16(logits);
+        if constexpr (sizeof(T) == 2) {
+            if (vec) {
+                argmax_kernel<T, true><<<int(rows), kThreads, 0, s>>>(
+                    static_cast<const T*>(logits), vocab, row_stride, out);
+                return launch_status("argmax");
+            }
+        }
+            argmax_kernel<T, false><<<int(rows), kThreads, 0, s>>>(
+                static_cast<const T*>(logits), vocab, row_stride, out);
+        return launch_status("argmax");
+    });
+}
+
+extern "C" int64_t tvllm_sample_workspace_size(int64_t rows, int64_t vocab) {
+    (void)rows;
+    (void)vocab;
+    return 0;  // single-pass-per-row design: no cross-workgroup partials
+}
+
+extern "C" int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
+                            int64_t row_stride, const float* temperature,
+                            const int64_t* top_k, const float* top_p,
+                            const int64_t* seeds, const int64_t* counters,
+                            int64_t* out, void* workspace, int64_t workspace_bytes,
+                            int dtype, tvllm_stream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    TVLLM_CHECK(rows >= 0 && vocab > 0 && row_stride >= vocab,
+                "sample: invalid logits geometry");
+    TVLLM_CHECK(vocab < (int64_t(1) << 24), "sample: vocab must be < 2^24");
+    TVLLM_CHECK(rows <= INT32_MAX, "sample: too many rows");
+    if (rows == 0) return TVLLM_OK;
+    TVLLM_CHECK(logits && temperature && top_k && top_p && seeds && counters && out,
+                "sample: null pointer");
+    hipStream_t s = as_hip(stream);
+    return dispatch_float(dtype, [&]<int DT>() {
+        using T = typename Elem<DT>::T;
+        sample_kernel<T><<<int(rows), kThreads, 0, s>>>(
+            static_cast<const T*>(logits), vocab, row_stride, temperature, top_k,
+            top_p, seeds, counters, out);
+        return launch_status("sample");
+    });
+}

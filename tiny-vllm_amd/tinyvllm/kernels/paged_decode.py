@@ -1,0 +1,81 @@
+"""Paged decode attention (reference wrapper: tinyvllm/kernels/paged_decode.py:10-32;
+host contract tinyvllm/kernels/paged_decode.cu:469-669)."""
+from __future__ import annotations
+
+import torch
+
+from tinyvllm.kernels._extension import (
+    check, dtype_code, load_kernels, require_gpu, stream_of,
+)
+from tinyvllm.paged_kv import PagedKVCache
+from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+
+def decode_workspace_bytes(
+    num_rows: int, num_heads: int, num_kv_heads: int, head_dim: int,
+    max_context_len: int, block_size: int,
+) -> int:
+    """Split-K scratch the decode kernel needs for this geometry."""
+    return int(load_kernels().tvllm_paged_decode_workspace_size(
+        num_rows, num_heads, num_kv_heads, head_dim, max_context_len, block_size,
+    ))
+
+
+def paged_decode_attention(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    layer_idx: int,
+    metadata: SingleQueryMetadata,
+    output: torch.Tensor,
+    *,
+    scale: float,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """Fill selected rows on the current stream; zero-length padding yields zeros.
+
+    ``workspace`` (optional, uint8, >= decode_workspace_bytes) holds split-K
+    partials; when omitted it is allocated from torch's caching allocator
+    (inside graph capture that is the graph's private pool).
+    """
+    lib = load_kernels()
+    k, v = cache.key[layer_idx], cache.value[layer_idx]
+    rows = metadata.query_rows
+    blocks = metadata.block_table_ids
+    offsets = metadata.block_table_offsets
+    lengths = metadata.context_lens
+    device = require_gpu(q, k, v, output, rows, blocks, offsets, lengths)
+    if q.dim() != 3:
+        raise RuntimeError("Q must be a GPU [tokens, heads, dim] tensor")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("Q must use float16 or bfloat16")
+    if k.dtype != q.dtype or output.dtype != q.dtype:
+        raise RuntimeError("Q/K/V/output must share device and dtype")
+    if output.shape != q.shape or q.stride(2) != 1 or output.stride(2) != 1:
+        raise RuntimeError("output must match Q shape with unit last stride")
+    for tensor in (rows, blocks, offsets, lengths):
+        if tensor.dtype != torch.long or tensor.dim() != 1 or not tensor.is_contiguous():
+            raise RuntimeError(
+                "metadata must be contiguous GPU int64 vectors on Q's device"
+            )
+    if rows.numel() != lengths.numel() or offsets.numel() != rows.numel() + 1:
+        raise RuntimeError("metadata lengths must align")
+    num_rows = rows.numel()
+    if num_rows == 0:
+        return
+    heads, dim = q.shape[1], q.shape[2]
+    max_len = metadata.max_context_len or cache.num_slots
+    need = int(lib.tvllm_paged_decode_workspace_size(
+        num_rows, heads, cache.num_kv_heads, dim, max_len, cache.block_size,
+    ))
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    check(lib.tvllm_paged_decode(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k.data_ptr(), v.data_ptr(),
+        output.data_ptr(), output.stride(0), output.stride(1),
+        rows.data_ptr(), blocks.data_ptr(), offsets.data_ptr(), lengths.data_ptr(),
+        num_rows, heads, cache.num_kv_heads, dim, cache.num_slots,
+        cache.block_size, max_len, float(scale),
+        workspace.data_ptr() if need else None, need,
+        dtype_code(q.dtype), stream_of(device),
+    ))

@@ -1,0 +1,58 @@
+"""Chunked-prefill paged attention on MFMA tiles.
+
+Replaces the reference's per-row gather + SDPA for query chunks with history
+(tinyvllm/runtime/attention.py:102-151, 235-285) and its optional FlashInfer
+wrapper (runtime/prefill.py:15-225).
+"""
+from __future__ import annotations
+
+import torch
+
+from tinyvllm.kernels._extension import (
+    check, dtype_code, load_kernels, require_gpu, stream_of,
+)
+from tinyvllm.paged_kv import PagedKVCache
+from tinyvllm.runtime.contracts import MultiQueryMetadata
+
+
+def paged_prefill_attention(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    layer_idx: int,
+    metadata: MultiQueryMetadata,
+    output: torch.Tensor,
+    *,
+    scale: float,
+) -> None:
+    """Causal (lower-right) attention of each item's query chunk over its
+    paged context; writes the items' rows of ``output`` in place."""
+    lib = load_kernels()
+    k, v = cache.key[layer_idx], cache.value[layer_idx]
+    m = metadata
+    device = require_gpu(q, k, v, output, m.query_offsets, m.block_table_ids,
+                         m.block_table_offsets, m.context_lens)
+    if q.dim() != 3 or output.shape != q.shape:
+        raise RuntimeError("Q/output must be [tokens, heads, dim] tensors")
+    if q.dtype not in (torch.float16, torch.bfloat16) or output.dtype != q.dtype \
+            or k.dtype != q.dtype:
+        raise RuntimeError("Q/K/V/output must share a float16 or bfloat16 dtype")
+    if q.stride(2) != 1 or output.stride(2) != 1:
+        raise RuntimeError("Q/output rows must have unit last stride")
+    for tensor in (m.query_offsets, m.block_table_ids, m.block_table_offsets,
+                   m.context_lens):
+        if tensor.dtype != torch.long or tensor.dim() != 1 or not tensor.is_contiguous():
+            raise RuntimeError("metadata must be contiguous GPU int64 vectors")
+    items = m.context_lens.numel()
+    if m.query_offsets.numel() != items + 1 or m.block_table_offsets.numel() != items + 1:
+        raise RuntimeError("metadata lengths must align")
+    if items == 0 or m.max_query_len == 0:
+        return
+    check(lib.tvllm_paged_prefill(
+        q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
+        output.data_ptr(), output.stride(0), output.stride(1),
+        m.query_offsets.data_ptr(), m.block_table_ids.data_ptr(),
+        m.block_table_offsets.data_ptr(), m.context_lens.data_ptr(),
+        items, m.max_query_len, q.shape[1], cache.num_kv_heads, q.shape[2],
+        cache.num_slots, cache.block_size, float(scale),
+        dtype_code(q.dtype), stream_of(device),
+    ))

@@ -1,0 +1,169 @@
+"""Qwen3 building blocks (reference: tinyvllm/layers.py:19-251).
+
+Dense projections stay on PyTorch-ROCm GEMMs (hipBLASLt); normalisation and
+activation run on the HIP kernels of ``tinyvllm.kernels.pointwise``.
+"""
+from __future__ import annotations
+
+import math
+from collections.abc import Sequence
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from tinyvllm._validation import _check_positive_int
+from tinyvllm.kernels.pointwise import add_rms_norm, rms_norm, silu_and_mul
+
+
+class PackedLinear(nn.Module):
+    """Bias-free linear layer whose output rows pack several named shards
+    (q|k|v, gate|up), so one GEMM serves them all (reference layers.py:19-125)."""
+
+    def __init__(
+        self,
+        input_size: int,
+        output_sizes: Sequence[int],
+        *,
+        shard_names: Sequence[str] | None = None,
+        device: torch.device | str | None = None,
+        dtype: torch.dtype | None = None,
+    ) -> None:
+        super().__init__()
+        _check_positive_int("input_size", input_size)
+        self.input_size = input_size
+        self.output_sizes = tuple(output_sizes)
+        if not self.output_sizes:
+            raise ValueError("output_sizes must be non-empty")
+        for size in self.output_sizes:
+            _check_positive_int("output_size", size)
+        names = (tuple(str(i) for i in range(len(self.output_sizes)))
+                 if shard_names is None else tuple(shard_names))
+        if len(names) != len(self.output_sizes):
+            raise ValueError("shard_names must match output_sizes")
+        if len(set(names)) != len(names):
+            raise ValueError("shard_names must be unique")
+        self.shard_names = names
+        self._index = {name: i for i, name in enumerate(names)}
+        starts = [0]
+        for size in self.output_sizes:
+            starts.append(starts[-1] + size)
+        self._starts = tuple(starts)
+        self.weight = nn.Parameter(
+            torch.empty(starts[-1], input_size, device=device, dtype=dtype)
+        )
+        self.reset_parameters()
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.linear(x, self.weight)
+
+    def reset_parameters(self) -> None:
+        if self.weight.device.type == "meta":
+            return
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+
+    def load_shard(self, shard: str | int, loaded_weight: torch.Tensor) -> None:
+        """Copy one logical shard (by name or index) into its packed rows."""
+        if isinstance(shard, str):
+            if shard not in self._index:
+                raise KeyError(f"unknown shard: {shard}")
+            index = self._index[shard]
+        else:
+            index = shard
+        if not isinstance(index, int) or not 0 <= index < len(self.output_sizes):
+            raise IndexError(f"shard index out of range: {index}")
+        start, size = self._starts[index], self.output_sizes[index]
+        expected = (size, self.input_size)
+        if tuple(loaded_weight.shape) != expected:
+            raise ValueError(
+                f"expected shard shape {expected}, got {tuple(loaded_weight.shape)}"
+            )
+        with torch.no_grad():
+            self.weight[start:start + size].copy_(loaded_weight)
+
+
+class RMSNorm(nn.Module):
+    """Qwen3 RMSNorm, fp32 variance accumulation (reference layers.py:129-164)."""
+
+    def __init__(
+        self,
+        hidden_size: int,
+        *,
+        eps: float = 1e-6,
+        device: torch.device | str | None = None,
+        dtype: torch.dtype | None = None,
+    ) -> None:
+        super().__init__()
+        if hidden_size <= 0:
+            raise ValueError("hidden_size must be positive")
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(hidden_size, device=device, dtype=dtype))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return rms_norm(x, self.weight, self.eps)
+
+    def add(
+        self, x: torch.Tensor, residual: torch.Tensor,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """(norm(x + residual), x + residual), both rounded to the storage type."""
+        return add_rms_norm(x, residual, self.weight, self.eps)
+
+
+class RotaryEmbedding(nn.Module):
+    """Half-split RoPE tables (reference layers.py:167-245).
+
+    The reference keeps fp32 cos/sin of every position and casts the
+    gathered rows to the activation dtype each forward; casting is
+    elementwise, so this module stores the tables already cast (per dtype,
+    built on first use) and a forward is one gather per table.
+    """
+
+    def __init__(
+        self,
+        head_dim: int,
+        max_position: int,
+        *,
+        base: float = 1_000_000.0,
+        device: torch.device | str | None = None,
+    ) -> None:
+        super().__init__()
+        if head_dim <= 0:
+            raise ValueError("head_dim must be positive")
+        if max_position <= 0:
+            raise ValueError("max_position must be positive")
+        if base <= 0:
+            raise ValueError("base must be positive")
+        if head_dim % 2:
+            raise ValueError("head_dim must be even")
+        exponents = torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim
+        inv_freq = 1.0 / (base ** exponents)
+        positions = torch.arange(max_position, dtype=torch.float32, device=device)
+        angles = torch.outer(positions, inv_freq)
+        self.register_buffer("cos", angles.cos(), persistent=False)
+        self.register_buffer("sin", angles.sin(), persistent=False)
+        self._cast: dict[torch.dtype, tuple[torch.Tensor, torch.Tensor]] = {}
+
+    def _apply(self, fn, recurse=True):  # keep cast tables in sync with .to()
+        self._cast = {}
+        return super()._apply(fn, recurse)
+
+    def forward(
+        self, positions: torch.Tensor, dtype: torch.dtype,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """cos, sin of ``positions`` as [tokens, 1, head_dim / 2] in ``dtype``."""
+        tables = self._cast.get(dtype)
+        if tables is None:
+            if self.cos.is_cuda and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("RoPE tables must be cast before graph capture")
+            tables = (self.cos.to(dtype), self.sin.to(dtype))
+            self._cast[dtype] = tables
+        cos = tables[0].index_select(0, positions).unsqueeze(1)
+        sin = tables[1].index_select(0, positions).unsqueeze(1)
+        return cos, sin
+
+
+class SiluAndMul(nn.Module):
+    """silu(gate) * up of a packed [gate | up] activation (reference layers.py:248-251)."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return silu_and_mul(x)
