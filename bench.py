@@ -1,0 +1,286 @@
+"""Decode-loop benchmark: Qwen3-8B bf16, 64 concurrent sequences at 2048-token
+context, greedy, on one MI355X.
+
+A step is one decode iteration of the whole batch through the product path:
+CPU batch build + validation, one H2D metadata copy, the replayed hipGraph
+(36 layers of fused QK-norm/RoPE/KV-write, split-K paged decode attention,
+GEMMs, norms, LM head, sampling kernel) and the D2H of the sampled ids.
+Weights are random-init N(0, 0.02) (no checkpoints offline); the 2048-token
+contexts' KV pages are filled with N(0, 1) values before timing.
+
+Also reported on the same JSON line:
+  roofline     -- the dominant kernel (paged decode attention, one layer at
+                  the workload's shape) timed with HIP events on the stream
+                  it runs on: algorithmic bytes / average launch duration.
+  cpu_baseline -- the CPU oracle's decode step, one layer at full batch
+                  timed and extrapolated to all layers + LM head.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "tiny-vllm_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+MODELS = {
+    "qwen3-0.6b": dict(vocab_size=151936, hidden_size=1024, intermediate_size=3072,
+                       num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8,
+                       head_dim=128, tie_word_embeddings=True),
+    "qwen3-8b": dict(vocab_size=151936, hidden_size=4096, intermediate_size=12288,
+                     num_hidden_layers=36, num_attention_heads=32, num_key_value_heads=8,
+                     head_dim=128, tie_word_embeddings=False),
+    "qwen3-32b": dict(vocab_size=151936, hidden_size=5120, intermediate_size=25600,
+                      num_hidden_layers=64, num_attention_heads=64, num_key_value_heads=8,
+                      head_dim=128, tie_word_embeddings=False),
+}
+HBM_PEAK_GBS = 8000.0
+
+
+def qwen3_config(name: str, max_position: int):
+    from tinyvllm.models.qwen3 import Qwen3Config
+
+    return Qwen3Config.from_dict(dict(model_type="qwen3", rope_theta=1e6, rms_norm_eps=1e-6,
+                                      max_position_embeddings=max_position,
+                                      **MODELS[name]))
+
+
+class DecodeWorkload:
+    """Synthetic sequences parked at a fixed context, advanced one token per step."""
+
+    def __init__(self, batch: int, context: int, block_size: int, num_blocks: int,
+                 vocab: int, seed: int = 0):
+        import numpy as np
+
+        rng = np.random.default_rng(seed)
+        self.batch, self.bs = batch, block_size
+        self.lengths = [context] * batch
+        self.max_pages = num_blocks // batch
+        perm = rng.permutation(num_blocks)
+        self.tables = [perm[i * self.max_pages:(i + 1) * self.max_pages].tolist()
+                       for i in range(batch)]
+        self.tokens = rng.integers(0, vocab, size=batch).tolist()
+        self.plan_id = 0
+
+    def batch_for_step(self):
+        from tinyvllm.batch import PreparedBatch, StepMode
+        from tinyvllm.request import SamplingParams
+
+        bs = self.bs
+        positions, slots, table_ids, offsets, after = [], [], [], [0], []
+        for table, length in zip(self.tables, self.lengths):
+            p = length  # writes position `length`, context becomes length + 1
+            pages = p // bs + 1
+            positions.append(p)
+            slots.append(table[p // bs] * bs + p % bs)
+            table_ids.extend(table[:pages])
+            offsets.append(len(table_ids))
+            after.append(length + 1)
+        self.plan_id += 1
+        n = self.batch
+        greedy = SamplingParams(max_new_tokens=1 << 20)
+        return PreparedBatch(
+            plan_id=self.plan_id, mode=StepMode.DECODE_ONLY, input_ids=tuple(self.tokens),
+            positions=tuple(positions), q_offsets=tuple(range(n + 1)),
+            context_lens_before=tuple(self.lengths), query_lens=(1,) * n,
+            context_lens_after=tuple(after), sample_token_indices=tuple(range(n)),
+            sample_request_ids=tuple(range(n)), sampling_params=(greedy,) * n,
+            kv_block_size=bs, kv_num_blocks=self.max_pages * n,
+            kv_block_table_ids=tuple(table_ids), kv_block_table_offsets=tuple(offsets),
+            kv_slot_mapping=tuple(slots), request_ids=tuple(range(n)),
+        )
+
+    def advance(self, tokens):
+        self.tokens = list(tokens)
+        self.lengths = [length + 1 for length in self.lengths]
+
+
+def attention_roofline(executor, workload, cfg, iters: int = 30) -> dict:
+    """Time the paged decode kernel on layer 0 of the live cache with the
+    live step metadata, with HIP events on the stream it launches on."""
+    import torch
+
+    from tinyvllm.kernels.paged_decode import paged_decode_attention
+
+    runner = executor.runner
+    batch = workload.batch_for_step()
+    model_input = runner.decode_inputs.prepare(batch, [0] * batch.num_items)
+    meta = model_input.kv.decode
+    stream = torch.cuda.current_stream()
+    q = torch.randn(batch.num_items, cfg.num_attention_heads, cfg.head_dim,
+                    dtype=torch.bfloat16, device=runner.device)
+    out = torch.empty_like(q)
+    scale = cfg.head_dim ** -0.5
+    for _ in range(3):
+        paged_decode_attention(q, runner.kv_cache, 0, meta, out, scale=scale,
+                               workspace=runner.decode_workspace)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        paged_decode_attention(q, runner.kv_cache, 0, meta, out, scale=scale,
+                               workspace=runner.decode_workspace)
+    end.record(stream)
+    end.synchronize()
+    seconds = start.elapsed_time(end) / 1e3 / iters
+    lengths = batch.context_lens_after
+    pages = sum(math.ceil(l / workload.bs) for l in lengths)
+    rows, hq, hkv, d = batch.num_items, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    algorithmic = (sum(lengths) * hkv * d * 2 * 2 + 2 * rows * hq * d * 2
+                   + 8 * pages + 8 * (3 * rows + 1))
+    achieved = algorithmic / seconds / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "paged_decode_d128 (+ split-K merge)",
+            "avg_launch_us": round(seconds * 1e6, 2), "bytes_per_launch": algorithmic}
+
+
+def cpu_baseline(cfg, batch: int, context: int, reps: int = 2) -> dict:
+    """The oracle's decode step on the host cores: one decoder layer at full
+    batch and context (GEMMs + paged gather + fp32 softmax attention + the
+    pointwise chain), timed `reps` times, extrapolated to all layers plus
+    the LM head."""
+    import torch
+
+    from oracle import attention as OA
+    from oracle import model as OM
+    from oracle import pointwise as OP
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    dt = torch.bfloat16
+    h, hq, hkv, d, inter = (cfg.hidden_size, cfg.num_attention_heads,
+                            cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size)
+
+    def mat(*shape):
+        return (torch.randn(*shape, generator=g) * 0.02).to(dt)
+
+    w_qkv, w_o = mat((hq + 2 * hkv) * d, h), mat(h, hq * d)
+    w_gu, w_down = mat(2 * inter, h), mat(h, inter)
+    ones_h, ones_d = torch.ones(h, dtype=dt), torch.ones(d, dtype=dt)
+    bs = 16
+    pages = math.ceil((context + 1) / bs)
+    kc = torch.randn(batch * pages * bs, hkv, d, generator=g).to(dt)
+    vc = torch.randn(batch * pages * bs, hkv, d, generator=g).to(dt)
+    blocks = torch.arange(batch * pages)
+    offsets = torch.arange(batch + 1) * pages
+    lengths = torch.full((batch,), context + 1)
+    x = torch.randn(batch, h, generator=g).to(dt)
+    res = torch.randn(batch, h, generator=g).to(dt)
+    pos = torch.full((batch,), context)
+    cos, sin = OP.rope_tables(pos, d, cfg.rope_theta, dt)
+    slots = blocks.view(batch, pages)[:, context // bs] * bs + context % bs
+
+    def layer():
+        y, r = OP.add_rms_norm(x, res, ones_h)
+        qkv = OM.linear(y, w_qkv)
+        q = qkv[:, :hq * d].view(batch, hq, d)
+        k = qkv[:, hq * d:(hq + hkv) * d].view(batch, hkv, d)
+        v = qkv[:, (hq + hkv) * d:].view(batch, hkv, d)
+        q, k = OP.qk_norm_rope(q, k, ones_d, ones_d, cos, sin)
+        kc[slots], vc[slots] = k, v
+        out = torch.empty_like(q)
+        OA.decode_attention(q, kc, vc, torch.arange(batch), blocks, offsets, lengths, bs,
+                            d ** -0.5, out)
+        o = OM.linear(out.view(batch, hq * d), w_o)
+        y, r = OP.add_rms_norm(o, r, ones_h)
+        return OM.linear(OP.silu_and_mul(OM.linear(y, w_gu)), w_down)
+
+    layer()  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+    per_layer = sorted(times)[len(times) // 2]
+    w_head = mat(cfg.vocab_size, h)
+    t0 = time.perf_counter()
+    OM.linear(x, w_head).float().argmax(-1)
+    head = time.perf_counter() - t0
+    step = per_layer * cfg.num_hidden_layers + head
+    return {"value": round(batch / step, 3), "unit": "tok/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"oracle decode step, 1 of {cfg.num_hidden_layers} layers at bs{batch} "
+                       f"ctx{context} timed x{reps} (median {per_layer:.2f} s) + LM head "
+                       f"({head:.2f} s), extrapolated to the full model")}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--model", default="qwen3-8b", choices=sorted(MODELS))
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--context", type=int, default=2048)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the decode path is single-GPU by design "
+              "(multi-GPU sharding is documented, not built); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from tinyvllm.executor import Executor
+    from tinyvllm.models.qwen3 import Qwen3ForCausalLM
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    bs = 16
+    total_steps = args.steps + args.warmup + 2
+    max_len = args.context + total_steps + 16
+    max_model_len = 1 << max(12, (max_len - 1).bit_length())  # e.g. 4096
+    cfg = qwen3_config(args.model, max_position=max(max_model_len, 40960))
+    model = Qwen3ForCausalLM.random_init(cfg, device=device, dtype=torch.bfloat16, seed=0)
+    pages = math.ceil(max_len / bs)
+    num_blocks = args.batch * pages
+    executor = Executor(model, block_size=bs, num_blocks=num_blocks,
+                        max_model_len=max_model_len, max_num_seqs=args.batch)
+    cache = executor.runner.kv_cache
+    gen = torch.Generator(device=device).manual_seed(1)
+    cache.key.normal_(generator=gen)
+    cache.value.normal_(generator=gen)
+    workload = DecodeWorkload(args.batch, args.context, bs, num_blocks, cfg.vocab_size)
+
+    for _ in range(args.warmup):
+        workload.advance(executor.execute(workload.batch_for_step()).sampled_token_ids)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        workload.advance(executor.execute(workload.batch_for_step()).sampled_token_ids)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    tok_s = args.batch * args.steps / elapsed
+
+    roof = attention_roofline(executor, workload, cfg)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg, args.batch, args.context)
+    line = {
+        "metric": "decode tok/s Qwen3-8B bs64 ctx2k; paged-attn HBM GB/s and % of peak",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights N(0,0.02), random token ids, "
+                "2048-token contexts' KV filled N(0,1)",
+        "config": {"workload": f"{args.model} decode bs{args.batch} ctx{args.context}",
+                   "model": args.model, "global_batch": args.batch,
+                   "seq_len": args.context, "parallelism": "single-gpu",
+                   "attention_backend": "hip", "graphs": True},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -56,3 +56,67 @@ def paged_decode_case(*, seed: int, batch: int, heads: int, kv_heads: int,
         lengths=torch.tensor(lengths, dtype=torch.long),
         block_size=block_size, scale=head_dim ** -0.5,
     )
+
+
+class ManualBatches:
+    """Hand-rolled PreparedBatch builder for runner tests: each sequence owns
+    consecutive slices of a shuffled block pool; prompts are prefilled in
+    chunks, then every step decodes one token per sequence."""
+
+    def __init__(self, prompts, *, block_size, num_blocks, seed=0):
+        g = torch.Generator().manual_seed(seed)
+        perm = torch.randperm(num_blocks, generator=g).tolist()
+        self.bs, self.num_blocks = block_size, num_blocks
+        per = num_blocks // len(prompts)
+        self.tables = [perm[i * per:(i + 1) * per] for i in range(len(prompts))]
+        self.tokens = [list(p) for p in prompts]
+        self.done = [0] * len(prompts)  # tokens already in the cache
+        self.plan = 0
+
+    def _batch(self, items):
+        from tinyvllm.batch import PreparedBatch, StepMode
+        from tinyvllm.request import SamplingParams
+
+        ids, pos, qoff, before, qlen, after, sidx, srid = [], [], [0], [], [], [], [], []
+        tids, toff, slots = [], [0], []
+        for seq, n, sample in items:
+            start = self.done[seq]
+            ids += self.tokens[seq][start:start + n]
+            pos += list(range(start, start + n))
+            qoff.append(len(ids))
+            before.append(start)
+            qlen.append(n)
+            after.append(start + n)
+            table = self.tables[seq][: -(-(start + n) // self.bs)]
+            tids += table
+            toff.append(len(tids))
+            slots += [table[p // self.bs] * self.bs + p % self.bs for p in range(start, start + n)]
+            if sample:
+                sidx.append(len(ids) - 1)
+                srid.append(seq)
+        self.plan += 1
+        greedy = SamplingParams(max_new_tokens=1 << 20)
+        return PreparedBatch(
+            plan_id=self.plan, mode=StepMode.MIXED, input_ids=tuple(ids), positions=tuple(pos),
+            q_offsets=tuple(qoff), context_lens_before=tuple(before), query_lens=tuple(qlen),
+            context_lens_after=tuple(after), sample_token_indices=tuple(sidx),
+            sample_request_ids=tuple(srid), sampling_params=(greedy,) * len(sidx),
+            kv_block_size=self.bs, kv_num_blocks=self.num_blocks, kv_block_table_ids=tuple(tids),
+            kv_block_table_offsets=tuple(toff), kv_slot_mapping=tuple(slots),
+            request_ids=tuple(seq for seq, _, _ in items),
+        )
+
+    def prefill(self, seq, n, sample):
+        batch = self._batch([(seq, n, sample)])
+        return batch
+
+    def commit(self, items, tokens):
+        """Mark items' tokens as cached and append sampled tokens."""
+        it = iter(tokens)
+        for seq, n, sample in items:
+            self.done[seq] += n
+            if sample:
+                self.tokens[seq].append(int(next(it)))
+
+    def step(self, items):
+        return self._batch(items)

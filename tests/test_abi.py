@@ -56,8 +56,11 @@ def test_decode_workspace_sizes():
     from tinyvllm.kernels._extension import load_kernels
 
     lib = load_kernels()
-    # 8B shape at bs64: 512 (row, kv-head) units -> 4 splits of a 4096 context.
+    # 8B shape at bs64: 512 (row, kv-head) units -> 2 splits of a 4096 context.
     assert lib.tvllm_paged_decode_workspace_size(64, 32, 8, 128, 4096, 16) == \
-        64 * 32 * 4 * 130 * 4
+        64 * 32 * 2 * 130 * 4
+    # Long context, few rows (32B shape at bs16): 128 units -> 16 splits.
+    assert lib.tvllm_paged_decode_workspace_size(16, 64, 8, 128, 32768, 16) == \
+        16 * 64 * 16 * 130 * 4
     # Enough rows to fill the chip on their own: no split, no workspace.
     assert lib.tvllm_paged_decode_workspace_size(512, 32, 8, 128, 4096, 16) == 0

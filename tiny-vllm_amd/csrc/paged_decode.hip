@@ -28,6 +28,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 namespace tvllm {
@@ -97,21 +98,31 @@ struct DecodeArgs {
     float* part_ml;    // [rows, heads, splits, 2] (running max, sum)
 };
 
-// GP: group size rounded up to a power of two (<= 16); SPLIT: write partials.
-template <typename T, int GP, bool SPLIT>
-__global__ void __launch_bounds__(64)
+__device__ __forceinline__ float fast_exp2(float x) {
+    return __builtin_amdgcn_exp2f(x);  // v_exp_f32; inputs here are <= 0
+}
+
+// GP: group size rounded up to a power of two (<= 16); SPLIT: write partials;
+// NT: 16-token MFMA tiles per iteration; WPB: waves per workgroup (each wave
+// owns one KV head of the same row and split, so the workgroup streams
+// WPB * 256 contiguous bytes of every cache row it touches).
+template <typename T, int GP, bool SPLIT, int NT, int WPB>
+__global__ void __launch_bounds__(64 * WPB)
 paged_decode_d128(DecodeArgs<T> a) {
     constexpr int D = 128;
     constexpr int ROW16 = D / 8;  // 16-byte units per cache row of one head
-    const int lane = threadIdx.x;
+    constexpr int CH = 16 * NT;   // tokens per iteration
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int quad = lane >> 4;   // 16-lane row of the wave
     const int col = lane & 15;
 
     const int id = blockIdx.x;
     const int split = id % a.splits;
-    const int unit = id / a.splits;
-    const int kvh = unit % a.kv_heads;
-    const int r = unit / a.kv_heads;
+    const int rest = id / a.splits;
+    const int head_groups = a.kv_heads / WPB;
+    const int kvh = (rest % head_groups) * WPB + wave;
+    const int r = rest / head_groups;
     const int h0 = kvh * a.group;
 
     const int64_t row = a.rows[r];
@@ -166,39 +177,51 @@ paged_decode_d128(DecodeArgs<T> a) {
     float m_run = -INFINITY;  // running max (base-2 units), per score lane
     float l_run = 0.f;        // this lane's share of the denominator
 
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += 64) {
-        // Lane x resolves the cache row of chunk token t0 + x (clamped to the
-        // last valid token so that masked lanes still read mapped memory).
-        uint32_t my_row;
-        {
-            const int64_t t = min(t0 + lane, t_end - 1);
-            const int64_t page = t / bs;
-            const int64_t slot = a.blocks[table + page] * bs + (t - page * bs);
-            my_row = static_cast<uint32_t>((slot * a.kv_heads + kvh) * ROW16);
-        }
-
-        U16x8 kreg[4][4];  // [tile][k-slice]: token 16*tile + col
-        U16x8 vreg[4][4];  // [tile][i]:       token 16*tile + 4*quad + i
+    // Lane x resolves the cache row (16-byte units) of chunk token t0 + x,
+    // clamped to the last valid token so masked lanes read mapped memory.
+    auto resolve = [&](int64_t t0) -> uint32_t {
+        const int64_t t = min(t0 + (lane % CH), t_end - 1);
+        const int64_t page = t / bs;
+        const int64_t slot = a.blocks[table + page] * bs + (t - page * bs);
+        return static_cast<uint32_t>((slot * a.kv_heads + kvh) * ROW16);
+    };
+    U16x8 kreg[NT][4];  // [tile][k-slice]: token 16*tile + col
+    U16x8 vreg[NT][4];  // [tile][i]:       token 16*tile + 4*quad + i
+    auto load_k = [&](uint32_t my_row) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NT; ++j) {
             const uint32_t kr = shfl_u32(my_row, 16 * j + col);
             const U16x8* kp = a.k + kr + quad;
 #pragma unroll
             for (int c = 0; c < 4; ++c) kreg[j][c] = kp[c * 4];
         }
+    };
+    auto load_v = [&](uint32_t my_row) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t vr = shfl_u32(my_row, 16 * j + 4 * quad + i);
                 vreg[j][i] = a.v[vr + col];
             }
-        }
+    };
+
+    // Software pipeline: the loads of chunk i+1 are issued as soon as the
+    // registers of chunk i are consumed (K after Q.K^T, V after P.V), so
+    // every wave keeps HBM requests in flight while it computes.
+    {
+        const uint32_t first = resolve(t_begin);
+        load_k(first);
+        load_v(first);
+    }
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += CH) {
+        const bool has_next = t0 + CH < t_end;
+        const uint32_t next = has_next ? resolve(t0 + CH) : 0u;
 
         // Scores: s[j][i] = token 16j + 4*quad + i, query head col.
-        float s[4][4];
+        float s[NT][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NT; ++j) {
             f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(kreg[j][c], qb[c], d);
@@ -208,25 +231,26 @@ paged_decode_d128(DecodeArgs<T> a) {
                 s[j][i] = t < t_end ? d[i] * a.scale_log2 : -INFINITY;
             }
         }
+        if (has_next) load_k(next);
 
         float cmax = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[j][i]);
         cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
         cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
         const float m_new = fmaxf(m_run, cmax);
-        const float alpha = exp2f(m_run - m_new);
+        const float alpha = fast_exp2(m_run - m_new);
         m_run = m_new;
 
-        float pw[4][4];
+        float pw[NT][4];
         float psum = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = exp2f(s[j][i] - m_new);
+                const float p = fast_exp2(s[j][i] - m_new);
                 psum += p;
                 pw[j][i] = p;
             }
@@ -240,7 +264,7 @@ paged_decode_d128(DecodeArgs<T> a) {
         });
 
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NT; ++j) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float vv[8];
@@ -253,6 +277,7 @@ paged_decode_d128(DecodeArgs<T> a) {
                 });
             }
         }
+        if (has_next) load_v(next);
     }
 
     // Combine the four 16-lane rows (disjoint token subsets).
@@ -390,16 +415,49 @@ paged_decode_generic(const T* __restrict__ q, int64_t qts, int64_t qhs,
     }
 }
 
-// Workgroups the split heuristic aims for: 8 per CU on 256 CUs keeps every
-// SIMD busy with two resident waves and leaves room for tail imbalance.
-constexpr int64_t kTargetGroups = 2048;
 constexpr int64_t kMaxSplits = 64;
+
+// Launch shape of the MFMA decode kernel. `target` is the number of
+// (row, KV head, split) wave units the split heuristic aims for (0 = the
+// default rule in choose_splits); `tiles` 16-token MFMA tiles per iteration
+// and `waves` KV heads per workgroup. Measured on MI355X at Qwen3-8B bs64
+// ctx2048: 2 tiles (2 waves/SIMD resident) and 4 waves per workgroup.
+struct Tuning {
+    int64_t target = 0;
+    int tiles = 2;
+    int waves = 4;
+};
+
+// Defaults can be overridden for measurement with
+// TVLLM_DECODE_TUNING="target,tiles,waves" (read once per process).
+const Tuning& tuning() {
+    static const Tuning t = [] {
+        Tuning v;
+        if (const char* env = std::getenv("TVLLM_DECODE_TUNING")) {
+            long long target = 0;
+            int tiles = 0, waves = 0;
+            if (std::sscanf(env, "%lld,%d,%d", &target, &tiles, &waves) == 3 &&
+                target >= 0 && (tiles == 2 || tiles == 4) &&
+                (waves == 1 || waves == 2 || waves == 4 || waves == 8)) {
+                v.target = target;
+                v.tiles = tiles;
+                v.waves = waves;
+            }
+        }
+        return v;
+    }();
+    return t;
+}
 
 int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
                       int64_t block_size) {
     const int64_t units = rows * kv_heads;
     if (units <= 0) return 1;
-    int64_t s = (kTargetGroups + units - 1) / units;
+    // Many (row, KV head) units: few splits keep the merge traffic small;
+    // few units (long-context, small batch): split deeper to fill 256 CUs.
+    const int64_t target = tuning().target ? tuning().target
+                                           : (units >= 256 ? 1024 : 2048);
+    int64_t s = (target + units - 1) / units;
     const int64_t max_pages = (max_context + block_size - 1) / block_size;
     // Each split should own at least one full 64-token iteration.
     const int64_t by_tokens = (max_context + 63) / 64;
@@ -507,12 +565,31 @@ extern "C" int tvllm_paged_decode(
         args.part_ml = need ? args.part_o + num_rows * num_heads * splits * head_dim
                             : nullptr;
 
-#define TVLLM_DEC(GP)                                                          \
-    do {                                                                       \
-        if (splits > 1)                                                        \
-            paged_decode_d128<T, GP, true><<<int(grid), 64, 0, s>>>(args);     \
-        else                                                                   \
-            paged_decode_d128<T, GP, false><<<int(grid), 64, 0, s>>>(args);    \
+        const Tuning tn = tuning();
+        int wpb = tn.waves;
+        while (wpb > 1 && num_kv_heads % wpb != 0) wpb >>= 1;
+        const int64_t blocks_n = grid / wpb;
+#define TVLLM_DEC3(GP, NT, W)                                                   \
+    do {                                                                        \
+        if (splits > 1)                                                         \
+            paged_decode_d128<T, GP, true, NT, W>                               \
+                <<<int(blocks_n), 64 * W, 0, s>>>(args);                        \
+        else                                                                    \
+            paged_decode_d128<T, GP, false, NT, W>                              \
+                <<<int(blocks_n), 64 * W, 0, s>>>(args);                        \
+    } while (0)
+#define TVLLM_DEC2(GP, NT)                                                      \
+    do {                                                                        \
+        switch (wpb) {                                                          \
+            case 8: TVLLM_DEC3(GP, NT, 8); break;                               \
+            case 4: TVLLM_DEC3(GP, NT, 4); break;                               \
+            case 2: TVLLM_DEC3(GP, NT, 2); break;                               \
+            default: TVLLM_DEC3(GP, NT, 1); break;                              \
+        }                                                                       \
+    } while (0)
+#define TVLLM_DEC(GP)                                                           \
+    do {                                                                        \
+        if (tn.tiles == 2) TVLLM_DEC2(GP, 2); else TVLLM_DEC2(GP, 4);           \
     } while (0)
         if (group <= 1) TVLLM_DEC(1);
         else if (group <= 2) TVLLM_DEC(2);
@@ -520,6 +597,8 @@ extern "C" int tvllm_paged_decode(
         else if (group <= 8) TVLLM_DEC(8);
         else TVLLM_DEC(16);
 #undef TVLLM_DEC
+#undef TVLLM_DEC2
+#undef TVLLM_DEC3
         int st = launch_status("paged_decode");
         if (st != TVLLM_OK || splits <= 1) return st;
         paged_decode_merge<T><<<int(num_rows * num_heads), 64, 0, s>>>(

@@ -1,0 +1,113 @@
+"""hipGraph capture and replay of the whole decode step
+(reference: tinyvllm/runtime/graphs.py:12-139).
+
+One graph per batch-size bucket holds embedding -> all layers (fused
+QK-norm/RoPE/KV-write, split-K paged decode, GEMMs, norms) -> LM head ->
+sampling kernel, reading only the fixed ``DecodeInputs`` views. A replay is
+a single host call, so the per-step host cost no longer scales with
+layers x kernels. The reference caps capture at 16 rows and runs larger
+batches eagerly; here buckets cover every size up to ``max_num_seqs``.
+All graphs share one memory pool (they are replayed one at a time on the
+runner's stream, and outputs are consumed before the next replay).
+"""
+from __future__ import annotations
+
+import torch
+
+from tinyvllm.kernels.sampling import sample
+from tinyvllm.paged_kv import PagedKVCache
+from tinyvllm.runtime.attention import HipAttention
+from tinyvllm.runtime.inputs import DecodeInputs
+
+
+def bucket_sizes(limit: int) -> tuple[int, ...]:
+    """1, 2, 4, 8, then multiples of 8 (multiples of 16 past 128) up to limit."""
+    sizes = [s for s in (1, 2, 4) if s < limit]
+    size = 8
+    while size < limit:
+        sizes.append(size)
+        size += 8 if size < 128 else 16
+    sizes.append(limit)
+    return tuple(sorted(set(sizes)))
+
+
+class DecodeGraphs:
+    """Startup-only capture; the runner keeps model, cache and inputs alive."""
+
+    def __init__(self, stream: torch.cuda.Stream) -> None:
+        self.stream = stream
+        self.entries: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
+        self.tokens: torch.Tensor | None = None
+        self.pool = None
+
+    @torch.inference_mode()
+    def capture(self, model: torch.nn.Module, inputs: DecodeInputs, cache: PagedKVCache,
+                workspace: torch.Tensor | None, *, max_size: int | None = None) -> None:
+        limit = min(inputs.capacity, cache.num_blocks,
+                    max_size if max_size is not None else inputs.capacity)
+        sizes = bucket_sizes(limit)
+        # Dummy rows: one distinct block each, context 1, greedy.
+        d = inputs.d
+        n = limit
+        d["tokens"][:n].zero_()
+        d["positions"][:n].zero_()
+        d["slots"][:n].copy_(inputs.rows[:n] * cache.block_size)
+        d["offsets"][:n + 1].copy_(torch.arange(n + 1, device=inputs.device))
+        d["lengths"][:n].fill_(1)
+        d["blocks"][:n].copy_(inputs.rows[:n])
+        self.tokens = torch.zeros(inputs.capacity, dtype=torch.long, device=inputs.device)
+        # Build dtype-cast RoPE tables before capture.
+        model.model.rotary_emb(inputs.d["positions"][:1], next(model.parameters()).dtype)
+
+        side = torch.cuda.Stream(device=inputs.device)
+        side.wait_stream(self.stream)
+        self.pool = torch.cuda.graph_pool_handle()
+        try:
+            with torch.cuda.stream(side):
+                for size in reversed(sizes):
+                    model_input = inputs.view(size)
+                    params = inputs.sampling_views(size)
+                    out = self.tokens[:size]
+
+                    def step():
+                        attention = HipAttention(model_input, cache, decode_workspace=workspace)
+                        hidden = model(model_input.input_ids, model_input.positions,
+                                       attention=attention)
+                        logits = model.compute_logits(hidden)
+                        sample(logits, *params, out=out)
+                        return logits
+
+                    for _ in range(2):
+                        step()
+                    side.synchronize()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, pool=self.pool, stream=side):
+                        logits = step()
+                    self.entries[size] = (graph, logits, out)
+        finally:
+            side.synchronize()
+            # Leave the padding state behind for the first real batch.
+            d["slots"].fill_(-1)
+            d["lengths"].zero_()
+            torch.cuda.current_stream(inputs.device).synchronize()
+        self.entries = dict(sorted(self.entries.items()))
+
+    def bucket(self, count: int) -> int | None:
+        for size in self.entries:
+            if count <= size:
+                return size
+        return None
+
+    def replay(self, count: int) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """Replay the smallest graph that fits; (logits[:count], tokens[:count])."""
+        size = self.bucket(count)
+        if size is None:
+            return None
+        graph, logits, tokens = self.entries[size]
+        graph.replay()
+        return logits[:count], tokens[:count]
+
+    def close(self) -> None:
+        self.stream.synchronize()
+        self.entries.clear()
+        self.pool = None
