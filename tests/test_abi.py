@@ -53,14 +53,17 @@ def test_argument_errors_surface_without_touching_a_gpu():
 
 
 def test_decode_workspace_sizes():
+    """Splits inside one workgroup merge in LDS (no workspace); only long
+    contexts over few rows also split across workgroups and need HBM
+    partials for the merge kernel."""
     from tinyvllm.kernels._extension import load_kernels
 
     lib = load_kernels()
-    # 8B shape at bs64: 512 (row, kv-head) units -> 2 splits of a 4096 context.
-    assert lib.tvllm_paged_decode_workspace_size(64, 32, 8, 128, 4096, 16) == \
-        64 * 32 * 2 * 130 * 4
-    # Long context, few rows (32B shape at bs16): 128 units -> 16 splits.
+    # 8B shape at bs64: 512 (row, KV head) units -> 2 splits, one workgroup.
+    assert lib.tvllm_paged_decode_workspace_size(64, 32, 8, 128, 4096, 16) == 0
+    assert lib.tvllm_paged_decode_workspace_size(64, 16, 8, 128, 1024, 16) == 0
+    # One row, 8 KV heads: 16 splits of a 512 context -> 2 workgroups per head.
+    assert lib.tvllm_paged_decode_workspace_size(1, 16, 8, 128, 512, 16) == 16 * 2 * 130 * 4
+    # 32B shape at bs16, 32k context: 128 units -> 16 splits = 8 waves x 2 groups.
     assert lib.tvllm_paged_decode_workspace_size(16, 64, 8, 128, 32768, 16) == \
-        16 * 64 * 16 * 130 * 4
-    # Enough rows to fill the chip on their own: no split, no workspace.
-    assert lib.tvllm_paged_decode_workspace_size(512, 32, 8, 128, 4096, 16) == 0
+        16 * 64 * 2 * 130 * 4

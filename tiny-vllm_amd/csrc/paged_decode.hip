@@ -14,9 +14,11 @@
 //  * one wave64 workgroup per (row, KV head, split): the G = Hq/Hkv query
 //    heads of a KV head share every K/V byte it loads, so the cache is read
 //    once per KV head instead of once per query head;
-//  * split-K: the row's pages are cut into `splits` equal page ranges so that
-//    rows x KV heads x splits fills the 256 CUs; a merge kernel combines the
-//    (max, sum, unnormalised output) partials with the usual LSE rescale;
+//  * split-K inside the workgroup: a row's pages are cut into `splits` (<= 8)
+//    equal page ranges, one wave each, so rows x KV heads x splits waves fill
+//    the 256 CUs; the waves of one (row, KV head) sit in the same workgroup
+//    and merge their (max, sum, unnormalised output) partials through LDS
+//    with the usual LSE rescale - no partials in HBM, no merge kernel;
 //  * Q.K^T on the matrix cores: per 16-token tile, 4 MFMA 16x16x32 steps with
 //    A = K rows (natural cache layout, 64 contiguous bytes per lane quad),
 //    B = the G query rows zero-padded to 16 columns;
@@ -92,22 +94,28 @@ struct DecodeArgs {
     const int64_t* blocks;
     const int64_t* offsets;
     const int64_t* lengths;
-    int heads, kv_heads, group, block_size, splits;
-    float scale_log2;  // softmax scale * log2(e): scores live in base 2
-    float* part_o;     // [rows, heads, splits, 128] unnormalised outputs
-    float* part_ml;    // [rows, heads, splits, 2] (running max, sum)
+    int heads, kv_heads, group, block_size;
+    int splits;         // waves per KV head per workgroup
+    int grid_splits;    // workgroups per (row, KV head group)
+    int heads_per_wg;   // KV heads per workgroup
+    float scale_log2;   // softmax scale * log2(e): scores live in base 2
+    float* part_o;      // [rows, heads, grid_splits, 128] (grid_splits > 1)
+    float* part_ml;     // [rows, heads, grid_splits, 2]
 };
+
+constexpr int kMaxWaves = 8;  // 2 resident waves per SIMD at <= 256 VGPRs
+constexpr int64_t kMaxSplits = 64;
 
 __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);  // v_exp_f32; inputs here are <= 0
 }
 
-// GP: group size rounded up to a power of two (<= 16); SPLIT: write partials;
-// NT: 16-token MFMA tiles per iteration; WPB: waves per workgroup (each wave
-// owns one KV head of the same row and split, so the workgroup streams
-// WPB * 256 contiguous bytes of every cache row it touches).
-template <typename T, int GP, bool SPLIT, int NT, int WPB>
-__global__ void __launch_bounds__(64 * WPB)
+// GP: group size rounded up to a power of two (<= 16); NT: 16-token MFMA
+// tiles per iteration. Wave w of a workgroup owns KV head
+// (group of the workgroup) * heads_per_wg + w / splits and page range
+// w % splits of its row.
+template <typename T, int GP, int NT>
+__global__ void __launch_bounds__(64 * kMaxWaves)
 paged_decode_d128(DecodeArgs<T> a) {
     constexpr int D = 128;
     constexpr int ROW16 = D / 8;  // 16-byte units per cache row of one head
@@ -117,57 +125,26 @@ paged_decode_d128(DecodeArgs<T> a) {
     const int quad = lane >> 4;   // 16-lane row of the wave
     const int col = lane & 15;
 
-    const int id = blockIdx.x;
-    const int split = id % a.splits;
-    const int rest = id / a.splits;
-    const int head_groups = a.kv_heads / WPB;
-    const int kvh = (rest % head_groups) * WPB + wave;
-    const int r = rest / head_groups;
+    // blockIdx.x = (r * head_groups + head group) * grid_splits + grid split
+    const int head_groups = a.kv_heads / a.heads_per_wg;
+    const int gsplit = blockIdx.x % a.grid_splits;
+    const int unit = blockIdx.x / a.grid_splits;
+    const int r = unit / head_groups;
+    const int local_head = wave / a.splits;
+    const int split = wave - local_head * a.splits;
+    const int kvh = (unit - r * head_groups) * a.heads_per_wg + local_head;
     const int h0 = kvh * a.group;
 
     const int64_t row = a.rows[r];
     const int64_t length = a.lengths[r];
     const int bs = a.block_size;
     const int64_t pages = (length + bs - 1) / bs;
-    const int64_t per_split = (pages + a.splits - 1) / a.splits;
-    const int64_t p_begin = int64_t(split) * per_split;
+    const int total_splits = a.splits * a.grid_splits;
+    const int64_t per_split = (pages + total_splits - 1) / total_splits;
+    const int64_t p_begin = int64_t(gsplit * a.splits + split) * per_split;
     const int64_t p_end = min(pages, p_begin + per_split);
     const int64_t t_begin = p_begin * bs;
     const int64_t t_end = min(length, p_end * bs);
-
-    if (t_begin >= t_end) {
-        if constexpr (SPLIT) {
-            if (lane < a.group) {
-                float* ml = a.part_ml + ((int64_t(r) * a.heads + h0 + lane) * a.splits + split) * 2;
-                ml[0] = -INFINITY;
-                ml[1] = 0.f;
-            }
-        } else {
-            // Zero-length row: zeros, without touching Q, tables or KV.
-            for (int g = 0; g < a.group; ++g) {
-                T* o = a.out + row * a.ots + (h0 + g) * a.ohs;
-                for (int d = lane; d < D; d += 64) o[d] = static_cast<T>(0.f);
-            }
-        }
-        return;
-    }
-
-    const int64_t table = a.offsets[r];
-
-    // B operand: query head g = col (zero beyond the group), dims c*32 + quad*8.
-    U16x8 qb[4];
-    {
-        const bool has = col < a.group;
-        const T* qrow = a.q + row * a.qts + (h0 + (has ? col : 0)) * a.qhs + quad * 8;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            if (has) {
-                qb[c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
-            } else {
-                qb[c].w[0] = qb[c].w[1] = qb[c].w[2] = qb[c].w[3] = 0u;
-            }
-        }
-    }
 
     float acc[GP][8];
 #pragma unroll
@@ -177,108 +154,131 @@ paged_decode_d128(DecodeArgs<T> a) {
     float m_run = -INFINITY;  // running max (base-2 units), per score lane
     float l_run = 0.f;        // this lane's share of the denominator
 
-    // Lane x resolves the cache row (16-byte units) of chunk token t0 + x,
-    // clamped to the last valid token so masked lanes read mapped memory.
-    auto resolve = [&](int64_t t0) -> uint32_t {
-        const int64_t t = min(t0 + (lane % CH), t_end - 1);
-        const int64_t page = t / bs;
-        const int64_t slot = a.blocks[table + page] * bs + (t - page * bs);
-        return static_cast<uint32_t>((slot * a.kv_heads + kvh) * ROW16);
-    };
-    U16x8 kreg[NT][4];  // [tile][k-slice]: token 16*tile + col
-    U16x8 vreg[NT][4];  // [tile][i]:       token 16*tile + 4*quad + i
-    auto load_k = [&](uint32_t my_row) {
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const uint32_t kr = shfl_u32(my_row, 16 * j + col);
-            const U16x8* kp = a.k + kr + quad;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) kreg[j][c] = kp[c * 4];
-        }
-    };
-    auto load_v = [&](uint32_t my_row) {
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t vr = shfl_u32(my_row, 16 * j + 4 * quad + i);
-                vreg[j][i] = a.v[vr + col];
-            }
-    };
+    // An empty range (zero-length padding row, or more splits than pages)
+    // reads nothing - not even Q or the block table - but still joins the
+    // workgroup merge below.
+    if (t_begin < t_end) {
+        const int64_t table = a.offsets[r];
 
-    // Software pipeline: the loads of chunk i+1 are issued as soon as the
-    // registers of chunk i are consumed (K after Q.K^T, V after P.V), so
-    // every wave keeps HBM requests in flight while it computes.
-    {
-        const uint32_t first = resolve(t_begin);
-        load_k(first);
-        load_v(first);
-    }
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += CH) {
-        const bool has_next = t0 + CH < t_end;
-        const uint32_t next = has_next ? resolve(t0 + CH) : 0u;
-
-        // Scores: s[j][i] = token 16j + 4*quad + i, query head col.
-        float s[NT][4];
+        // B operand: query head g = col (zero beyond the group), dims c*32 + quad*8.
+        U16x8 qb[4];
+        {
+            const bool has = col < a.group;
+            const T* qrow = a.q + row * a.qts + (h0 + (has ? col : 0)) * a.qhs + quad * 8;
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            f32x4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(kreg[j][c], qb[c], d);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t t = t0 + 16 * j + 4 * quad + i;
-                s[j][i] = t < t_end ? d[i] * a.scale_log2 : -INFINITY;
+            for (int c = 0; c < 4; ++c) {
+                if (has) {
+                    qb[c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
+                } else {
+                    qb[c].w[0] = qb[c].w[1] = qb[c].w[2] = qb[c].w[3] = 0u;
+                }
             }
         }
-        if (has_next) load_k(next);
 
-        float cmax = -INFINITY;
+        // Lane x resolves the cache row (16-byte units) of chunk token t0 + x,
+        // clamped to the last valid token so masked lanes read mapped memory.
+        auto resolve = [&](int64_t t0) -> uint32_t {
+            const int64_t t = min(t0 + (lane % CH), t_end - 1);
+            const int64_t page = t / bs;
+            const int64_t slot = a.blocks[table + page] * bs + (t - page * bs);
+            return static_cast<uint32_t>((slot * a.kv_heads + kvh) * ROW16);
+        };
+        U16x8 kreg[NT][4];  // [tile][k-slice]: token 16*tile + col
+        U16x8 vreg[NT][4];  // [tile][i]:       token 16*tile + 4*quad + i
+        auto load_k = [&](uint32_t my_row) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
+            for (int j = 0; j < NT; ++j) {
+                const uint32_t kr = shfl_u32(my_row, 16 * j + col);
+                const U16x8* kp = a.k + kr + quad;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[j][i]);
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-        const float m_new = fmaxf(m_run, cmax);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-
-        float pw[NT][4];
-        float psum = 0.f;
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = fast_exp2(s[j][i] - m_new);
-                psum += p;
-                pw[j][i] = p;
+                for (int c = 0; c < 4; ++c) kreg[j][c] = kp[c * 4];
             }
-        l_run = l_run * alpha + psum;
+        };
+        auto load_v = [&](uint32_t my_row) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t vr = shfl_u32(my_row, 16 * j + 4 * quad + i);
+                    vreg[j][i] = a.v[vr + col];
+                }
+        };
 
-        static_for<0, GP>([&](auto gc) {
-            constexpr int g = decltype(gc)::value;
-            const float ag = read_lane<g>(alpha);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
-        });
-
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float vv[8];
-                unpack8<T>(vreg[j][i], vv);
-                static_for<0, GP>([&](auto gc) {
-                    constexpr int g = decltype(gc)::value;
-                    const float p = row_bcast<g>(pw[j][i]);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vv[e], acc[g][e]);
-                });
-            }
+        // Software pipeline: the loads of chunk i+1 are issued as soon as the
+        // registers of chunk i are consumed (K after Q.K^T, V after P.V), so
+        // every wave keeps HBM requests in flight while it computes.
+        {
+            const uint32_t first = resolve(t_begin);
+            load_k(first);
+            load_v(first);
         }
-        if (has_next) load_v(next);
-    }
+        for (int64_t t0 = t_begin; t0 < t_end; t0 += CH) {
+            const bool has_next = t0 + CH < t_end;
+            const uint32_t next = has_next ? resolve(t0 + CH) : 0u;
+
+            // Scores: s[j][i] = token 16j + 4*quad + i, query head col.
+            float s[NT][4];
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(kreg[j][c], qb[c], d);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t t = t0 + 16 * j + 4 * quad + i;
+                    s[j][i] = t < t_end ? d[i] * a.scale_log2 : -INFINITY;
+                }
+            }
+            if (has_next) load_k(next);
+
+            float cmax = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[j][i]);
+            cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+            cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+            const float m_new = fmaxf(m_run, cmax);
+            const float alpha = fast_exp2(m_run - m_new);
+            m_run = m_new;
+
+            float pw[NT][4];
+            float psum = 0.f;
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = fast_exp2(s[j][i] - m_new);
+                    psum += p;
+                    pw[j][i] = p;
+                }
+            l_run = l_run * alpha + psum;
+
+            static_for<0, GP>([&](auto gc) {
+                constexpr int g = decltype(gc)::value;
+                const float ag = read_lane<g>(alpha);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
+            });
+
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float vv[8];
+                    unpack8<T>(vreg[j][i], vv);
+                    static_for<0, GP>([&](auto gc) {
+                        constexpr int g = decltype(gc)::value;
+                        const float p = row_bcast<g>(pw[j][i]);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vv[e], acc[g][e]);
+                    });
+                }
+            }
+            if (has_next) load_v(next);
+        }
+
+    }  // t_begin < t_end
 
     // Combine the four 16-lane rows (disjoint token subsets).
 #pragma unroll
@@ -291,35 +291,78 @@ paged_decode_d128(DecodeArgs<T> a) {
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
 
-    if constexpr (SPLIT) {
-        static_for<0, GP>([&](auto gc) {
-            constexpr int g = decltype(gc)::value;
-            if (g < a.group && quad == 0) {
-                float4* po = reinterpret_cast<float4*>(
-                    a.part_o + ((int64_t(r) * a.heads + h0 + g) * a.splits + split) * D +
-                    col * 8);
-                po[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-                po[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-            }
-        });
-        if (lane < a.group) {
-            float* ml = a.part_ml + ((int64_t(r) * a.heads + h0 + lane) * a.splits + split) * 2;
-            ml[0] = m_run;
-            ml[1] = l_run;
-        }
-    } else {
-        static_for<0, GP>([&](auto gc) {
-            constexpr int g = decltype(gc)::value;
-            const float denom = read_lane<g>(l_run);
-            if (g < a.group && quad == 0) {
-                U16x8 o;
+    // Split merge through LDS: waves with split > 0 publish (o, m, l); the
+    // split-0 wave of each head rescales and sums them:
+    //   out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s,  M = max_s m_s.
+    __shared__ float red_o[kMaxWaves - 1][GP][D];
+    __shared__ float red_ml[kMaxWaves - 1][GP][2];
+    if (a.splits > 1) {
+        if (split > 0) {
+            const int slot = local_head * (a.splits - 1) + split - 1;
+            if (quad == 0) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    o.w[e] = pack2<T>(acc[g][2 * e] / denom, acc[g][2 * e + 1] / denom);
-                *reinterpret_cast<U16x8*>(a.out + row * a.ots + (h0 + g) * a.ohs + col * 8) = o;
+                for (int g = 0; g < GP; ++g) {
+                    float4* po = reinterpret_cast<float4*>(&red_o[slot][g][col * 8]);
+                    po[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+                    po[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+                }
+                if (col < GP) {
+                    red_ml[slot][col][0] = m_run;
+                    red_ml[slot][col][1] = l_run;
+                }
             }
-        });
+        }
+        __syncthreads();
+        if (split > 0) return;
     }
+
+    static_for<0, GP>([&](auto gc) {
+        constexpr int g = decltype(gc)::value;
+        float m_self = read_lane<g>(m_run);
+        float mx = m_self;
+        for (int s = 1; s < a.splits; ++s)
+            mx = fmaxf(mx, red_ml[local_head * (a.splits - 1) + s - 1][g][0]);
+        if (g >= a.group || quad != 0) return;
+        float num[8];
+        float den = 0.f;
+        if (mx == -INFINITY) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) num[e] = 0.f;
+        } else {
+            const float w0 = fast_exp2(m_self - mx);
+            den = w0 * read_lane<g>(l_run);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) num[e] = w0 * acc[g][e];
+            for (int s = 1; s < a.splits; ++s) {
+                const int slot = local_head * (a.splits - 1) + s - 1;
+                const float ms = red_ml[slot][g][0];
+                if (ms == -INFINITY) continue;
+                const float ws = fast_exp2(ms - mx);
+                den += ws * red_ml[slot][g][1];
+                const float4* po = reinterpret_cast<const float4*>(&red_o[slot][g][col * 8]);
+                const float4 p0 = po[0], p1 = po[1];
+                num[0] += ws * p0.x; num[1] += ws * p0.y; num[2] += ws * p0.z; num[3] += ws * p0.w;
+                num[4] += ws * p1.x; num[5] += ws * p1.y; num[6] += ws * p1.z; num[7] += ws * p1.w;
+            }
+        }
+        if (a.grid_splits > 1) {
+            // Unnormalised partial of this workgroup's page ranges.
+            const int64_t base = (int64_t(r) * a.heads + h0 + g) * a.grid_splits + gsplit;
+            float4* po = reinterpret_cast<float4*>(a.part_o + base * D + col * 8);
+            po[0] = make_float4(num[0], num[1], num[2], num[3]);
+            po[1] = make_float4(num[4], num[5], num[6], num[7]);
+            if (col == 0) {
+                a.part_ml[base * 2] = mx;
+                a.part_ml[base * 2 + 1] = den;
+            }
+            return;
+        }
+        if (mx == -INFINITY) den = 1.f;  // zero-length row: zeros
+        U16x8 packed;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) packed.w[e] = pack2<T>(num[2 * e] / den, num[2 * e + 1] / den);
+        *reinterpret_cast<U16x8*>(a.out + row * a.ots + (h0 + g) * a.ohs + col * 8) = packed;
+    });
 }
 
 // Merge split partials: out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
@@ -353,6 +396,7 @@ paged_decode_merge(const float* __restrict__ part_o, const float* __restrict__ p
         o[d] = static_cast<T>(num / denom);
     }
 }
+
 
 // Any head_dim <= 256 and any group: one wave per (row, query head), one
 // token at a time. Used for shapes the MFMA path does not cover.
@@ -415,13 +459,11 @@ paged_decode_generic(const T* __restrict__ q, int64_t qts, int64_t qhs,
     }
 }
 
-constexpr int64_t kMaxSplits = 64;
-
 // Launch shape of the MFMA decode kernel. `target` is the number of
-// (row, KV head, split) wave units the split heuristic aims for (0 = the
-// default rule in choose_splits); `tiles` 16-token MFMA tiles per iteration
-// and `waves` KV heads per workgroup. Measured on MI355X at Qwen3-8B bs64
-// ctx2048: 2 tiles (2 waves/SIMD resident) and 4 waves per workgroup.
+// (row, KV head, split) waves the split heuristic aims for (0 = the default
+// rule in choose_splits); `tiles` 16-token MFMA tiles per iteration;
+// `waves` the preferred waves per workgroup. Measured on MI355X at Qwen3-8B
+// bs64 ctx2048: 2 tiles (2 waves/SIMD resident) and 4 waves per workgroup.
 struct Tuning {
     int64_t target = 0;
     int tiles = 2;
@@ -437,8 +479,8 @@ const Tuning& tuning() {
             long long target = 0;
             int tiles = 0, waves = 0;
             if (std::sscanf(env, "%lld,%d,%d", &target, &tiles, &waves) == 3 &&
-                target >= 0 && (tiles == 2 || tiles == 4) &&
-                (waves == 1 || waves == 2 || waves == 4 || waves == 8)) {
+                target >= 0 && (tiles == 2 || tiles == 4) && waves >= 1 &&
+                waves <= kMaxWaves) {
                 v.target = target;
                 v.tiles = tiles;
                 v.waves = waves;
@@ -453,17 +495,46 @@ int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
                       int64_t block_size) {
     const int64_t units = rows * kv_heads;
     if (units <= 0) return 1;
-    // Many (row, KV head) units: few splits keep the merge traffic small;
-    // few units (long-context, small batch): split deeper to fill 256 CUs.
+    // Many (row, KV head) units: few splits; few units (long context, small
+    // batch): split deeper so that the waves still cover all 256 CUs.
     const int64_t target = tuning().target ? tuning().target
                                            : (units >= 256 ? 1024 : 2048);
     int64_t s = (target + units - 1) / units;
     const int64_t max_pages = (max_context + block_size - 1) / block_size;
-    // Each split should own at least one full 64-token iteration.
-    const int64_t by_tokens = (max_context + 63) / 64;
+    // Each split should own at least one full 32-token iteration.
+    const int64_t by_tokens = (max_context + 31) / 32;
     s = std::min(s, std::min(max_pages, by_tokens));
-    s = std::min(s, kMaxSplits);
+    s = std::min<int64_t>(s, kMaxSplits);
     return std::max<int64_t>(s, 1);
+}
+
+// Splits of one (row, KV head): `waves` page ranges inside a workgroup
+// (merged in LDS) times `grid` workgroups (merged by a second kernel).
+struct SplitPlan {
+    int64_t waves, grid;
+    int heads;  // KV heads per workgroup
+};
+
+int heads_per_group(int64_t kv_heads, int64_t splits);
+
+SplitPlan plan_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
+                      int64_t block_size) {
+    const int64_t total = choose_splits(rows, kv_heads, max_context, block_size);
+    SplitPlan p;
+    p.waves = std::min<int64_t>(total, kMaxWaves);
+    p.grid = (total + p.waves - 1) / p.waves;
+    p.heads = heads_per_group(kv_heads, p.waves);
+    return p;
+}
+
+// KV heads per workgroup: the largest power of two dividing kv_heads with
+// heads * splits <= the preferred waves per workgroup.
+int heads_per_group(int64_t kv_heads, int64_t splits) {
+    int h = 1;
+    while (h * 2 * splits <= std::max<int64_t>(tuning().waves, splits) &&
+           kv_heads % (h * 2) == 0)
+        h *= 2;
+    return h;
 }
 
 bool fast_path(int64_t head_dim, int64_t group, const void* q, int64_t qts,
@@ -486,11 +557,14 @@ extern "C" int64_t tvllm_paged_decode_workspace_size(int64_t num_rows,
                                                      int64_t head_dim,
                                                      int64_t max_context_len,
                                                      int64_t block_size) {
+    // Partials of the waves of one workgroup merge in LDS; only contexts
+    // split over several workgroups (few rows, long contexts) need HBM
+    // partials for the merge kernel.
     if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || head_dim != 128)
         return 0;
-    const int64_t s = choose_splits(num_rows, num_kv_heads, max_context_len, block_size);
-    if (s <= 1) return 0;
-    return num_rows * num_heads * s * (head_dim + 2) * int64_t(sizeof(float));
+    const SplitPlan p = plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
+    if (p.grid <= 1) return 0;
+    return num_rows * num_heads * p.grid * (head_dim + 2) * int64_t(sizeof(float));
 }
 
 extern "C" int tvllm_paged_decode(
@@ -529,18 +603,20 @@ extern "C" int tvllm_paged_decode(
                 int(head_dim), int(block_size), scale_log2);
             return launch_status("paged_decode");
         }
-        const int64_t splits =
-            choose_splits(num_rows, num_kv_heads, max_context_len, block_size);
-        const int64_t need = splits > 1
-            ? num_rows * num_heads * splits * (head_dim + 2) * int64_t(sizeof(float))
+        const SplitPlan plan =
+            plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
+        const int hpg = plan.heads;
+        const int64_t grid = num_rows * (num_kv_heads / hpg) * plan.grid;
+        TVLLM_CHECK(grid <= INT32_MAX, "paged_decode: decode grid is too large");
+        const int threads = int(64 * hpg * plan.waves);
+        const int64_t need = plan.grid > 1
+            ? num_rows * num_heads * plan.grid * (head_dim + 2) * int64_t(sizeof(float))
             : 0;
         TVLLM_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr),
                     "paged_decode: workspace of %lld bytes required, %lld given",
                     (long long)need, (long long)workspace_bytes);
         TVLLM_CHECK(need == 0 || aligned16(workspace),
                     "paged_decode: workspace must be 16-byte aligned");
-        const int64_t grid = num_rows * num_kv_heads * splits;
-        TVLLM_CHECK(grid <= INT32_MAX, "paged_decode: decode grid is too large");
 
         DecodeArgs<T> args;
         args.q = static_cast<const T*>(q);
@@ -559,52 +635,36 @@ extern "C" int tvllm_paged_decode(
         args.kv_heads = int(num_kv_heads);
         args.group = int(group);
         args.block_size = int(block_size);
-        args.splits = int(splits);
+        args.splits = int(plan.waves);
+        args.grid_splits = int(plan.grid);
+        args.heads_per_wg = hpg;
         args.scale_log2 = scale_log2;
         args.part_o = static_cast<float*>(workspace);
-        args.part_ml = need ? args.part_o + num_rows * num_heads * splits * head_dim
+        args.part_ml = need ? args.part_o + num_rows * num_heads * plan.grid * head_dim
                             : nullptr;
 
-        const Tuning tn = tuning();
-        int wpb = tn.waves;
-        while (wpb > 1 && num_kv_heads % wpb != 0) wpb >>= 1;
-        const int64_t blocks_n = grid / wpb;
-#define TVLLM_DEC3(GP, NT, W)                                                   \
-    do {                                                                        \
-        if (splits > 1)                                                         \
-            paged_decode_d128<T, GP, true, NT, W>                               \
-                <<<int(blocks_n), 64 * W, 0, s>>>(args);                        \
-        else                                                                    \
-            paged_decode_d128<T, GP, false, NT, W>                              \
-                <<<int(blocks_n), 64 * W, 0, s>>>(args);                        \
-    } while (0)
-#define TVLLM_DEC2(GP, NT)                                                      \
-    do {                                                                        \
-        switch (wpb) {                                                          \
-            case 8: TVLLM_DEC3(GP, NT, 8); break;                               \
-            case 4: TVLLM_DEC3(GP, NT, 4); break;                               \
-            case 2: TVLLM_DEC3(GP, NT, 2); break;                               \
-            default: TVLLM_DEC3(GP, NT, 1); break;                              \
-        }                                                                       \
-    } while (0)
 #define TVLLM_DEC(GP)                                                           \
     do {                                                                        \
-        if (tn.tiles == 2) TVLLM_DEC2(GP, 2); else TVLLM_DEC2(GP, 4);           \
+        if (tuning().tiles == 4)                                                \
+            paged_decode_d128<T, GP, 4><<<int(grid), threads, 0, s>>>(args);    \
+        else                                                                    \
+            paged_decode_d128<T, GP, 2><<<int(grid), threads, 0, s>>>(args);    \
     } while (0)
+        // Groups above 4 carry 64+ accumulator registers per lane: one
+        // 16-token tile per iteration keeps them within 256 VGPRs.
         if (group <= 1) TVLLM_DEC(1);
         else if (group <= 2) TVLLM_DEC(2);
         else if (group <= 4) TVLLM_DEC(4);
-        else if (group <= 8) TVLLM_DEC(8);
-        else TVLLM_DEC(16);
+        else if (group <= 8)
+            paged_decode_d128<T, 8, 1><<<int(grid), threads, 0, s>>>(args);
+        else
+            paged_decode_d128<T, 16, 1><<<int(grid), threads, 0, s>>>(args);
 #undef TVLLM_DEC
-#undef TVLLM_DEC2
-#undef TVLLM_DEC3
-        int st = launch_status("paged_decode");
-        if (st != TVLLM_OK || splits <= 1) return st;
+        const int st = launch_status("paged_decode");
+        if (st != TVLLM_OK || plan.grid <= 1) return st;
         paged_decode_merge<T><<<int(num_rows * num_heads), 64, 0, s>>>(
-            args.part_o, args.part_ml, static_cast<T*>(out), rows,
-            out_token_stride, out_head_stride, int(num_heads), int(splits),
-            int(head_dim));
+            args.part_o, args.part_ml, static_cast<T*>(out), rows, out_token_stride,
+            out_head_stride, int(num_heads), int(plan.grid), int(head_dim));
         return launch_status("paged_decode merge");
     });
 }

@@ -72,13 +72,15 @@ rms_norm_kernel(const T* __restrict__ x, int64_t rows, int64_t heads, int width,
     const T* src = x + tok * token_stride + (r - tok * heads) * head_stride;
     const T* res = RESIDUAL ? residual + tok * residual_stride : nullptr;
 
-    float v[NV][8];
+    // Weights are loaded up front so their latency overlaps the reduction.
+    float v[NV][8], wv[NV][8];
     float ss = 0.f;
 #pragma unroll
     for (int n = 0; n < NV; ++n) {
         const int c = (n * TPR + t) * 8;
         const int valid = active ? min(8, width - c) : 0;
         load8<T, VEC>(src + c, valid, v[n]);
+        load8<T, VEC>(weight + c, valid, wv[n]);
         if constexpr (RESIDUAL) {
             float rv[8];
             load8<T, VEC>(res + c, valid, rv);
@@ -105,10 +107,9 @@ rms_norm_kernel(const T* __restrict__ x, int64_t rows, int64_t heads, int width,
         const int c = (n * TPR + t) * 8;
         const int valid = min(8, width - c);
         if (valid <= 0) continue;
-        float w[8], y[8];
-        load8<T, VEC>(weight + c, valid, w);
+        float y[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) y[i] = rnd<T>(rnd<T>(v[n][i] * inv) * w[i]);
+        for (int i = 0; i < 8; ++i) y[i] = rnd<T>(rnd<T>(v[n][i] * inv) * wv[n][i]);
         store8<T, VEC>(dst + c, valid, y);
         if constexpr (RESIDUAL) store8<T, VEC>(rdst + c, valid, v[n]);
     }
@@ -240,7 +241,8 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
     const float eps = is_q ? q_eps : k_eps;
     const int half = head_dim / 2;
 
-    float x1[NP], x2[NP];
+    // Row, weights and RoPE angles are all loaded before the reduction.
+    float x1[NP], x2[NP], w1[NP], w2[NP], cs[NP], sn[NP];
     float ss = 0.f;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -248,6 +250,10 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
         const bool ok = d < half;
         x1[p] = ok ? to_f<T>(src[d]) : 0.f;
         x2[p] = ok ? to_f<T>(src[d + half]) : 0.f;
+        w1[p] = ok ? to_f<T>(w[d]) : 0.f;
+        w2[p] = ok ? to_f<T>(w[d + half]) : 0.f;
+        cs[p] = ok ? to_f<T>(cos_t[tok * half + d]) : 0.f;
+        sn[p] = ok ? to_f<T>(sin_t[tok * half + d]) : 0.f;
         ss += x1[p] * x1[p];
         ss += x2[p] * x2[p];
     }
@@ -272,10 +278,10 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
     for (int p = 0; p < NP; ++p) {
         const int d = lane + 64 * p;
         if (d >= half) continue;
-        const float n1 = rnd<T>(rnd<T>(x1[p] * inv) * to_f<T>(w[d]));
-        const float n2 = rnd<T>(rnd<T>(x2[p] * inv) * to_f<T>(w[d + half]));
-        const float c = to_f<T>(cos_t[tok * half + d]);
-        const float s = to_f<T>(sin_t[tok * half + d]);
+        const float n1 = rnd<T>(rnd<T>(x1[p] * inv) * w1[p]);
+        const float n2 = rnd<T>(rnd<T>(x2[p] * inv) * w2[p]);
+        const float c = cs[p];
+        const float s = sn[p];
         const float o1 = rnd<T>(n1 * c) - rnd<T>(n2 * s);
         const float o2 = rnd<T>(n2 * c) + rnd<T>(n1 * s);
         if (dst != nullptr) {
