@@ -102,6 +102,21 @@ class DecodeWorkload:
         self.lengths = [length + 1 for length in self.lengths]
 
 
+COUNTERS_FILE = ROOT / "profiles" / "paged_decode_qwen3-8b_bs64_ctx2k_counters.txt"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (copy-calibrated); None if that summary is absent."""
+    try:
+        for line in COUNTERS_FILE.read_text().splitlines():
+            if "traffic_bytes_per_launch:" in line:
+                return int(line.split("traffic_bytes_per_launch:")[1].strip(" )"))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def attention_roofline(executor, workload, cfg, iters: int = 30) -> dict:
     """Time the paged decode kernel on layer 0 of the live cache with the
     live step metadata, with HIP events on the stream it launches on."""
@@ -137,8 +152,9 @@ def attention_roofline(executor, workload, cfg, iters: int = 30) -> dict:
                    + 8 * pages + 8 * (3 * rows + 1))
     achieved = algorithmic / seconds / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "paged_decode_d128 (+ split-K merge)",
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(),
+            "kernel": "paged_decode_d128",
             "avg_launch_us": round(seconds * 1e6, 2), "bytes_per_launch": algorithmic}
 
 
@@ -213,6 +229,105 @@ def cpu_baseline(cfg, batch: int, context: int, reps: int = 2) -> dict:
                        f"({head:.2f} s), extrapolated to the full model")}
 
 
+def kernel_only(args) -> None:
+    """The decode-attention kernel alone at the workload's shape (one layer of
+    KV, the step's metadata), plus a 1 GiB device copy for counter
+    calibration. Used for rocprofv3 PMC passes, which profile dispatches
+    launched outside graphs."""
+    import torch
+
+    from tinyvllm.kernels.paged_decode import decode_workspace_bytes, paged_decode_attention
+    from tinyvllm.paged_kv import PagedKVCache
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    cfg = qwen3_config(args.model, max_position=40960)
+    device = torch.device("cuda", 0)
+    bs, rows, ctx = 16, args.batch, args.context + 1
+    pages = math.ceil(ctx / bs)
+    cache = PagedKVCache(num_layers=1, num_blocks=rows * pages, block_size=bs,
+                         num_kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+                         device=device, dtype=torch.bfloat16)
+    gen = torch.Generator(device=device).manual_seed(1)
+    cache.key.normal_(generator=gen)
+    cache.value.normal_(generator=gen)
+    perm = torch.randperm(rows * pages, device=device, generator=gen)
+    max_len = 4096
+    meta = SingleQueryMetadata(torch.arange(rows, device=device), perm,
+                               torch.arange(rows + 1, device=device) * pages,
+                               torch.full((rows,), ctx, device=device), max_len)
+    ws_bytes = decode_workspace_bytes(rows, cfg.num_attention_heads, cfg.num_key_value_heads,
+                                      cfg.head_dim, max_len, bs)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
+    q = torch.randn(rows, cfg.num_attention_heads, cfg.head_dim, dtype=torch.bfloat16,
+                    device=device)
+    out = torch.empty_like(q)
+    for _ in range(args.steps):
+        paged_decode_attention(q, cache, 0, meta, out, scale=cfg.head_dim ** -0.5,
+                               workspace=ws)
+    src = torch.empty(1 << 29, dtype=torch.bfloat16, device=device)  # 1 GiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel_only": True, "rows": rows, "context": ctx,
+                      "decode_launches": args.steps, "copy_bytes": src.numel() * 2}))
+
+
+def summarize_profile(directory: str, tail: int = 33) -> None:
+    """Print a short text summary of a rocprofv3 --kernel-trace --stats run
+    (kernel_stats.csv) and, when present, PMC counter averages per kernel."""
+    import csv
+    from collections import defaultdict
+
+    root = Path(directory)
+    stats = sorted(root.rglob("*kernel_stats.csv"))
+    if stats:
+        rows = list(csv.DictReader(open(stats[0])))
+        rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+        print(f"{'total ms':>9} {'%':>6} {'calls':>6} {'avg us':>9}  kernel")
+        for r in rows[:20]:
+            print(f"{float(r['TotalDurationNs']) / 1e6:9.2f} {float(r['Percentage']):6.2f} "
+                  f"{r['Calls']:>6} {float(r['AverageNs']) / 1e3:9.2f}  {r['Name'][:100]}")
+    traces = sorted(root.rglob("*kernel_trace.csv"))
+    if traces:
+        trace = list(csv.DictReader(open(traces[0])))
+        trace.sort(key=lambda r: int(r["Start_Timestamp"]))
+
+        def dur(r):
+            return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+        decode = [dur(r) for r in trace if "paged_decode_d128" in r["Kernel_Name"]]
+        if len(decode) >= tail:
+            print(f"-- paged_decode_d128: mean of the last {tail} dispatches "
+                  f"(bench.py's roofline loop) = {sum(decode[-tail:]) / tail:.2f} us")
+        ends = [i for i, r in enumerate(trace) if "sample_kernel" in r["Kernel_Name"]]
+        if len(ends) >= 2:
+            step = trace[ends[-2] + 1:ends[-1] + 1]
+            wall = (int(trace[ends[-1]]["End_Timestamp"])
+                    - int(trace[ends[-2]]["End_Timestamp"])) / 1e3
+            busy = sum(dur(r) for r in step)
+            groups = defaultdict(lambda: [0.0, 0])
+            for r in step:
+                name = r["Kernel_Name"]
+                key = ("GEMM (hipBLASLt " + name.split("_MT")[1][:10] + ")"
+                       if name.startswith("Cijk") else name[:70])
+                groups[key][0] += dur(r)
+                groups[key][1] += 1
+            print(f"-- last decode step (between sampling kernels): wall {wall:.1f} us, "
+                  f"kernels busy {busy:.1f} us, {len(step)} dispatches")
+            for key, (t, n) in sorted(groups.items(), key=lambda kv: -kv[1][0]):
+                print(f"  {t:9.1f} us  x{n:<4d} {key}")
+    for counters in sorted(root.rglob("*counter_collection.csv")):
+        acc = defaultdict(lambda: defaultdict(list))
+        for r in csv.DictReader(open(counters)):
+            acc[r["Kernel_Name"][:100]][r["Counter_Name"]].append(float(r["Counter_Value"]))
+        print(f"-- counters ({counters.name}): mean per dispatch")
+        for name, by_counter in sorted(acc.items()):
+            vals = ", ".join(f"{c}={sum(v) / len(v):.1f} (n={len(v)})"
+                             for c, v in sorted(by_counter.items()))
+            print(f"  {name}: {vals}")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,12 +337,23 @@ def main() -> None:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="run only the decode-attention kernel (for PMC passes)")
+    ap.add_argument("--summarize-profile", metavar="DIR",
+                    help="print a summary of a rocprofv3 output directory and exit")
     args = ap.parse_args()
+    if args.summarize_profile:
+        summarize_profile(args.summarize_profile)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path is single-GPU by design "
               "(multi-GPU sharding is documented, not built); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.kernel_only:
+        kernel_only(args)
+        return
 
     import torch
 
@@ -244,8 +370,10 @@ def main() -> None:
     model = Qwen3ForCausalLM.random_init(cfg, device=device, dtype=torch.bfloat16, seed=0)
     pages = math.ceil(max_len / bs)
     num_blocks = args.batch * pages
+    # Every step carries exactly `batch` rows: capture that one graph.
     executor = Executor(model, block_size=bs, num_blocks=num_blocks,
-                        max_model_len=max_model_len, max_num_seqs=args.batch)
+                        max_model_len=max_model_len, max_num_seqs=args.batch,
+                        graph_sizes=(args.batch,))
     cache = executor.runner.kv_cache
     gen = torch.Generator(device=device).manual_seed(1)
     cache.key.normal_(generator=gen)

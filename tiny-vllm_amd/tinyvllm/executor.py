@@ -52,11 +52,12 @@ class Executor:
     def __init__(self, model: nn.Module, *, block_size: int, num_blocks: int,
                  max_model_len: int | None = None, sampler: Sampler | None = None,
                  max_num_seqs: int = 64, attention_backend: str = "hip",
-                 enforce_eager: bool = False) -> None:
+                 enforce_eager: bool = False,
+                 graph_sizes: tuple[int, ...] | None = None) -> None:
         self.runner = ModelRunner(model, block_size=block_size, num_blocks=num_blocks,
                                   max_model_len=max_model_len, max_num_seqs=max_num_seqs,
                                   attention_backend=attention_backend,
-                                  enforce_eager=enforce_eager)
+                                  enforce_eager=enforce_eager, graph_sizes=graph_sizes)
         self.capabilities = ExecutorCapabilities(
             vocab_size=model.config.vocab_size,
             max_model_len=self.runner.max_model_len,

@@ -42,10 +42,13 @@ class DecodeGraphs:
 
     @torch.inference_mode()
     def capture(self, model: torch.nn.Module, inputs: DecodeInputs, cache: PagedKVCache,
-                workspace: torch.Tensor | None, *, max_size: int | None = None) -> None:
-        limit = min(inputs.capacity, cache.num_blocks,
-                    max_size if max_size is not None else inputs.capacity)
-        sizes = bucket_sizes(limit)
+                workspace: torch.Tensor | None, *,
+                sizes: tuple[int, ...] | None = None) -> None:
+        """Capture one graph per bucket size (default: ``bucket_sizes`` up to
+        the input capacity)."""
+        limit = min(inputs.capacity, cache.num_blocks)
+        sizes = bucket_sizes(limit) if sizes is None else tuple(
+            sorted({min(int(x), limit) for x in sizes}))
         # Dummy rows: one distinct block each, context 1, greedy.
         d = inputs.d
         n = limit

@@ -37,7 +37,7 @@ class ModelRunner:
         max_num_seqs: int = 64,
         attention_backend: str = "hip",
         enforce_eager: bool = False,
-        max_graph_batch: int | None = None,
+        graph_sizes: tuple[int, ...] | None = None,
     ) -> None:
         if type(enforce_eager) is not bool:
             raise TypeError("enforce_eager must be bool")
@@ -84,7 +84,7 @@ class ModelRunner:
                     self.decode_graphs = DecodeGraphs(self.decode_inputs.stream)
                     self.decode_graphs.capture(model, self.decode_inputs, self.kv_cache,
                                                self.decode_workspace,
-                                               max_size=max_graph_batch)
+                                               sizes=graph_sizes)
         except Exception:
             self.clear()
             raise
