@@ -328,6 +328,74 @@ def summarize_profile(directory: str, tail: int = 33) -> None:
             print(f"  {name}: {vals}")
 
 
+E2E = {
+    # name: (model, requests, prompt length(s), new tokens, shared prefix, arrivals)
+    "c3": dict(model="qwen3-0.6b", requests=32, prompt=512, new=256),
+    "c4": dict(model="qwen3-8b", requests=64, prompt=2048, new=256, poisson_ms=20.0),
+    "c5": dict(model="qwen3-32b", requests=16, prompt=(16384, 32768), new=128,
+               shared_prefix=4096),
+}
+
+
+def end_to_end(name: str, args) -> None:
+    """A SURVEY end-to-end configuration through the full engine (scheduler,
+    chunked prefill, prefix cache, graph-replayed decode): random-init
+    weights, random token-id prompts, greedy, output tokens per second."""
+    import numpy as np
+    import torch
+
+    from tinyvllm import GenerateRequest, SamplingParams
+    from tinyvllm.bootstrap import build_engine
+    from tinyvllm.models.qwen3 import Qwen3ForCausalLM
+
+    spec = E2E[name]
+    rng = np.random.default_rng(0)
+    n = spec["requests"]
+    if isinstance(spec["prompt"], tuple):
+        lengths = rng.integers(spec["prompt"][0], spec["prompt"][1] + 1, size=n).tolist()
+    else:
+        lengths = [spec["prompt"]] * n
+    cfg0 = qwen3_config(spec["model"], max_position=40960)
+    shared = rng.integers(0, cfg0.vocab_size, size=spec.get("shared_prefix", 0)).tolist()
+    prompts = [shared + rng.integers(0, cfg0.vocab_size, size=L - len(shared)).tolist()
+               for L in lengths]
+    max_len = max(lengths) + spec["new"] + 16
+    max_model_len = 1 << (max_len - 1).bit_length()
+    cfg = qwen3_config(spec["model"], max_position=max(max_model_len, 40960))
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    model = Qwen3ForCausalLM.random_init(cfg, device=device, dtype=torch.bfloat16, seed=0)
+    # Worst-case KV of every request (no preemption), rounded to blocks.
+    blocks = sum(-(-(L + spec["new"]) // 16) for L in lengths) + 64
+    engine = build_engine(model, max_model_len=max_model_len, max_num_seqs=n,
+                          max_num_batched_tokens=4096, num_blocks=blocks,
+                          prefill_chunk_size=512)
+    params = SamplingParams(max_new_tokens=spec["new"], ignore_eos=True)
+    start_ns = time.monotonic_ns()
+    offsets = np.zeros(n)
+    if spec.get("poisson_ms"):
+        offsets = np.cumsum(rng.exponential(spec["poisson_ms"] * 1e6, size=n))
+    requests = [GenerateRequest(p, params, arrival_ns=int(start_ns + o))
+                for p, o in zip(prompts, offsets)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    outputs = engine.generate(requests)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    generated = sum(len(o.output_token_ids) for o in outputs)
+    hits = engine.scheduler.block_manager.prefix_cache.hit_tokens
+    print(json.dumps({
+        "metric": f"end-to-end output tok/s ({name})", "value": round(generated / elapsed, 1),
+        "unit": "tok/s", "elapsed_s": round(elapsed, 2), "requests": n,
+        "prompt_tokens": sum(lengths), "output_tokens": generated,
+        "prefix_hit_tokens": hits, "dtype": "bf16",
+        "data": "synthetic: random-init weights N(0,0.02), random token-id prompts",
+        "config": {"workload": name, "model": spec["model"], **{
+            k: v for k, v in spec.items() if k != "model"}},
+    }), flush=True)
+    engine.close()
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -337,6 +405,8 @@ def main() -> None:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=["decode", *E2E], default="decode",
+                    help="decode (the metric) or an end-to-end SURVEY config")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the decode-attention kernel (for PMC passes)")
     ap.add_argument("--summarize-profile", metavar="DIR",
@@ -353,6 +423,9 @@ def main() -> None:
 
     if args.kernel_only:
         kernel_only(args)
+        return
+    if args.workload != "decode":
+        end_to_end(args.workload, args)
         return
 
     import torch

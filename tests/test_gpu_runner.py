@@ -2,9 +2,8 @@
 
 A tiny random-init Qwen3 (head_dim 128, two layers) is prefilled in chunks
 (MFMA prefill kernel, fused KV write) and then decoded greedily through the
-captured hipGraphs; every sampled token must equal the oracle's greedy
-continuation computed by full recomputation on the CPU (>= 99% agreement is
-the stated bar; these tiny models agree exactly)."""
+captured hipGraphs; at >= 99% of steps the sampled token must be the CPU
+oracle's greedy choice for the same context (teacher-forced)."""
 import pytest
 import torch
 
@@ -69,11 +68,11 @@ def test_greedy_decode_matches_oracle(device, enforce_eager):
         items = [(s, 1, True) for s in range(3)]
         res = executor.execute(mb.step(items))
         mb.commit(items, res.sampled_token_ids)
+    from test_gpu_engine import teacher_forced_agreement
+
     for s, prompt in enumerate(prompts):
         ours = mb.tokens[s][len(prompt):]
-        expect = OM.greedy_generate(CFG, weights, prompt, new)
-        agree = sum(a == b for a, b in zip(ours, expect)) / new
-        assert agree >= 0.99, (s, ours, expect)
+        assert teacher_forced_agreement(weights, prompt, ours) / new >= 0.99, (s, ours)
 
 
 def test_logits_match_oracle_at_every_position(device):

@@ -1,0 +1,309 @@
+"""Serial engine loop (reference: tinyvllm/engine.py:31-564).
+
+``step()`` applies queued commands, asks the scheduler for one plan,
+flattens it (BatchBuilder), runs it on the executor and commits the sampled
+tokens. Any failure after dispatch is fail-stop: the engine releases all
+KV ownership and refuses further work. Time is injectable (``clock``,
+``sleep``, ``step(now_ns)``) for deterministic arrival schedules.
+"""
+from __future__ import annotations
+
+import time
+from collections.abc import Callable, Sequence
+from dataclasses import dataclass, replace
+from typing import TYPE_CHECKING, Protocol
+
+from tinyvllm._validation import _check_non_negative_int
+from tinyvllm.batch import BatchBuilder, PreparedBatch, StepResult
+from tinyvllm.executor import ExecutorCapabilities
+from tinyvllm.request import CompletionEvent, RequestStatus, SamplingParams
+from tinyvllm.scheduler import (
+    AddCommand, CancelCommand, EngineCommand, ScheduleDecision, Scheduler,
+)
+
+if TYPE_CHECKING:
+    from tinyvllm.config import EngineConfig
+
+
+class EngineExecutor(Protocol):
+    @property
+    def capabilities(self) -> ExecutorCapabilities: ...
+
+    def execute(self, batch: PreparedBatch) -> StepResult: ...
+
+    def release(self, request_id: int) -> None: ...
+
+    def clear(self) -> None: ...
+
+
+@dataclass(frozen=True, slots=True)
+class GenerateRequest:
+    prompt_token_ids: tuple[int, ...]
+    sampling: SamplingParams
+    request_id: int | None = None
+    arrival_ns: int | None = None
+
+    def __post_init__(self) -> None:
+        object.__setattr__(self, "prompt_token_ids", tuple(self.prompt_token_ids))
+        if not isinstance(self.sampling, SamplingParams):
+            raise TypeError("sampling must be SamplingParams")
+
+
+@dataclass(frozen=True, slots=True)
+class TokenEvent:
+    request_id: int
+    token_id: int
+
+
+@dataclass(frozen=True, slots=True)
+class EngineStepEvents:
+    token_events: tuple[TokenEvent, ...] = ()
+    completion_events: tuple[CompletionEvent, ...] = ()
+
+    def __post_init__(self) -> None:
+        object.__setattr__(self, "token_events", tuple(self.token_events))
+        object.__setattr__(self, "completion_events", tuple(self.completion_events))
+
+
+@dataclass(frozen=True, slots=True)
+class RequestOutput:
+    request_id: int
+    status: RequestStatus
+    output_token_ids: tuple[int, ...]
+    prompt_token_count: int
+
+    @classmethod
+    def from_event(cls, event: CompletionEvent) -> "RequestOutput":
+        return cls(event.request_id, event.status, event.output_token_ids,
+                   event.prompt_token_count)
+
+
+class Engine:
+    """A serial engine; generate() owns its request batch exclusively."""
+
+    def __init__(self, scheduler: Scheduler, executor: EngineExecutor, *,
+                 clock: Callable[[], int] = time.monotonic_ns,
+                 sleep: Callable[[float], None] = time.sleep) -> None:
+        executor.capabilities.validate_configuration(
+            max_model_len=scheduler.max_model_len,
+            block_size=scheduler.kv_block_size,
+            num_blocks=scheduler.block_manager.pool.num_blocks,
+            max_batch_size=min(scheduler.max_step_requests, scheduler.max_scheduled_tokens),
+        )
+        executor.capabilities.validate_token_ids(scheduler.eos_token_ids)
+        self.scheduler = scheduler
+        self.executor = executor
+        self.builder = BatchBuilder(max_model_len=scheduler.max_model_len)
+        self._clock = clock
+        self._sleep = sleep
+        self._commands: list[EngineCommand] = []
+        self._next_seq = scheduler.last_command_seq + 1
+        self._active: set[int] = set(scheduler.request_ids)
+        self._next_id = max(self._active, default=-1) + 1
+        self._cancelling: set[int] = set()
+        self._closed = False
+        self._failed: str | None = None
+        self._generating = False
+
+    @classmethod
+    def from_config(cls, config: "EngineConfig") -> "Engine":
+        from tinyvllm.bootstrap import create_engine
+
+        return create_engine(config)
+
+    # ----------------------------------------------------------- requests --
+
+    def submit(self, prompt_token_ids: Sequence[int], sampling: SamplingParams, *,
+               arrival_ns: int | None = None, request_id: int | None = None) -> int:
+        self._healthy()
+        if self._generating:
+            raise RuntimeError("generate() owns the engine until it returns")
+        commands, next_id = self._stage((GenerateRequest(
+            tuple(prompt_token_ids), sampling, request_id, arrival_ns),))
+        self._publish(commands, next_id)
+        return commands[0].request_id
+
+    def _stage(self, specs) -> tuple[tuple[AddCommand, ...], int]:
+        """Validate requests and turn them into sequenced AddCommands."""
+        commands: list[AddCommand] = []
+        staged: set[int] = set()
+        next_id = self._next_id
+        for spec in specs:
+            if not isinstance(spec, GenerateRequest):
+                raise TypeError("requests must contain GenerateRequest values")
+            self.scheduler.validate_request(spec.prompt_token_ids, spec.sampling)
+            self.executor.capabilities.validate_token_ids(spec.prompt_token_ids)
+            arrival = self._clock() if spec.arrival_ns is None else spec.arrival_ns
+            _check_non_negative_int("arrival_ns", arrival)
+            rid = next_id if spec.request_id is None else spec.request_id
+            _check_non_negative_int("request_id", rid)
+            if rid in self._active or rid in staged:
+                raise ValueError(f"duplicate active request_id: {rid}")
+            commands.append(AddCommand(seq=self._next_seq + len(commands), request_id=rid,
+                                       prompt_token_ids=spec.prompt_token_ids,
+                                       sampling=spec.sampling, arrival_ns=arrival))
+            staged.add(rid)
+            next_id = max(next_id, rid + 1)
+        return tuple(commands), next_id
+
+    def _publish(self, commands: tuple[AddCommand, ...], next_id: int) -> None:
+        self._commands.extend(commands)
+        self._active.update(c.request_id for c in commands)
+        self._next_seq += len(commands)
+        self._next_id = next_id
+
+    def cancel(self, request_id: int) -> bool:
+        self._healthy()
+        _check_non_negative_int("request_id", request_id)
+        if request_id not in self._active or request_id in self._cancelling:
+            return False
+        self._commands.append(CancelCommand(seq=self._next_seq, request_id=request_id))
+        self._next_seq += 1
+        self._cancelling.add(request_id)
+        return True
+
+    # -------------------------------------------------------------- steps --
+
+    def step(self, now_ns: int | None = None) -> EngineStepEvents:
+        self._healthy()
+        explicit = now_ns is not None
+        start = self._clock() if now_ns is None else now_ns
+        _check_non_negative_int("now_ns", start)
+        commands = tuple(self._commands)
+        self.scheduler.apply_commands(commands, start)
+        del self._commands[:len(commands)]
+        for command in commands:
+            if isinstance(command, CancelCommand):
+                self._cancelling.discard(command.request_id)
+        txn = self.scheduler.begin_step(start)
+        if txn is None:
+            try:
+                return self._events(None)
+            except BaseException as exc:
+                self._fail_stop(exc)
+                raise
+        try:
+            requests = tuple(self.scheduler.get_request(i.request_id) for i in txn.plan.items)
+            batch = self.builder.prepare(txn.plan, requests, kv=txn.kv)
+            dispatch = start if explicit else max(start, self._clock())
+        except BaseException:
+            self.scheduler.rollback(txn)
+            raise
+        try:
+            self.scheduler.mark_dispatched(txn, dispatch)
+        except BaseException as exc:
+            self._fail_stop(exc)
+            raise
+        try:
+            result = self.executor.execute(batch)
+        except BaseException as exc:
+            self._fail_stop(exc)
+            raise RuntimeError("executor failed; engine is failed") from exc
+        try:
+            done = dispatch if explicit else max(dispatch, self._clock())
+            self.scheduler.commit_step(txn, result, done)
+            return self._events(result)
+        except BaseException as exc:
+            self._fail_stop(exc)
+            raise
+
+    def has_unfinished(self) -> bool:
+        return bool(self._active)
+
+    def generate(self, requests: Sequence[GenerateRequest]) -> list[RequestOutput]:
+        """Run a batch of requests to completion (arrivals honoured)."""
+        self._healthy()
+        if self._generating or self.has_unfinished():
+            raise RuntimeError("generate() requires an idle engine")
+        commands, next_id = self._stage(tuple(requests))
+        if not commands:
+            return []
+        ids = tuple(c.request_id for c in commands)
+        self._publish(commands, next_id)
+        outputs: dict[int, RequestOutput] = {}
+        self._generating = True
+        try:
+            while self.has_unfinished():
+                events = self.step()
+                for event in events.completion_events:
+                    outputs[event.request_id] = RequestOutput.from_event(event)
+                if self.scheduler.last_decision is ScheduleDecision.IDLE:
+                    arrival = self.scheduler.next_arrival_ns
+                    if arrival is not None:
+                        delay = (arrival - self._clock()) / 1e9
+                        if delay > 0:
+                            self._sleep(delay)
+        finally:
+            self._generating = False
+        if len(outputs) != len(ids):
+            raise RuntimeError("engine stopped before all requests completed")
+        return [outputs[i] for i in ids]
+
+    def _events(self, result: StepResult | None) -> EngineStepEvents:
+        completions = self.scheduler.consume_finished()
+        done = {e.request_id for e in completions}
+        # A cancel queued during execute may target a request that just
+        # finished: drop it before the request id becomes reusable.
+        if done & self._cancelling:
+            kept = [c for c in self._commands
+                    if not (isinstance(c, CancelCommand) and c.request_id in done)]
+            first = self.scheduler.last_command_seq + 1
+            self._commands = [replace(c, seq=first + k) for k, c in enumerate(kept)]
+            self._next_seq = first + len(kept)
+        self._active -= done
+        self._cancelling -= done
+        for event in completions:
+            self.executor.release(event.request_id)
+        if result is None:
+            return EngineStepEvents(completion_events=completions)
+        tokens = tuple(TokenEvent(r, t) for r, t in zip(result.sample_request_ids,
+                                                        result.sampled_token_ids))
+        return EngineStepEvents(token_events=tokens, completion_events=completions)
+
+    def reset_prefix_cache(self) -> None:
+        """Drop reusable prefixes between workloads, without reallocating KV."""
+        self._healthy()
+        if self._generating or self.has_unfinished():
+            raise RuntimeError("reset_prefix_cache requires an idle engine")
+        self.scheduler.block_manager.reset_prefix_cache()
+
+    def close(self) -> None:
+        """Permanently dispose resources; pending requests are discarded."""
+        if self._closed:
+            return
+        if self._generating:
+            raise RuntimeError("cannot close while generate() is running")
+        self._closed = True
+        error = RuntimeError("engine cleanup failed")
+        self._dispose(error)
+        if getattr(error, "__notes__", None):
+            raise error
+
+    def _healthy(self) -> None:
+        if self._closed:
+            raise RuntimeError("engine is closed")
+        if self._failed is not None:
+            raise RuntimeError(f"engine is failed: {self._failed}")
+
+    def _fail_stop(self, cause: BaseException) -> None:
+        self._failed = f"{type(cause).__name__}: {cause}"
+        self._dispose(cause)
+
+    def _dispose(self, cause: BaseException) -> None:
+        self._commands.clear()
+        self._active.clear()
+        self._cancelling.clear()
+        for name, cleanup in (("scheduler", self.scheduler.shutdown),
+                              ("executor", self.executor.clear)):
+            try:
+                cleanup()
+            except BaseException as err:  # keep cleaning up the rest
+                _note(cause, f"{name} cleanup failed: {err!r}")
+
+
+def _note(exc: BaseException, message: str) -> None:
+    """BaseException.add_note, also on Python 3.10."""
+    if hasattr(exc, "add_note"):
+        exc.add_note(message)
+    else:
+        exc.__notes__ = [*getattr(exc, "__notes__", []), message]
