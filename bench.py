@@ -67,34 +67,39 @@ class DecodeWorkload:
         self.tables = [perm[i * self.max_pages:(i + 1) * self.max_pages].tolist()
                        for i in range(batch)]
         self.tokens = rng.integers(0, vocab, size=batch).tolist()
+        self.np_tables_2d = np.asarray(self.tables, dtype=np.int64)
+        self.np_tables = list(self.np_tables_2d)
         self.plan_id = 0
+        from tinyvllm.request import SamplingParams
+
+        self.greedy = SamplingParams(max_new_tokens=1 << 20)
 
     def batch_for_step(self):
+        """The next decode step's PreparedBatch (block tables and slots as
+        int64 arrays, like BatchBuilder emits)."""
+        import numpy as np
+
         from tinyvllm.batch import PreparedBatch, StepMode
         from tinyvllm.request import SamplingParams
 
         bs = self.bs
-        positions, slots, table_ids, offsets, after = [], [], [], [0], []
-        for table, length in zip(self.tables, self.lengths):
-            p = length  # writes position `length`, context becomes length + 1
-            pages = p // bs + 1
-            positions.append(p)
-            slots.append(table[p // bs] * bs + p % bs)
-            table_ids.extend(table[:pages])
-            offsets.append(len(table_ids))
-            after.append(length + 1)
-        self.plan_id += 1
         n = self.batch
-        greedy = SamplingParams(max_new_tokens=1 << 20)
+        pos = np.asarray(self.lengths, dtype=np.int64)  # writes position `length`
+        pages = pos // bs + 1
+        offsets = np.concatenate(([0], np.cumsum(pages)))
+        table_ids = np.concatenate([t[:p] for t, p in zip(self.np_tables, pages)])
+        slots = self.np_tables_2d[np.arange(n), pos // bs] * bs + pos % bs
+        self.plan_id += 1
         return PreparedBatch(
             plan_id=self.plan_id, mode=StepMode.DECODE_ONLY, input_ids=tuple(self.tokens),
-            positions=tuple(positions), q_offsets=tuple(range(n + 1)),
+            positions=tuple(self.lengths), q_offsets=tuple(range(n + 1)),
             context_lens_before=tuple(self.lengths), query_lens=(1,) * n,
-            context_lens_after=tuple(after), sample_token_indices=tuple(range(n)),
-            sample_request_ids=tuple(range(n)), sampling_params=(greedy,) * n,
-            kv_block_size=bs, kv_num_blocks=self.max_pages * n,
-            kv_block_table_ids=tuple(table_ids), kv_block_table_offsets=tuple(offsets),
-            kv_slot_mapping=tuple(slots), request_ids=tuple(range(n)),
+            context_lens_after=tuple(l + 1 for l in self.lengths),
+            sample_token_indices=tuple(range(n)), sample_request_ids=tuple(range(n)),
+            sampling_params=(self.greedy,) * n, kv_block_size=bs,
+            kv_num_blocks=self.max_pages * n, kv_block_table_ids=table_ids,
+            kv_block_table_offsets=tuple(offsets.tolist()), kv_slot_mapping=slots,
+            request_ids=tuple(range(n)),
         )
 
     def advance(self, tokens):
@@ -344,7 +349,7 @@ def end_to_end(name: str, args) -> None:
     import numpy as np
     import torch
 
-    from tinyvllm import GenerateRequest, SamplingParams
+    from tinyvllm import SamplingParams
     from tinyvllm.bootstrap import build_engine
     from tinyvllm.models.qwen3 import Qwen3ForCausalLM
 
@@ -375,20 +380,34 @@ def end_to_end(name: str, args) -> None:
     offsets = np.zeros(n)
     if spec.get("poisson_ms"):
         offsets = np.cumsum(rng.exponential(spec["poisson_ms"] * 1e6, size=n))
-    requests = [GenerateRequest(p, params, arrival_ns=int(start_ns + o))
-                for p, o in zip(prompts, offsets)]
+    for p, o in zip(prompts, offsets):
+        engine.submit(p, params, arrival_ns=int(start_ns + o))
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    outputs = engine.generate(requests)
+    t0 = last = time.perf_counter()
+    generated = 0
+    first_token: dict[int, float] = {}
+    while engine.has_unfinished():
+        events = engine.step()
+        now = time.perf_counter()
+        generated += len(events.token_events)
+        for ev in events.token_events:
+            first_token.setdefault(ev.request_id, now - t0)
+        if not events.token_events and not events.completion_events:
+            arrival = engine.scheduler.next_arrival_ns
+            if arrival is not None:
+                time.sleep(max(0.0, (arrival - time.monotonic_ns()) / 1e9))
+        if now - last > 20:
+            print(f"[{name}] {now - t0:.0f}s: {generated} tokens", file=sys.stderr, flush=True)
+            last = now
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    generated = sum(len(o.output_token_ids) for o in outputs)
     hits = engine.scheduler.block_manager.prefix_cache.hit_tokens
     print(json.dumps({
         "metric": f"end-to-end output tok/s ({name})", "value": round(generated / elapsed, 1),
         "unit": "tok/s", "elapsed_s": round(elapsed, 2), "requests": n,
         "prompt_tokens": sum(lengths), "output_tokens": generated,
         "prefix_hit_tokens": hits, "dtype": "bf16",
+        "mean_ttft_s": round(sum(first_token.values()) / max(1, len(first_token)), 3),
         "data": "synthetic: random-init weights N(0,0.02), random token-id prompts",
         "config": {"workload": name, "model": spec["model"], **{
             k: v for k, v in spec.items() if k != "model"}},

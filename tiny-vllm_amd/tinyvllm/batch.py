@@ -10,6 +10,8 @@ from dataclasses import dataclass, field
 from enum import Enum, auto
 from typing import Protocol
 
+import numpy as np
+
 from tinyvllm._validation import _check_positive_int
 from tinyvllm.request import RequestState, SamplingParams, WorkClass
 
@@ -79,6 +81,10 @@ class StepPlan:
 
 @dataclass(frozen=True, slots=True)
 class PreparedBatch:
+    """One step's flat CPU metadata. Sequence fields are tuples of ints or
+    1-D int64 numpy arrays (BatchBuilder emits arrays for the block-table
+    ids and the slot mapping)."""
+
     plan_id: int
     mode: StepMode
     input_ids: tuple[int, ...]
@@ -92,9 +98,9 @@ class PreparedBatch:
     sampling_params: tuple[SamplingParams, ...]
     kv_block_size: int
     kv_num_blocks: int
-    kv_block_table_ids: tuple[int, ...]
+    kv_block_table_ids: tuple[int, ...] | np.ndarray
     kv_block_table_offsets: tuple[int, ...]
-    kv_slot_mapping: tuple[int, ...]
+    kv_slot_mapping: tuple[int, ...] | np.ndarray
     request_ids: tuple[int, ...]
 
     @property
@@ -134,13 +140,16 @@ class KVPlan(Protocol):
     num_blocks: int
 
     def append_metadata(self, request_id: int, start: int,
-                        count: int) -> tuple[tuple[int, ...], tuple[int, ...]]:
+                        count: int) -> tuple[np.ndarray, np.ndarray]:
         """(block ids of the request's table, slots of positions [start, start+count))."""
         ...
 
 
 class BatchBuilder:
-    """Flattens a StepPlan into a PreparedBatch (reference batch.py:164-288)."""
+    """Flattens a StepPlan into a PreparedBatch (reference batch.py:164-288).
+
+    The block-table ids and the slot mapping - the large, per-step fields -
+    are int64 numpy arrays; every other field is a tuple."""
 
     def __init__(self, *, max_model_len: int) -> None:
         _check_positive_int("max_model_len", max_model_len)
@@ -163,9 +172,9 @@ class BatchBuilder:
         sample_idx: list[int] = []
         sample_rid: list[int] = []
         params: list[SamplingParams] = []
-        table_ids: list[int] = []
+        tables: list[np.ndarray] = []
         table_off = [0]
-        slots: list[int] = []
+        slots: list[np.ndarray] = []
         rids: list[int] = []
         for item, request in zip(plan.items, requests):
             if request.request_id != item.request_id:
@@ -181,9 +190,9 @@ class BatchBuilder:
             table, slot_map = kv.append_metadata(item.request_id, item.token_start,
                                                  item.query_len)
             rids.append(request.request_id)
-            table_ids.extend(table)
-            table_off.append(len(table_ids))
-            slots.extend(slot_map)
+            tables.append(table)
+            table_off.append(table_off[-1] + len(table))
+            slots.append(slot_map)
             input_ids.extend(tokens)
             positions.extend(range(item.context_len_before, after))
             q_offsets.append(len(input_ids))
@@ -201,7 +210,9 @@ class BatchBuilder:
             query_lens=tuple(query_l), context_lens_after=tuple(after_l),
             sample_token_indices=tuple(sample_idx), sample_request_ids=tuple(sample_rid),
             sampling_params=tuple(params), kv_block_size=kv.block_size,
-            kv_num_blocks=kv.num_blocks, kv_block_table_ids=tuple(table_ids),
-            kv_block_table_offsets=tuple(table_off), kv_slot_mapping=tuple(slots),
+            kv_num_blocks=kv.num_blocks,
+            kv_block_table_ids=np.concatenate(tables) if tables else np.zeros(0, np.int64),
+            kv_block_table_offsets=tuple(table_off),
+            kv_slot_mapping=np.concatenate(slots) if slots else np.zeros(0, np.int64),
             request_ids=tuple(rids),
         )

@@ -19,8 +19,13 @@ from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 from enum import Enum, auto
 
+import numpy as np
+
 from tinyvllm._validation import _check_non_negative_int, _check_positive_int
 from tinyvllm.prefix_cache import PrefixCache
+
+
+_EMPTY = np.zeros(0, dtype=np.int64)
 
 
 class BlockState(Enum):
@@ -208,15 +213,16 @@ class BlockPlanTxn:
     """One step's staged block-table changes and slot mappings."""
 
     __slots__ = ("_plan_id", "_state", "_manager", "_reservation", "_tables",
-                 "_slots", "_ends", "_prefixes")
+                 "_ids", "_slots", "_ends", "_prefixes")
 
-    def __init__(self, *, plan_id, manager, reservation, tables, slots, ends, prefixes):
+    def __init__(self, *, plan_id, manager, reservation, tables, ids, slots, ends, prefixes):
         self._plan_id = plan_id
         self._state = BlockTxnState.PREPARED
         self._manager = manager
         self._reservation = reservation
         self._tables: dict[int, tuple[BlockRef, ...]] = tables
-        self._slots: dict[int, tuple[int, ...]] = slots
+        self._ids: dict[int, np.ndarray] = ids
+        self._slots: dict[int, np.ndarray] = slots
         self._ends: dict[int, int] = ends
         self._prefixes: dict[int, tuple[BlockRef, ...]] = prefixes
 
@@ -242,14 +248,17 @@ class BlockPlanTxn:
         return self._manager.pool.num_blocks
 
     def append_metadata(self, request_id: int, token_start: int,
-                        query_len: int) -> tuple[tuple[int, ...], tuple[int, ...]]:
-        """(physical block ids of the request's table, write slots)."""
+                        query_len: int) -> tuple[np.ndarray, np.ndarray]:
+        """(physical block ids of the request's table, write slots) as int64
+        arrays (the reference returns BlockRefs and a slot tuple; ids are
+        what every consumer reads, kept as arrays so a step's metadata is
+        flattened with memcpys)."""
         self._readable()
         if (request_id not in self._ends
                 or self._ends[request_id] != token_start + query_len
                 or len(self._slots[request_id]) != query_len):
             raise ValueError("work item does not match its KV append")
-        return tuple(r.block_id for r in self._tables[request_id]), self._slots[request_id]
+        return self._ids[request_id], self._slots[request_id]
 
     def _readable(self) -> None:
         if self._state not in (BlockTxnState.PREPARED, BlockTxnState.DISPATCHED):
@@ -278,6 +287,7 @@ class BlockManager:
         self.prefix_cache = PrefixCache(block_size=block_size, pool=self.pool,
                                         enabled=enable_prefix_caching)
         self._tables: dict[int, tuple[BlockRef, ...]] = {}
+        self._ids: dict[int, np.ndarray] = {}   # block ids of each table (int64)
         self._valid: dict[int, int] = {}
         self._open: BlockPlanTxn | None = None
         self._last: BlockPlanTxn | None = None
@@ -307,11 +317,14 @@ class BlockManager:
         if not swaps:
             return
         updated = list(table)
+        ids = self._ids[request_id].copy()
         for index, canonical in swaps:
             self.pool.retain(canonical)
             self.pool.release(table[index])
             updated[index] = canonical
+            ids[index] = canonical.block_id
         self._tables[request_id] = tuple(updated)
+        self._ids[request_id] = ids
 
     def reset_prefix_cache(self) -> None:
         if self._open is not None or self._tables:
@@ -366,18 +379,27 @@ class BlockManager:
                 self._unpin(prefixes)
                 return None
         fresh = iter(reservation.block_refs if reservation else ())
-        tables, slots, ends = {}, {}, {}
+        tables, ids, slots, ends = {}, {}, {}, {}
         bs = self.block_size
         for append, need in zip(appends, needs):
-            table = (append.prefix or self.block_table(append.request_id)) + tuple(
-                next(fresh) for _ in range(need))
+            rid = append.request_id
+            new = tuple(next(fresh) for _ in range(need))
+            if append.prefix:
+                base = append.prefix
+                base_ids = np.fromiter((r.block_id for r in base), np.int64, len(base))
+            else:
+                base = self.block_table(rid)
+                base_ids = self._ids.get(rid, _EMPTY)
+            table = base + new
+            table_ids = (np.concatenate((base_ids, np.fromiter(
+                (r.block_id for r in new), np.int64, need))) if need else base_ids)
             end = append.token_start + append.query_len
-            tables[append.request_id] = table
-            ends[append.request_id] = end
-            slots[append.request_id] = tuple(
-                table[p // bs].block_id * bs + p % bs for p in range(append.token_start, end))
+            pos = np.arange(append.token_start, end, dtype=np.int64)
+            tables[rid], ids[rid], ends[rid] = table, table_ids, end
+            slots[rid] = table_ids[pos // bs] * bs + pos % bs
         self._open = BlockPlanTxn(plan_id=plan_id, manager=self, reservation=reservation,
-                                  tables=tables, slots=slots, ends=ends, prefixes=prefixes)
+                                  tables=tables, ids=ids, slots=slots, ends=ends,
+                                  prefixes=prefixes)
         self._last = None
         return self._open
 
@@ -385,6 +407,7 @@ class BlockManager:
         if self._open is not None:
             raise RuntimeError("cannot release blocks during a KV transaction")
         table = self._tables.pop(request_id, ())
+        self._ids.pop(request_id, None)
         self._valid.pop(request_id, None)
         self.prefix_cache.forget_request(request_id)
         for ref in reversed(table):
@@ -416,6 +439,7 @@ class BlockManager:
         if txn._reservation is not None:
             self.pool.commit(txn._reservation)
         self._tables.update(txn._tables)
+        self._ids.update(txn._ids)
         txn._state = BlockTxnState.DISPATCHED
 
     def _complete_writes(self, txn: BlockPlanTxn) -> None:

@@ -113,11 +113,16 @@ class DecodeInputs:
         h["lengths"][:count] = batch.context_lens_after
         h["blocks"][:table_size] = batch.kv_block_table_ids
         params = batch.sampling_params
-        h["temperature"][:count] = [p.temperature for p in params]
-        h["top_p"][:count] = [p.top_p for p in params]
-        h["top_k"][:count] = [p.top_k for p in params]
+        first = params[0]
+        if all(p == first for p in params):  # one policy for the whole batch
+            rows = [first]
+        else:
+            rows = params
+        h["temperature"][:count] = [p.temperature for p in rows]
+        h["top_p"][:count] = [p.top_p for p in rows]
+        h["top_k"][:count] = [p.top_k for p in rows]
         h["seeds"][:count] = [p.seed - (1 << 64) if p.seed >= (1 << 63) else p.seed
-                              for p in params]
+                              for p in rows]
         h["counters"][:count] = counters
         size = self._blocks_offset + 8 * table_size
         self.device_data[:size].copy_(self.host[:size], non_blocking=True)

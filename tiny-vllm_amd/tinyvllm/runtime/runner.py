@@ -137,15 +137,19 @@ class ModelRunner:
         tlen = np.diff(toff)
         if (tlen != -(-after // bs)).any():
             raise ValueError("block table length does not match context")
-        owner = np.repeat(np.arange(count), tlen)
-        if np.unique(owner * cache.num_blocks + ids).size != ids.size:
-            raise ValueError("one request cannot alias its logical blocks")
-        # Written blocks: logical index >= before // bs of their row.
-        logical = np.arange(ids.size) - toff[owner]
-        written = logical >= (before // bs)[owner]
-        uniq, refs = np.unique(ids, return_counts=True)
-        if np.isin(ids[written], uniq[refs > 1]).any():
-            raise ValueError("shared blocks must be complete read-only prefixes")
+        # Blocks referenced more than once are the only ones that can alias
+        # inside a row or be shared between rows; usually there are none.
+        ordered = np.sort(ids)
+        repeated = ordered[1:][ordered[1:] == ordered[:-1]]
+        if repeated.size:
+            owner = np.repeat(np.arange(count), tlen)
+            if np.unique(owner * cache.num_blocks + ids).size != ids.size:
+                raise ValueError("one request cannot alias its logical blocks")
+            # Written blocks: logical index >= before // bs of their row.
+            logical = np.arange(ids.size) - toff[owner]
+            written = logical >= (before // bs)[owner]
+            if np.isin(ids[written], repeated).any():
+                raise ValueError("shared blocks must be complete read-only prefixes")
         expect = ids[toff[item] + pos // bs] * bs + pos % bs
         if (expect != np.asarray(batch.kv_slot_mapping, dtype=np.int64)).any():
             raise ValueError("write slots do not match block tables and positions")
