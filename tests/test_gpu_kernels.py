@@ -331,3 +331,15 @@ def test_sample_stays_in_kept_set_and_follows_softmax(device):
                  torch.arange(n, device=device)).cpu()
     freq = torch.bincount(out, minlength=3).float() / n
     assert torch.allclose(freq, probs, atol=0.03), freq
+
+
+@pytest.mark.parametrize("rows,heads,ctx,max_ctx", [
+    (64, 32, 2049, 4096),   # the benchmark shape: 2 splits, 4-wave workgroups
+    (4, 64, 20000, 32768),  # long context, few rows: workgroup-level splits + merge
+])
+def test_decode_benchmark_and_long_context_shapes(device, rows, heads, ctx, max_ctx):
+    pages = -(-ctx // 16)
+    case = paged_decode_case(seed=rows + ctx, batch=rows, heads=heads, kv_heads=8,
+                             pool_blocks=rows * pages + 8, lengths=[ctx] * rows)
+    out, expect = _run_decode(case, device, max_context_len=max_ctx)
+    assert_bf16_close(out, expect)

@@ -114,12 +114,13 @@ __device__ __forceinline__ float fast_exp2(float x) {
 // tiles per iteration. Wave w of a workgroup owns KV head
 // (group of the workgroup) * heads_per_wg + w / splits and page range
 // w % splits of its row.
-template <typename T, int GP, int NT>
-__global__ void __launch_bounds__(64 * kMaxWaves)
+template <typename T, int GP, int NT, int MAXW>
+__global__ void __launch_bounds__(64 * MAXW)
 paged_decode_d128(DecodeArgs<T> a) {
     constexpr int D = 128;
     constexpr int ROW16 = D / 8;  // 16-byte units per cache row of one head
     constexpr int CH = 16 * NT;   // tokens per iteration
+    static_assert(CH <= 64, "one lane resolves one token of an iteration");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int quad = lane >> 4;   // 16-lane row of the wave
@@ -461,12 +462,14 @@ paged_decode_generic(const T* __restrict__ q, int64_t qts, int64_t qhs,
 
 // Launch shape of the MFMA decode kernel. `target` is the number of
 // (row, KV head, split) waves the split heuristic aims for (0 = the default
-// rule in choose_splits); `tiles` 16-token MFMA tiles per iteration;
-// `waves` the preferred waves per workgroup. Measured on MI355X at Qwen3-8B
-// bs64 ctx2048: 2 tiles (2 waves/SIMD resident) and 4 waves per workgroup.
+// rule in choose_splits); `tiles` 16-token MFMA tiles per iteration (4 is
+// used when a workgroup has at most 4 waves: one wave per SIMD with a
+// 512-register budget keeps 32 KiB of K/V loads in flight per wave; larger
+// workgroups use 2 tiles at 2 waves per SIMD); `waves` the preferred waves
+// per workgroup. Measured on MI355X at Qwen3-8B bs64 ctx2048.
 struct Tuning {
     int64_t target = 0;
-    int tiles = 2;
+    int tiles = 4;
     int waves = 4;
 };
 
@@ -645,10 +648,11 @@ extern "C" int tvllm_paged_decode(
 
 #define TVLLM_DEC(GP)                                                           \
     do {                                                                        \
-        if (tuning().tiles == 4)                                                \
-            paged_decode_d128<T, GP, 4><<<int(grid), threads, 0, s>>>(args);    \
+        if (tuning().tiles == 4 && threads <= 256)                              \
+            paged_decode_d128<T, GP, 4, 4><<<int(grid), threads, 0, s>>>(args); \
         else                                                                    \
-            paged_decode_d128<T, GP, 2><<<int(grid), threads, 0, s>>>(args);    \
+            paged_decode_d128<T, GP, 2, kMaxWaves>                              \
+                <<<int(grid), threads, 0, s>>>(args);                           \
     } while (0)
         // Groups above 4 carry 64+ accumulator registers per lane: one
         // 16-token tile per iteration keeps them within 256 VGPRs.
@@ -656,9 +660,9 @@ extern "C" int tvllm_paged_decode(
         else if (group <= 2) TVLLM_DEC(2);
         else if (group <= 4) TVLLM_DEC(4);
         else if (group <= 8)
-            paged_decode_d128<T, 8, 1><<<int(grid), threads, 0, s>>>(args);
+            paged_decode_d128<T, 8, 1, kMaxWaves><<<int(grid), threads, 0, s>>>(args);
         else
-            paged_decode_d128<T, 16, 1><<<int(grid), threads, 0, s>>>(args);
+            paged_decode_d128<T, 16, 1, kMaxWaves><<<int(grid), threads, 0, s>>>(args);
 #undef TVLLM_DEC
         const int st = launch_status("paged_decode");
         if (st != TVLLM_OK || plan.grid <= 1) return st;

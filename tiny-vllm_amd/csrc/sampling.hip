@@ -63,33 +63,7 @@ __device__ void block_argmax(float& v, int64_t& idx) {
 template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
 argmax_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride,
-              int64_t* __restrict__ out) {
-    const T* row = logits + int64_t(blockIdx.x) * stride;
-    float best = -INFINITY;
-    int64_t bi = INT64_MAX;
-    if constexpr (VEC) {
-        const int64_t nvec = vocab / 8;
-        const U16x8* rv = reinterpret_cast<const U16x8*>(row);
-        for (int64_t c = threadIdx.x; c < nvec; c += kThreads) {
-            float x[8];
-            unpack8<T>(rv[c], x);
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (better(x[e], c * 8 + e, best, bi)) { best = x[e]; bi = c * 8 + e; }
-        }
-        for (int64_t i = nvec * 8 + threadIdx.x; i < vocab; i += kThreads) {
-            const float x = load_logit(row, i);
-            if (better(x, i, best, bi)) { best = x; bi = i; }
-        }
-    } else {
-        for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
-            const float x = load_logit(row, i);
-            if (better(x, i, best, bi)) { best = x; bi = i; }
-        }
-    }
-    block_argmax(best, bi);
-    if (threadIdx.x == 0) out[blockIdx.x] = bi;
-}
+              int64_t* __restrict__ out);
 
 // ------------------------------------------------------------ sampling ----
 
@@ -241,7 +215,30 @@ __device__ Cut radix_cut(const T* row, int64_t vocab, const RowCtx& ctx,
     return Cut{prefix, static_cast<int64_t>(iprefix), false};
 }
 
-template <typename T>
+// Per-thread running argmax over a row (16-byte vector loads when VEC).
+template <typename T, bool VEC>
+__device__ __forceinline__ void thread_argmax(const T* row, int64_t vocab, float& best,
+                                              int64_t& bi) {
+    int64_t tail = 0;
+    if constexpr (VEC) {
+        const int64_t nvec = vocab / 8;
+        const U16x8* rv = reinterpret_cast<const U16x8*>(row);
+        for (int64_t c = threadIdx.x; c < nvec; c += kThreads) {
+            float x[8];
+            unpack8<T>(rv[c], x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (better(x[e], c * 8 + e, best, bi)) { best = x[e]; bi = c * 8 + e; }
+        }
+        tail = nvec * 8;
+    }
+    for (int64_t i = tail + threadIdx.x; i < vocab; i += kThreads) {
+        const float x = load_logit(row, i);
+        if (better(x, i, best, bi)) { best = x; bi = i; }
+    }
+}
+
+template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
 sample_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride,
               const float* __restrict__ temperature, const int64_t* __restrict__ top_k,
@@ -253,10 +250,7 @@ sample_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride,
     // Row max (also the greedy answer).
     float best = -INFINITY;
     int64_t bi = INT64_MAX;
-    for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
-        const float x = load_logit(row, i);
-        if (better(x, i, best, bi)) { best = x; bi = i; }
-    }
+    thread_argmax<T, VEC>(row, vocab, best, bi);
     block_argmax(best, bi);
     const float temp = temperature[r];
     if (!(temp > 0.f)) {
@@ -319,6 +313,18 @@ sample_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride,
     if (threadIdx.x == 0) out[r] = bidx;
 }
 
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+argmax_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride,
+              int64_t* __restrict__ out) {
+    const T* row = logits + int64_t(blockIdx.x) * stride;
+    float best = -INFINITY;
+    int64_t bi = INT64_MAX;
+    thread_argmax<T, VEC>(row, vocab, best, bi);
+    block_argmax(best, bi);
+    if (threadIdx.x == 0) out[blockIdx.x] = bi;
+}
+
 }  // namespace
 }  // namespace tvllm
 
@@ -373,7 +379,16 @@ extern "C" int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
     hipStream_t s = as_hip(stream);
     return dispatch_float(dtype, [&]<int DT>() {
         using T = typename Elem<DT>::T;
-        sample_kernel<T><<<int(rows), kThreads, 0, s>>>(
+        const bool vec = sizeof(T) == 2 && row_stride % 8 == 0 && aligned16(logits);
+        if constexpr (sizeof(T) == 2) {
+            if (vec) {
+                sample_kernel<T, true><<<int(rows), kThreads, 0, s>>>(
+                    static_cast<const T*>(logits), vocab, row_stride, temperature, top_k,
+                    top_p, seeds, counters, out);
+                return launch_status("sample");
+            }
+        }
+        sample_kernel<T, false><<<int(rows), kThreads, 0, s>>>(
             static_cast<const T*>(logits), vocab, row_stride, temperature, top_k,
             top_p, seeds, counters, out);
         return launch_status("sample");
