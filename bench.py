@@ -333,6 +333,239 @@ def summarize_profile(directory: str, tail: int = 33) -> None:
             print(f"  {name}: {vals}")
 
 
+EAGER_OPS = False  # --eager: launch op-benchmark kernels directly (PMC passes)
+
+
+def _event_time(fn, iters: int) -> float:
+    """Mean device seconds per call of `fn`: `iters` calls captured in one
+    hipGraph (so Python launch overhead is not timed), replayed and timed
+    with HIP events on the replay stream. With --eager the calls are
+    launched directly (rocprofv3 counter passes see only such dispatches)."""
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    if EAGER_OPS:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            fn()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / 1e3 / iters
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / 1e3 / iters
+
+
+def _cpu_time(fn, reps: int = 5) -> float:
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def _hbm(bytes_: int, seconds: float) -> dict:
+    gbs = bytes_ / seconds / 1e9
+    return {"us": round(seconds * 1e6, 2), "bytes": bytes_, "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def op_c1(args) -> dict:
+    """C1: the paged-decode op alone at Qwen3-0.6B shapes (8 rows, 16Q/8KV
+    heads, D128, L ~ U[64,1024], 16-token pages from a 1024-page pool), plus
+    the 8B-shape variant (64 rows, 32Q/8KV, L=2048)."""
+    import torch
+
+    from oracle import attention as OA
+    from tinyvllm.kernels.paged_decode import decode_workspace_bytes, paged_decode_attention
+    from tinyvllm.paged_kv import PagedKVCache
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    device = torch.device("cuda", 0)
+    result = {}
+    for name, rows, hq, lengths_fn, pool in (
+            ("c1_qwen3-0.6b_bs8", 8, 16, lambda g: torch.randint(64, 1025, (8,), generator=g), 1024),
+            ("qwen3-8b_bs64_ctx2048", 64, 32, lambda g: torch.full((64,), 2048), 64 * 128)):
+        g = torch.Generator().manual_seed(0)
+        lengths = lengths_fn(g)
+        pages = [math.ceil(int(l) / 16) for l in lengths]
+        perm = torch.randperm(pool, generator=g)
+        blocks = perm[:sum(pages)]
+        offsets = torch.tensor([0] + list(torch.tensor(pages).cumsum(0).tolist()))
+        cache = PagedKVCache(num_layers=1, num_blocks=pool, block_size=16, num_kv_heads=8,
+                             head_dim=128, device="cpu", dtype=torch.bfloat16)
+        cache.key.normal_(generator=g)
+        cache.value.normal_(generator=g)
+        q = torch.randn(rows, hq, 128, generator=g).to(torch.bfloat16)
+        scale = 128 ** -0.5
+        gcache = PagedKVCache(num_layers=1, num_blocks=pool, block_size=16, num_kv_heads=8,
+                              head_dim=128, device=device, dtype=torch.bfloat16)
+        gcache.key.copy_(cache.key)
+        gcache.value.copy_(cache.value)
+        meta = SingleQueryMetadata(torch.arange(rows, device=device), blocks.to(device),
+                                   offsets.to(device), lengths.to(device),
+                                   int(lengths.max()))
+        ws = torch.empty(max(16, decode_workspace_bytes(rows, hq, 8, 128, int(lengths.max()),
+                                                        16)), dtype=torch.uint8, device=device)
+        gq, gout = q.to(device), torch.empty(rows, hq, 128, dtype=torch.bfloat16, device=device)
+        seconds = _event_time(lambda: paged_decode_attention(
+            gq, gcache, 0, meta, gout, scale=scale, workspace=ws), 200)
+        ref = torch.empty_like(q)
+        oracle_call = lambda: OA.decode_attention(  # noqa: E731
+            q, cache.key[0], cache.value[0], torch.arange(rows), blocks, offsets, lengths, 16,
+            scale, ref)
+        cpu = _cpu_time(oracle_call, reps=3)
+        err = (gout.cpu().float() - ref.float()).abs()
+        algorithmic = (int(lengths.sum()) * 8 * 128 * 4 + 2 * rows * hq * 128 * 2
+                       + 8 * sum(pages) + 8 * (3 * rows + 1))
+        result[name] = {**_hbm(algorithmic, seconds), "max_abs_err_vs_oracle":
+                        round(err.max().item(), 5),
+                        "cpu_oracle_us": round(cpu * 1e6, 1)}
+    return result
+
+
+def op_c2(args) -> dict:
+    """C2: the fused pointwise chain at Qwen3-0.6B shapes, 256 tokens: RMSNorm
+    (hidden 1024), add+RMSNorm, QK-norm + RoPE + slot-mapped KV write (one
+    kernel), SiLU*up (intermediate 3072); per kernel HBM rate."""
+    import torch
+
+    from oracle import pointwise as OP
+    from tinyvllm.kernels import pointwise as KP
+
+    device = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(0)
+    bf = torch.bfloat16
+    T, H, hq, hkv, d, inter, pool = 256, 1024, 16, 8, 128, 3072, 16384
+    x = torch.randn(T, H, generator=g).to(bf)
+    res = torch.randn(T, H, generator=g).to(bf)
+    w = (1 + 0.02 * torch.randn(H, generator=g)).to(bf)
+    qkv = torch.randn(T, (hq + 2 * hkv) * d, generator=g).to(bf)
+    qw = (1 + 0.02 * torch.randn(d, generator=g)).to(bf)
+    kw = (1 + 0.02 * torch.randn(d, generator=g)).to(bf)
+    pos = torch.randint(0, 2048, (T,), generator=g)
+    cos, sin = OP.rope_tables(pos, d, 1e6, bf)
+    slots = torch.randperm(pool, generator=g)[:T]
+    gu = torch.randn(T, 2 * inter, generator=g).to(bf)
+    G = lambda t: t.to(device)  # noqa: E731
+    gx, gres, gw, gqkv, gqw, gkw, gcos, gsin, gslots, ggu = map(
+        G, (x, res, w, qkv, qw, kw, cos, sin, slots, gu))
+    kc = torch.zeros(pool, hkv, d, dtype=bf, device=device)
+    vc = torch.zeros_like(kc)
+    q_v = gqkv[:, :hq * d].view(T, hq, d)
+    k_v = gqkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
+    v_v = gqkv[:, (hq + hkv) * d:].view(T, hkv, d)
+    runs = {
+        "rms_norm": (lambda: KP.rms_norm(gx, gw, 1e-6), T * H * 2 * 2 + H * 2),
+        "add_rms_norm": (lambda: KP.add_rms_norm(gx, gres, gw, 1e-6), T * H * 2 * 4 + H * 2),
+        "qk_norm_rope_kv_write": (
+            lambda: KP.qk_norm_rope_store(q_v, k_v, v_v, gqw, gkw, gcos, gsin, 1e-6, 1e-6,
+                                          kc, vc, gslots),
+            T * (hq + 2 * hkv) * d * 2 + T * hq * d * 2 + T * 2 * hkv * d * 2
+            + T * d * 2 + T * 8 + 2 * d * 2),
+        "silu_and_mul": (lambda: KP.silu_and_mul(ggu), T * inter * 2 * 3),
+    }
+    result = {}
+    total_s = total_b = 0
+    for name, (fn, nbytes) in runs.items():
+        s = _event_time(fn, 200)
+        result[name] = _hbm(nbytes, s)
+        total_s += s
+        total_b += nbytes
+    result["chain"] = _hbm(total_b, total_s)
+    # Parity of the chain on these inputs (bit-exact KV rows, bf16 tolerance).
+    q_ref, k_ref = OP.qk_norm_rope(qkv[:, :hq * d].view(T, hq, d),
+                                   qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d), qw, kw, cos, sin)
+    q_out, k_out = KP.qk_norm_rope_store(q_v, k_v, v_v, gqw, gkw, gcos, gsin, 1e-6, 1e-6,
+                                         kc, vc, gslots, key_out=True)
+    torch.cuda.synchronize()
+    result["parity"] = {
+        "rms_norm_max_abs": round((KP.rms_norm(gx, gw, 1e-6).cpu().float()
+                                   - OP.rms_norm(x, w).float()).abs().max().item(), 5),
+        "q_max_abs": round((q_out.cpu().float() - q_ref.float()).abs().max().item(), 5),
+        "k_max_abs": round((k_out.cpu().float() - k_ref.float()).abs().max().item(), 5),
+        "kv_write_bitexact": bool(torch.equal(kc.cpu()[slots], k_out.cpu())
+                                  and torch.equal(vc.cpu()[slots], v_v.cpu())),
+        "silu_max_abs": round((KP.silu_and_mul(ggu).cpu().float()
+                               - OP.silu_and_mul(gu).float()).abs().max().item(), 5),
+    }
+    cpu = _cpu_time(lambda: (OP.rms_norm(x, w), OP.add_rms_norm(x, res, w),
+                             OP.qk_norm_rope(qkv[:, :hq * d].view(T, hq, d),
+                                             qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d),
+                                             qw, kw, cos, sin),
+                             OP.silu_and_mul(gu)))
+    result["cpu_oracle_chain_us"] = round(cpu * 1e6, 1)
+    return result
+
+
+def op_prefill(args) -> dict:
+    """Chunked-prefill paged attention at the C4 chunk shape: 512-query chunks
+    of 2048-token prompts (the last chunk sees 2048 keys), Qwen3-8B heads
+    (32Q/8KV, D128), 4 items; MFMA roofline (flops of the causal region)."""
+    import torch
+
+    from oracle import attention as OA
+    from tinyvllm.kernels.paged_prefill import paged_prefill_attention
+    from tinyvllm.paged_kv import PagedKVCache
+    from tinyvllm.runtime.contracts import MultiQueryMetadata
+
+    device = torch.device("cuda", 0)
+    result = {}
+    for name, items, qlen, ctx in (("c4_chunk512_ctx2048_x4", 4, 512, 2048),
+                                   ("c4_chunk512_ctx512_x4", 4, 512, 512)):
+        hq, hkv, d, bs = 32, 8, 128, 16
+        g = torch.Generator().manual_seed(0)
+        pages = ctx // bs
+        pool = items * pages
+        cache = PagedKVCache(num_layers=1, num_blocks=pool, block_size=bs, num_kv_heads=hkv,
+                             head_dim=d, device=device, dtype=torch.bfloat16)
+        gen = torch.Generator(device=device).manual_seed(1)
+        cache.key.normal_(generator=gen)
+        cache.value.normal_(generator=gen)
+        blocks = torch.randperm(pool, generator=g)
+        meta = MultiQueryMetadata(
+            torch.arange(items + 1, device=device) * qlen, blocks.to(device),
+            torch.arange(items + 1, device=device) * pages,
+            torch.full((items,), ctx, device=device), qlen)
+        q = torch.randn(items * qlen, hq, d, dtype=torch.bfloat16, device=device)
+        out = torch.empty_like(q)
+        scale = d ** -0.5
+        seconds = _event_time(lambda: paged_prefill_attention(
+            q, cache, 0, meta, out, scale=scale), 50)
+        pairs = items * (qlen * (ctx - qlen) + qlen * (qlen + 1) // 2)
+        flops = 4 * hq * d * pairs
+        tflops = flops / seconds / 1e12
+        # Parity on the first item.
+        ref = torch.empty(qlen, hq, d, dtype=torch.bfloat16)
+        OA.prefill_attention(q[:qlen].cpu(), cache.key[0].cpu(), cache.value[0].cpu(),
+                             torch.tensor([0, qlen]), blocks[:pages], torch.tensor([0, pages]),
+                             torch.tensor([ctx]), bs, scale, ref)
+        err = (out[:qlen].cpu().float() - ref.float()).abs().max().item()
+        result[name] = {"us": round(seconds * 1e6, 1), "flops": flops,
+                        "TFLOP/s": round(tflops, 1), "frac_bf16_mfma": round(tflops / 2500, 4),
+                        "max_abs_err_vs_oracle_item0": round(err, 5)}
+    return result
+
+
+OPS = {"c1": op_c1, "c2": op_c2, "prefill": op_prefill}
+
+
 E2E = {
     # name: (model, requests, prompt length(s), new tokens, shared prefix, arrivals)
     "c3": dict(model="qwen3-0.6b", requests=32, prompt=512, new=256),
@@ -424,8 +657,10 @@ def main() -> None:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["decode", *E2E], default="decode",
+    ap.add_argument("--workload", choices=["decode", *E2E, *OPS], default="decode",
                     help="decode (the metric) or an end-to-end SURVEY config")
+    ap.add_argument("--eager", action="store_true",
+                    help="op workloads: launch kernels directly instead of graph replay")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the decode-attention kernel (for PMC passes)")
     ap.add_argument("--summarize-profile", metavar="DIR",
@@ -442,6 +677,15 @@ def main() -> None:
 
     if args.kernel_only:
         kernel_only(args)
+        return
+    if args.workload in OPS:
+        import torch
+
+        global EAGER_OPS
+        EAGER_OPS = args.eager
+        torch.cuda.set_device(0)
+        print(json.dumps({"workload": args.workload, "dtype": "bf16",
+                          "data": "synthetic, seeded", **OPS[args.workload](args)}), flush=True)
         return
     if args.workload != "decode":
         end_to_end(args.workload, args)

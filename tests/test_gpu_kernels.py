@@ -150,15 +150,25 @@ def test_decode_fp16(device):
 
 # ------------------------------------------------------------- prefill attn --
 
-@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 8)])
-def test_prefill_chunks_with_history(device, heads, kv_heads):
+PREFILL_ITEMS = {
+    # (context, query_len): fresh prompt, chunk with history, short tail, 1-token;
+    # the largest query length selects 64, 128 or 256 queries per workgroup.
+    "q512": [(70, 70), (600, 128), (513, 1), (300, 45), (1024, 512)],
+    "q100": [(100, 100), (700, 99), (65, 1), (129, 64)],
+    "q50": [(50, 50), (333, 17), (64, 64), (1, 1)],
+}
+
+
+@pytest.mark.parametrize("heads,kv_heads,items,bs", [
+    (16, 8, "q512", 16), (32, 8, "q512", 16), (32, 8, "q100", 16), (64, 8, "q50", 16),
+    (32, 4, "q100", 8), (16, 16, "q50", 32)])
+def test_prefill_chunks_with_history(device, heads, kv_heads, items, bs):
     from tinyvllm.kernels.paged_prefill import paged_prefill_attention
     from tinyvllm.runtime.contracts import MultiQueryMetadata
 
     g = torch.Generator().manual_seed(31)
-    d, bs, pool = 128, 16, 512
-    # (context, query_len): fresh prompt, chunk with history, short tail, 1-token
-    items = [(70, 70), (600, 128), (513, 1), (300, 45), (1024, 512)]
+    d, pool = 128, 8192 // bs
+    items = PREFILL_ITEMS[items]
     k = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
     v = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
     perm = torch.randperm(pool, generator=g).tolist()

@@ -41,6 +41,10 @@ inline hipStream_t as_hip(tvllm_stream_t s) {
     return reinterpret_cast<hipStream_t>(s);
 }
 
+inline bool aligned8(const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 7u) == 0;
+}
+
 inline bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
