@@ -8,30 +8,32 @@
 // seeing tokens t <= context_len - query_len + j.
 //
 // MI355X design (head_dim 128): one workgroup of W waves per (item, query
-// head, tile of 16*QB*W queries); each wave owns QB blocks of 16 queries.
-// K/V tiles of 64 tokens are gathered through the block table into LDS once
-// per workgroup, double-buffered: the next tile's global loads are issued
-// into registers before the current tile's MFMA work and written to the
-// other LDS buffer after it, so there is one barrier per tile.
-//  * S^T = K Q^T with MFMA 16x16x32 (A = K rows from LDS, shared by the
-//    wave's QB query blocks; B = Q rows held in registers). A lane's score
-//    accumulator is (4 tokens x its own query) - exactly the B-operand
-//    layout of the transposed product below, so P never moves.
-//  * O^T += V^T P^T with MFMA 16x16x32: A = V^T read from an LDS copy that
-//    staging stores transposed (dims x tokens, 8-byte writes of 4 tokens),
-//    B = the lane's probabilities rounded to the storage type. The O^T
-//    accumulator of a lane belongs to its own query, so the online-softmax
-//    rescale and the final 1/l need no cross-lane traffic.
-//  * online softmax in base 2 (v_exp_f32), one running (max, sum) per query,
-//    raised lazily (kSlack) so most tiles skip the accumulator rescale;
-//    key tiles past a wave's last query are skipped (causal), and tiles
-//    entirely below its first query skip the mask.
+// head, tile of 32*W queries); each wave owns 32 queries. The products use
+// the 32x32x16 MFMA, which issues twice the work per cycle of the 16x16x32
+// form on gfx950.
+//  * K/V tiles of 64 tokens are gathered through the block table into LDS
+//    once per workgroup, double-buffered: tile i+2's global loads are in
+//    flight and tile i+1 waits in registers while tile i is computed, so a
+//    tile costs one barrier. Block ids are fetched a tile ahead of the K/V
+//    loads that use them.
+//  * S^T = K Q^T (A = 32 K rows from LDS, B = the wave's 32 queries held in
+//    registers). A lane's score accumulator covers its own query and 16
+//    tokens - exactly the k values the transposed product below needs, so P
+//    never moves between lanes.
+//  * O^T += V^T P^T (A = V^T from an LDS copy that staging stores transposed,
+//    with the tokens of each 16-token step ordered the way the MFMA k index
+//    visits them; B = the lane's probabilities rounded to the storage type).
+//    The O^T accumulator of a lane belongs to its own query: the softmax
+//    rescale and the final 1/l are lane-local.
+//  * online softmax in base 2 (v_exp_f32) with one running (max, sum) per
+//    query, raised lazily (kSlack) so most tiles skip the rescale; key tiles
+//    past a wave's last query are skipped (causal) and tiles entirely below
+//    its first query skip the mask.
 // Work order: block ids are spread over the 8 XCDs so the workgroups of one
 // (item, KV head) share an XCD's L2, and the causal tiles with the most keys
 // start first.
 #include "common.h"
 
-#include <cstdio>
 #include <cstdlib>
 #include <type_traits>
 
@@ -40,28 +42,40 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// D[32x32] += A[32x16] B[16x32]. Lane l: A row l%32 and B column l%32 with
+// k = 8*(l/32)..+7; D column l%32, rows 8*(v/4) + 4*(l/32) + v%4 for v < 16.
 template <typename T>
-__device__ __forceinline__ f32x4 mfma(const U16x8& a, const U16x8& b, f32x4 c) {
+__device__ __forceinline__ f32x16 mfma32(const U16x8& a, const U16x8& b, f32x16 c) {
     if constexpr (std::is_same_v<T, __bf16>) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
-            0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
     } else {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
-            0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
     }
 }
 
 constexpr int D = 128;
 constexpr int BK = 64;          // tokens per KV tile
-constexpr int K_LD = D + 8;     // K tile row stride (elements), breaks bank aliasing
-constexpr int V_LD = BK + 4;    // V^T tile row stride (elements)
+constexpr int K_LD = D + 8;     // K tile row stride (elements): 68 dwords
+constexpr int V_LD = BK + 8;    // V^T tile row stride (elements): 36 dwords
 constexpr int K_TILE = BK * K_LD;
 constexpr int V_TILE = D * V_LD;
 constexpr float kLog2e = 1.4426950408889634f;
+
+// V^T rows order each 16-token P.V step as the MFMA k index visits it:
+// tile token 16s + 8jj + 4h + i sits at 16s + 8h + 4jj + i, so the eight k
+// values of a lane in half h are one 16-byte read. First slot of quad tq:
+__device__ __forceinline__ int vt_pos(int tq) {
+    return 16 * (tq >> 2) + 8 * (tq & 1) + 4 * ((tq >> 1) & 1);
+}
+
+// Running maxima are only raised when a tile's maximum exceeds them by more
+// than this (log2 units): probabilities then stay below 2^kSlack, and most
+// tiles skip the rescale of the output accumulators.
+constexpr float kSlack = 8.f;
 
 template <typename T>
 struct PrefillArgs {
@@ -79,38 +93,24 @@ struct PrefillArgs {
     float scale_log2;
 };
 
-// Running maxima are only raised when a tile's maximum exceeds them by more
-// than this (log2 units): probabilities then stay below 2^kSlack, and most
-// tiles skip the rescale of the output accumulators.
-constexpr float kSlack = 8.f;
-
 __device__ __forceinline__ float as_f(uint32_t x) { return __uint_as_float(x); }
 __device__ __forceinline__ uint32_t as_u(float x) { return __float_as_uint(x); }
 
-// Reductions over the four lanes col, col+16, col+32, col+48 (the quads that
-// share one query), with the gfx950 row-swap permutes instead of LDS shuffles.
-__device__ __forceinline__ float quad_max(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(as_u(x), as_u(x), false, false);
-    x = fmaxf(as_f(a[0]), as_f(a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(as_u(x), as_u(x), false, false);
-    return fmaxf(as_f(b[0]), as_f(b[1]));
+// Lanes l and l+32 hold the same query: combine them with one row swap.
+__device__ __forceinline__ float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(as_u(x), as_u(x), false, false);
+    return fmaxf(as_f(r[0]), as_f(r[1]));
 }
-__device__ __forceinline__ float quad_sum(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(as_u(x), as_u(x), false, false);
-    x = as_f(a[0]) + as_f(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(as_u(x), as_u(x), false, false);
-    return as_f(b[0]) + as_f(b[1]);
+__device__ __forceinline__ float pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(as_u(x), as_u(x), false, false);
+    return as_f(r[0]) + as_f(r[1]);
 }
 
-__device__ __forceinline__ uint32_t half16(const U16x8& v, int e) {
-    return (v.w[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-}
-
-template <typename T, int QB, int W>
-__global__ void __launch_bounds__(64 * W)
+template <typename T, int W>
+__global__ void __launch_bounds__(64 * W, 8 / W)  // two waves per SIMD
 paged_prefill_d128(PrefillArgs<T> a) {
     constexpr int NTH = 64 * W;
-    constexpr int BQ = 16 * QB * W;      // queries per workgroup
+    constexpr int BQ = 32 * W;           // queries per workgroup
     constexpr int JOBS = 2 * 16 * 16;    // (K|V) x 16 token quads x 16 pieces
     static_assert(JOBS % NTH == 0, "staging jobs must divide the threads");
     constexpr int JPT = JOBS / NTH;
@@ -120,8 +120,8 @@ paged_prefill_d128(PrefillArgs<T> a) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int quad = lane >> 4;
-    const int col = lane & 15;
+    const int col = lane & 31;
+    const int half = lane >> 5;
 
     // XCD-aware order: hardware deals block ids round-robin over 8 XCDs;
     // give each XCD a contiguous range of logical work.
@@ -142,38 +142,28 @@ paged_prefill_d128(PrefillArgs<T> a) {
     const int64_t table = a.block_offsets[item];
     const int64_t kv_end = min(ctx, first_pos + min(q_len - 1, q0 + BQ - 1) + 1);
 
-    // This wave's queries: wq0 + 16b + col for block b.
-    const int64_t wq0 = q0 + int64_t(wave) * 16 * QB;
+    // This wave's queries: wq0 + col.
+    const int64_t wq0 = q0 + int64_t(wave) * 32;
     const bool wave_active = wq0 < q_len;
-    const int64_t wave_kv_end = min(kv_end, first_pos + min(q_len - 1, wq0 + 16 * QB - 1) + 1);
+    const int64_t wave_kv_end = min(kv_end, first_pos + min(q_len - 1, wq0 + 31) + 1);
     const int64_t wave_first_pos = first_pos + wq0;
+    const int64_t qi_lane = min(wq0 + col, q_len - 1);
+    const int64_t my_pos = first_pos + qi_lane;
 
-    U16x8 qb[QB][4];
-    int64_t my_pos[QB];
+    U16x8 qv[8];  // B operand of k-step c: dims 16c + 8*half .. +7
+    {
+        const T* qrow = a.q + (q_begin + qi_lane) * a.qts + h * a.qhs + 8 * half;
 #pragma unroll
-    for (int b = 0; b < QB; ++b) {
-        const int64_t qi = min(wq0 + 16 * b + col, q_len - 1);
-        my_pos[b] = first_pos + qi;
-        const T* qrow = a.q + (q_begin + qi) * a.qts + h * a.qhs + quad * 8;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) qb[b][c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
+        for (int c = 0; c < 8; ++c) qv[c] = *reinterpret_cast<const U16x8*>(qrow + 16 * c);
     }
 
-    f32x4 o[QB][8];  // O^T: lane = (dims 16n + 4quad + i, query col)
+    f32x16 o[4];  // O^T: lane = (dims 32n + 8g + 4*half + i, query col)
 #pragma unroll
-    for (int b = 0; b < QB; ++b)
-#pragma unroll
-        for (int n = 0; n < 8; ++n) o[b][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run[QB], l_run[QB];
-#pragma unroll
-    for (int b = 0; b < QB; ++b) {
-        m_run[b] = -INFINITY;
-        l_run[b] = 0.f;
-    }
+    for (int n = 0; n < 4; ++n) o[n] = f32x16{};
+    float m_run = -INFINITY, l_run = 0.f;
 
-    // Staging: job = (kind, piece, token quad); 4 tokens x 16 bytes each.
+    // Staging: job = (K|V, piece, token quad); 4 tokens x 16 bytes each.
     const int bs = a.block_size;
-    U16x8 stage[JPT][4];
     auto job_coords = [&](int r, bool& is_v, int& tq, int& piece) {
         const int job = tid + r * NTH;
         is_v = job >> 8;
@@ -182,53 +172,60 @@ paged_prefill_d128(PrefillArgs<T> a) {
         tq = is_v ? (job & 15) : ((job >> 4) & 15);
         piece = is_v ? ((job >> 4) & 15) : (job & 15);
     };
-    // Block ids are fetched one tile ahead of the K/V loads that use them, so
-    // the two dependent global loads never sit back to back on the critical path.
-    auto load_ids = [&](int64_t t0, int64_t (&ids)[JPT][4]) {
+    // Token positions fit in 32 bits (contexts < 2^31) and slots in 32 bits
+    // (checked on the host); the element offset of a slot is formed in 64 bits.
+    const int end1 = int(kv_end) - 1;
+    const uint32_t slot_elems = uint32_t(a.kv_heads) * D;
+    // Fast path (power-of-two pages of >= 4 tokens): a job's 4 tokens share a
+    // page, so one block id serves all four.
+    const bool quad_pages = a.block_shift >= 2;
+    auto load_ids = [&](int t0, uint32_t (&ids)[JPT][4]) {
 #pragma unroll
         for (int r = 0; r < JPT; ++r) {
             bool is_v;
             int tq, piece;
             job_coords(r, is_v, tq, piece);
+            if (quad_pages) {
+                ids[r][0] = uint32_t(a.blocks[table + (min(t0 + 4 * tq, end1) >> a.block_shift)]);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int64_t t = min(t0 + 4 * tq + e, kv_end - 1);
-                const int64_t page = a.block_shift >= 0 ? (t >> a.block_shift) : t / bs;
-                ids[r][e] = a.blocks[table + page];
+                for (int e = 0; e < 4; ++e)
+                    ids[r][e] = uint32_t(a.blocks[table + min(t0 + 4 * tq + e, end1) / bs]);
             }
         }
     };
-    auto load_tile = [&](int64_t t0, const int64_t (&ids)[JPT][4]) {
+    auto load_tile = [&](int t0, const uint32_t (&ids)[JPT][4], U16x8 (&stage)[JPT][4]) {
 #pragma unroll
         for (int r = 0; r < JPT; ++r) {
             bool is_v;
             int tq, piece;
             job_coords(r, is_v, tq, piece);
-            const T* src = is_v ? a.v : a.k;
+            const T* src = (is_v ? a.v : a.k) + kvh * D + piece * 8;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int64_t t = min(t0 + 4 * tq + e, kv_end - 1);
-                const int64_t in_page = a.block_shift >= 0 ? (t & (bs - 1)) : t % bs;
-                const int64_t slot = ids[r][e] * bs + in_page;
-                stage[r][e] = *reinterpret_cast<const U16x8*>(
-                    src + (slot * a.kv_heads + kvh) * D + piece * 8);
+                const int t = min(t0 + 4 * tq + e, end1);
+                const uint32_t slot = quad_pages ? ids[r][0] * uint32_t(bs) + uint32_t(t & (bs - 1))
+                                                 : ids[r][e] * uint32_t(bs) + uint32_t(t % bs);
+                stage[r][e] = *reinterpret_cast<const U16x8*>(src + uint64_t(slot) * slot_elems);
             }
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](int buf, const U16x8 (&stage)[JPT][4]) {
 #pragma unroll
         for (int r = 0; r < JPT; ++r) {
             bool is_v;
             int tq, piece;
             job_coords(r, is_v, tq, piece);
             if (is_v) {
-                // V^T: dim row (piece*8 + dd), tokens 4tq..4tq+3 -> one 8-byte write.
+                // V^T: dim row (piece*8 + dd), the quad's 4 tokens -> one 8-byte write;
+                // v_perm picks the low (even dd) or high (odd dd) halves of two words.
 #pragma unroll
                 for (int dd = 0; dd < 8; ++dd) {
+                    const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
                     uint2 w;
-                    w.x = half16(stage[r][0], dd) | (half16(stage[r][1], dd) << 16);
-                    w.y = half16(stage[r][2], dd) | (half16(stage[r][3], dd) << 16);
-                    *reinterpret_cast<uint2*>(&vt[buf][(piece * 8 + dd) * V_LD + 4 * tq]) = w;
+                    w.x = __builtin_amdgcn_perm(stage[r][1].w[dd >> 1], stage[r][0].w[dd >> 1], sel);
+                    w.y = __builtin_amdgcn_perm(stage[r][3].w[dd >> 1], stage[r][2].w[dd >> 1], sel);
+                    *reinterpret_cast<uint2*>(&vt[buf][(piece * 8 + dd) * V_LD + vt_pos(tq)]) = w;
                 }
             } else {
 #pragma unroll
@@ -239,134 +236,124 @@ paged_prefill_d128(PrefillArgs<T> a) {
         }
     };
 
-    int64_t ids_next[JPT][4], ids_after[JPT][4];
-    load_ids(0, ids_next);
-    load_tile(0, ids_next);
-    if (BK < kv_end) load_ids(BK, ids_next);
-    store_tile(0);
-    __syncthreads();
-    int buf = 0;
-    for (int64_t t0 = 0; t0 < kv_end; t0 += BK, buf ^= 1) {
-        const bool has_next = t0 + BK < kv_end;
-        if (has_next) {
-            load_tile(t0 + BK, ids_next);
-            if (t0 + 2 * BK < kv_end) load_ids(t0 + 2 * BK, ids_after);
+    auto compute = [&](int64_t t0, int buf) {
+        if (!wave_active || t0 >= wave_kv_end) return;
+        const uint16_t* kt = ks[buf];
+        const uint16_t* vtt = vt[buf];
+        // ---- S^T: s[tb][v] = token t0 + 32tb + 8(v/4) + 4*half + v%4, query col
+        f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                const U16x8 kk = *reinterpret_cast<const U16x8*>(
+                    &kt[(32 * tb + col) * K_LD + 16 * c + 8 * half]);
+                s[tb] = mfma32<T>(kk, qv[c], s[tb]);
+            }
+        if (t0 + BK - 1 > wave_first_pos) {  // tile crosses the diagonal
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t t = t0 + 32 * tb + 8 * (v >> 2) + 4 * half + (v & 3);
+                    if (t > my_pos) s[tb][v] = -INFINITY;
+                }
         }
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) cmax = fmaxf(cmax, s[tb][v]);
+        const float cm = pair_max(cmax) * a.scale_log2;  // scale > 0
+        const bool grow = cm > m_run + kSlack;  // also: first finite max
+        float alpha = 1.f;
+        if (grow) {
+            alpha = __builtin_amdgcn_exp2f(m_run - cm);
+            m_run = cm;
+        }
+        if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform
+            l_run *= alpha;
+#pragma unroll
+            for (int n = 0; n < 4; ++n) o[n] *= alpha;
+        }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float psum = 0.f;
+        U16x8 pb[4];  // k-step st: tokens 16st + 8jj + 4*half + i at k = 4jj + i
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            float p[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[tb][v], a.scale_log2, -m_use));
+                psum += p[v];
+            }
+#pragma unroll
+            for (int sh = 0; sh < 2; ++sh) {
+                U16x8& w = pb[2 * tb + sh];
+                w.w[0] = pack2<T>(p[8 * sh + 0], p[8 * sh + 1]);
+                w.w[1] = pack2<T>(p[8 * sh + 2], p[8 * sh + 3]);
+                w.w[2] = pack2<T>(p[8 * sh + 4], p[8 * sh + 5]);
+                w.w[3] = pack2<T>(p[8 * sh + 6], p[8 * sh + 7]);
+            }
+        }
+        l_run += psum;
+        // ---- O^T += V^T P^T over four 16-token steps.
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const U16x8 va = *reinterpret_cast<const U16x8*>(
+                    &vtt[(32 * n + col) * V_LD + 16 * st + 8 * half]);
+                o[n] = mfma32<T>(va, pb[st], o[n]);
+            }
+    };
 
-        if (wave_active && t0 < wave_kv_end) {
-            const uint16_t* kt = ks[buf];
-            const uint16_t* vtt = vt[buf];
-            // ---- S^T tiles: s[b][j][i] = token t0 + 16j + 4quad + i, query (b, col)
-            float s[QB][4][4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                f32x4 d[QB];
-#pragma unroll
-                for (int b = 0; b < QB; ++b) d[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const U16x8 kk = *reinterpret_cast<const U16x8*>(
-                        &kt[(16 * j + col) * K_LD + c * 32 + quad * 8]);
-#pragma unroll
-                    for (int b = 0; b < QB; ++b) d[b] = mfma<T>(kk, qb[b][c], d[b]);
-                }
-#pragma unroll
-                for (int b = 0; b < QB; ++b)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) s[b][j][i] = d[b][i];
-            }
-            if (t0 + BK - 1 > wave_first_pos) {  // tile crosses the diagonal
-#pragma unroll
-                for (int b = 0; b < QB; ++b)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int64_t t = t0 + 16 * j + 4 * quad + i;
-                            if (t > my_pos[b]) s[b][j][i] = -INFINITY;
-                        }
-            }
-            U16x8 pb[QB][2];
-#pragma unroll
-            for (int b = 0; b < QB; ++b) {
-                float cmax = -INFINITY;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[b][j][i]);
-                const float cm = quad_max(cmax) * a.scale_log2;  // scale > 0
-                const bool grow = cm > m_run[b] + kSlack;  // also: first finite max
-                float alpha = 1.f;
-                if (grow) {
-                    alpha = __builtin_amdgcn_exp2f(m_run[b] - cm);
-                    m_run[b] = cm;
-                }
-                if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform
-                    l_run[b] *= alpha;
-#pragma unroll
-                    for (int n = 0; n < 8; ++n) o[b][n] *= alpha;
-                }
-                const float m_use = m_run[b] == -INFINITY ? 0.f : m_run[b];
-                float psum = 0.f;
-                float pf[4][4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        pf[j][i] = __builtin_amdgcn_exp2f(
-                            __builtin_fmaf(s[b][j][i], a.scale_log2, -m_use));
-                        psum += pf[j][i];
-                    }
-                l_run[b] += psum;
-#pragma unroll
-                for (int st = 0; st < 2; ++st) {
-                    const int ja = 2 * st, jb = 2 * st + 1;
-                    pb[b][st].w[0] = pack2<T>(pf[ja][0], pf[ja][1]);
-                    pb[b][st].w[1] = pack2<T>(pf[ja][2], pf[ja][3]);
-                    pb[b][st].w[2] = pack2<T>(pf[jb][0], pf[jb][1]);
-                    pb[b][st].w[3] = pack2<T>(pf[jb][2], pf[jb][3]);
-                }
-            }
-            // ---- O^T += V^T P^T over two 32-token steps.
-#pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const int ja = 2 * st, jb = 2 * st + 1;
-#pragma unroll
-                for (int n = 0; n < 8; ++n) {
-                    const uint16_t* vrow = &vtt[(16 * n + col) * V_LD];
-                    U16x8 va;
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * ja + 4 * quad);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * jb + 4 * quad);
-                    va.w[0] = lo.x; va.w[1] = lo.y; va.w[2] = hi.x; va.w[3] = hi.y;
-#pragma unroll
-                    for (int b = 0; b < QB; ++b) o[b][n] = mfma<T>(va, pb[b][st], o[b][n]);
-                }
-            }
+    // Two staging register sets alternate: while tile i is computed from LDS,
+    // tile i+1 sits loaded in registers (stored to the other LDS buffer after
+    // the compute) and tile i+2's loads are already in flight.
+    const int ntiles = int((kv_end + BK - 1) / BK);
+    U16x8 st_a[JPT][4], st_b[JPT][4];
+    uint32_t id_a[JPT][4], id_b[JPT][4];
+    load_ids(0, id_a);
+    load_tile(0, id_a, st_a);
+    if (ntiles > 1) {
+        load_ids(BK, id_b);
+        load_tile(BK, id_b, st_b);
+    }
+    if (ntiles > 2) load_ids(2 * BK, id_a);
+    store_tile(0, st_a);
+    __syncthreads();
+    // step(i): `held` has tile i+1, `spare` is free, `ids` are tile i+2's.
+    auto step = [&](int i, const U16x8 (&held)[JPT][4], U16x8 (&spare)[JPT][4],
+                    const uint32_t (&ids)[JPT][4], uint32_t (&ids_out)[JPT][4]) {
+        if (i + 2 < ntiles) {
+            load_tile((i + 2) * BK, ids, spare);
+            if (i + 3 < ntiles) load_ids((i + 3) * BK, ids_out);
         }
-        if (has_next) store_tile(buf ^ 1);
+        compute(int64_t(i) * BK, i & 1);
+        if (i + 1 < ntiles) store_tile((i + 1) & 1, held);
         __syncthreads();
-#pragma unroll
-        for (int r = 0; r < JPT; ++r)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ids_next[r][e] = ids_after[r][e];
+    };
+    for (int i = 0; i < ntiles; i += 2) {
+        step(i, st_b, st_a, id_a, id_b);
+        if (i + 1 < ntiles) step(i + 1, st_a, st_b, id_b, id_a);
     }
     if (!wave_active) return;
 
+    const float l = pair_sum(l_run);
+    const int64_t qi = wq0 + col;
+    if (qi >= q_len) return;
+    const float inv = 1.f / l;
+    T* orow = a.out + (q_begin + qi) * a.ots + h * a.ohs + 4 * half;
 #pragma unroll
-    for (int b = 0; b < QB; ++b) {
-        const float l = quad_sum(l_run[b]);
-        const int64_t qi = wq0 + 16 * b + col;
-        if (qi >= q_len) continue;
-        const float inv = 1.f / l;
-        T* orow = a.out + (q_begin + qi) * a.ots + h * a.ohs + 4 * quad;
+    for (int n = 0; n < 4; ++n)
 #pragma unroll
-        for (int n = 0; n < 8; ++n) {
+        for (int g = 0; g < 4; ++g) {
             uint2 w;
-            w.x = pack2<T>(o[b][n][0] * inv, o[b][n][1] * inv);
-            w.y = pack2<T>(o[b][n][2] * inv, o[b][n][3] * inv);
-            *reinterpret_cast<uint2*>(orow + 16 * n) = w;
+            w.x = pack2<T>(o[n][4 * g + 0] * inv, o[n][4 * g + 1] * inv);
+            w.y = pack2<T>(o[n][4 * g + 2] * inv, o[n][4 * g + 3] * inv);
+            *reinterpret_cast<uint2*>(orow + 32 * n + 8 * g) = w;
         }
-    }
 }
 
 }  // namespace
@@ -387,6 +374,7 @@ extern "C" int tvllm_paged_prefill(
                 "paged_prefill: invalid GQA geometry");
     TVLLM_CHECK(block_size > 0 && num_slots % block_size == 0,
                 "paged_prefill: invalid block geometry");
+    TVLLM_CHECK(num_slots <= INT32_MAX, "paged_prefill: at most 2^31-1 cache slots");
     TVLLM_CHECK(num_items >= 0 && max_query_len >= 0,
                 "paged_prefill: negative sizes");
     TVLLM_CHECK(scale > 0.f && scale < INFINITY, "paged_prefill: scale must be positive");
@@ -399,22 +387,15 @@ extern "C" int tvllm_paged_prefill(
                 "paged_prefill: Q and caches must be 16-byte aligned rows");
     TVLLM_CHECK(out_token_stride % 4 == 0 && out_head_stride % 4 == 0 && aligned8(out),
                 "paged_prefill: output rows must be 8-byte aligned");
-    // Queries per wave: 16*QB; a workgroup of W waves covers 16*QB*W queries.
-    // Eight waves per workgroup (two or three per SIMD) keep the MFMA pipes
-    // fed while other waves run their softmax; 4-wave shapes measured slower.
-    int qb = max_query_len > 128 ? 2 : 1;
-    int waves = 8;
+    // 32 queries per wave. Eight waves per workgroup (two per SIMD) keep the
+    // MFMA pipes fed while the other wave runs its softmax; chunks of at most
+    // 128 queries use four-wave workgroups so that more of them run at once.
+    int waves = max_query_len > 128 ? 8 : 4;
     if (const char* env = std::getenv("TVLLM_PREFILL_TUNING")) {
-        // Measurement override "qb,waves": one of 1,4 2,4 4,4 1,8 2,8.
-        int eq = 0, ew = 0;
-        if (std::sscanf(env, "%d,%d", &eq, &ew) == 2 &&
-            ((ew == 4 && (eq == 1 || eq == 2 || eq == 4)) ||
-             (ew == 8 && (eq == 1 || eq == 2)))) {
-            qb = eq;
-            waves = ew;
-        }
+        const int ew = std::atoi(env);  // measurement override: 4 or 8 waves
+        if (ew == 4 || ew == 8) waves = ew;
     }
-    const int64_t bq = 16 * qb * waves;
+    const int64_t bq = 32 * waves;
     const int64_t q_tiles = (max_query_len + bq - 1) / bq;
     const int64_t grid = num_items * num_heads * q_tiles;
     TVLLM_CHECK(grid <= INT32_MAX, "paged_prefill: grid too large");
@@ -442,16 +423,8 @@ extern "C" int tvllm_paged_prefill(
         args.scale_log2 = scale * kLog2e;
         args.block_shift = (block_size & (block_size - 1)) == 0
                                ? __builtin_ctzll(uint64_t(block_size)) : -1;
-        if (waves == 8) {
-            if (qb == 2) paged_prefill_d128<T, 2, 8><<<int(grid), 512, 0, s>>>(args);
-            else paged_prefill_d128<T, 1, 8><<<int(grid), 512, 0, s>>>(args);
-        } else if (qb == 4) {
-            paged_prefill_d128<T, 4, 4><<<int(grid), 256, 0, s>>>(args);
-        } else if (qb == 2) {
-            paged_prefill_d128<T, 2, 4><<<int(grid), 256, 0, s>>>(args);
-        } else {
-            paged_prefill_d128<T, 1, 4><<<int(grid), 256, 0, s>>>(args);
-        }
+        if (waves == 8) paged_prefill_d128<T, 8><<<int(grid), 512, 0, s>>>(args);
+        else paged_prefill_d128<T, 4><<<int(grid), 256, 0, s>>>(args);
         return launch_status("paged_prefill");
     });
 }
