@@ -161,13 +161,13 @@ PREFILL_ITEMS = {
 
 @pytest.mark.parametrize("heads,kv_heads,items,bs", [
     (16, 8, "q512", 16), (32, 8, "q512", 16), (32, 8, "q100", 16), (64, 8, "q50", 16),
-    (32, 4, "q100", 8), (16, 16, "q50", 32)])
+    (32, 4, "q100", 8), (16, 16, "q50", 32), (32, 8, "q512", 12), (16, 8, "q100", 2)])
 def test_prefill_chunks_with_history(device, heads, kv_heads, items, bs):
     from tinyvllm.kernels.paged_prefill import paged_prefill_attention
     from tinyvllm.runtime.contracts import MultiQueryMetadata
 
     g = torch.Generator().manual_seed(31)
-    d, pool = 128, 8192 // bs
+    d, pool = 128, 12288 // bs
     items = PREFILL_ITEMS[items]
     k = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
     v = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)

@@ -106,10 +106,13 @@ __device__ __forceinline__ uint16_t bits_of(float x) {
     return b;
 }
 
+// Two floats rounded (nearest-even) into one word; a single v_cvt_pk_* on gfx950.
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(bits_of<T>(lo)) |
-           (static_cast<uint32_t>(bits_of<T>(hi)) << 16);
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef T t2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, t2_t));
 }
 
 template <typename T>

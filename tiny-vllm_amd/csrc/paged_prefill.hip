@@ -106,7 +106,7 @@ __device__ __forceinline__ float pair_sum(float x) {
     return as_f(r[0]) + as_f(r[1]);
 }
 
-template <typename T, int W>
+template <typename T, int W, bool QUAD>
 __global__ void __launch_bounds__(64 * W, 8 / W)  // two waves per SIMD
 paged_prefill_d128(PrefillArgs<T> a) {
     constexpr int NTH = 64 * W;
@@ -176,16 +176,28 @@ paged_prefill_d128(PrefillArgs<T> a) {
     // (checked on the host); the element offset of a slot is formed in 64 bits.
     const int end1 = int(kv_end) - 1;
     const uint32_t slot_elems = uint32_t(a.kv_heads) * D;
-    // Fast path (power-of-two pages of >= 4 tokens): a job's 4 tokens share a
-    // page, so one block id serves all four.
-    const bool quad_pages = a.block_shift >= 2;
-    auto load_ids = [&](int t0, uint32_t (&ids)[JPT][4]) {
+    // QUAD (power-of-two pages of >= 4 tokens): a job's 4 tokens share a
+    // page, so one block id serves all four. A template parameter, not a
+    // branch: two load paths in the loop would make the wait-count pass
+    // treat the prefetch registers as possibly pending and stall on them.
+    constexpr bool quad_pages = QUAD;
+    // Staging is branch-free: tiles past the end (or before the start, in the
+    // prologue) load clamped, valid rows and store them into a buffer nobody
+    // reads again, so every load is consumed on every path and the wait-count
+    // pass never has to assume a prefetch register is still in flight.
+    // Staging runs ahead of the math: at iteration i the K rows of tile i+1
+    // (for S(i+1)) and the V rows of tile i (for P.V) are in LDS, and this
+    // iteration writes K(i+2) and V(i+1) from registers loaded during the
+    // previous one. `lead` is that distance for the job's kind.
+    auto lead_of = [](bool is_v) { return is_v ? 1 : 2; };
+    auto load_ids = [&](int tile_base, uint32_t (&ids)[JPT][4]) {
 #pragma unroll
         for (int r = 0; r < JPT; ++r) {
             bool is_v;
             int tq, piece;
             job_coords(r, is_v, tq, piece);
-            if (quad_pages) {
+            const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
+            if constexpr (quad_pages) {
                 ids[r][0] = uint32_t(a.blocks[table + (min(t0 + 4 * tq, end1) >> a.block_shift)]);
             } else {
 #pragma unroll
@@ -194,28 +206,31 @@ paged_prefill_d128(PrefillArgs<T> a) {
             }
         }
     };
-    auto load_tile = [&](int t0, const uint32_t (&ids)[JPT][4], U16x8 (&stage)[JPT][4]) {
+    auto load_tile = [&](int tile_base, const uint32_t (&ids)[JPT][4], U16x8 (&stage)[JPT][4]) {
 #pragma unroll
         for (int r = 0; r < JPT; ++r) {
             bool is_v;
             int tq, piece;
             job_coords(r, is_v, tq, piece);
+            const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
             const T* src = (is_v ? a.v : a.k) + kvh * D + piece * 8;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = min(t0 + 4 * tq + e, end1);
-                const uint32_t slot = quad_pages ? ids[r][0] * uint32_t(bs) + uint32_t(t & (bs - 1))
-                                                 : ids[r][e] * uint32_t(bs) + uint32_t(t % bs);
+                uint32_t slot;
+                if constexpr (quad_pages) slot = ids[r][0] * uint32_t(bs) + uint32_t(t & (bs - 1));
+                else slot = ids[r][e] * uint32_t(bs) + uint32_t(t % bs);
                 stage[r][e] = *reinterpret_cast<const U16x8*>(src + uint64_t(slot) * slot_elems);
             }
         }
     };
-    auto store_tile = [&](int buf, const U16x8 (&stage)[JPT][4]) {
+    auto store_tile = [&](int tile_base, const U16x8 (&stage)[JPT][4]) {
 #pragma unroll
         for (int r = 0; r < JPT; ++r) {
             bool is_v;
             int tq, piece;
             job_coords(r, is_v, tq, piece);
+            const int buf = (tile_base + lead_of(is_v)) & 1;
             if (is_v) {
                 // V^T: dim row (piece*8 + dd), the quad's 4 tokens -> one 8-byte write;
                 // v_perm picks the low (even dd) or high (odd dd) halves of two words.
@@ -236,34 +251,38 @@ paged_prefill_d128(PrefillArgs<T> a) {
         }
     };
 
-    auto compute = [&](int64_t t0, int buf) {
-        if (!wave_active || t0 >= wave_kv_end) return;
-        const uint16_t* kt = ks[buf];
-        const uint16_t* vtt = vt[buf];
-        // ---- S^T: s[tb][v] = token t0 + 32tb + 8(v/4) + 4*half + v%4, query col
-        f32x16 s[2] = {f32x16{}, f32x16{}};
+    // ---- per-wave math on one tile j ----------------------------------
+    f32x16 sc[2];  // raw S^T of the tile: sc[tb][v] = token 32tb + 8(v/4) + 4*half + v%4
+    U16x8 pb[4];   // P of the tile, k-step st: token 16st + 8jj + 4*half + i at k = 4jj + i
+    auto scores = [&](int j) {
+        const uint16_t* kt = ks[j & 1];
+        sc[0] = f32x16{};
+        sc[1] = f32x16{};
 #pragma unroll
         for (int c = 0; c < 8; ++c)
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
                 const U16x8 kk = *reinterpret_cast<const U16x8*>(
                     &kt[(32 * tb + col) * K_LD + 16 * c + 8 * half]);
-                s[tb] = mfma32<T>(kk, qv[c], s[tb]);
+                sc[tb] = mfma32<T>(kk, qv[c], sc[tb]);
             }
+    };
+    auto softmax = [&](int j) {
+        const int64_t t0 = int64_t(j) * BK;
         if (t0 + BK - 1 > wave_first_pos) {  // tile crosses the diagonal
+            // Keys past this lane's query: offset within the tile > lim.
+            const int lim = int(my_pos - t0) - 4 * half;
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t t = t0 + 32 * tb + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (t > my_pos) s[tb][v] = -INFINITY;
-                }
+                for (int v = 0; v < 16; ++v)
+                    if (32 * tb + 8 * (v >> 2) + (v & 3) > lim) sc[tb][v] = -INFINITY;
         }
         float cmax = -INFINITY;
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) cmax = fmaxf(cmax, s[tb][v]);
+            for (int v = 0; v < 16; ++v) cmax = fmaxf(cmax, sc[tb][v]);
         const float cm = pair_max(cmax) * a.scale_log2;  // scale > 0
         const bool grow = cm > m_run + kSlack;  // also: first finite max
         float alpha = 1.f;
@@ -278,13 +297,12 @@ paged_prefill_d128(PrefillArgs<T> a) {
         }
         const float m_use = m_run == -INFINITY ? 0.f : m_run;
         float psum = 0.f;
-        U16x8 pb[4];  // k-step st: tokens 16st + 8jj + 4*half + i at k = 4jj + i
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             float p[16];
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[tb][v], a.scale_log2, -m_use));
+                p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tb][v], a.scale_log2, -m_use));
                 psum += p[v];
             }
 #pragma unroll
@@ -297,7 +315,9 @@ paged_prefill_d128(PrefillArgs<T> a) {
             }
         }
         l_run += psum;
-        // ---- O^T += V^T P^T over four 16-token steps.
+    };
+    auto pv = [&](int j) {  // O^T += V^T P^T over four 16-token steps
+        const uint16_t* vtt = vt[j & 1];
 #pragma unroll
         for (int st = 0; st < 4; ++st)
 #pragma unroll
@@ -308,35 +328,66 @@ paged_prefill_d128(PrefillArgs<T> a) {
             }
     };
 
-    // Two staging register sets alternate: while tile i is computed from LDS,
-    // tile i+1 sits loaded in registers (stored to the other LDS buffer after
-    // the compute) and tile i+2's loads are already in flight.
     const int ntiles = int((kv_end + BK - 1) / BK);
-    U16x8 st_a[JPT][4], st_b[JPT][4];
-    uint32_t id_a[JPT][4], id_b[JPT][4];
-    load_ids(0, id_a);
-    load_tile(0, id_a, st_a);
-    if (ntiles > 1) {
-        load_ids(BK, id_b);
-        load_tile(BK, id_b, st_b);
+    const int wt = wave_active ? int((wave_kv_end + BK - 1) / BK) : 0;  // this wave's tiles
+    // Ping-pong: waves 0..W/2-1 ("matrix first") and W/2..W-1 ("vector
+    // first") pair up on each SIMD. Every tile is split in two halves at a
+    // barrier; in each half one wave of a pair issues MFMAs (P.V of tile i
+    // and S of tile i+1) while the other runs exponentials, so the matrix
+    // cores and the vector ALUs work at the same time.
+    const bool matrix_first = wave < W / 2;
+
+    // Prologue: K(0), K(1), V(0) into LDS; registers then hold K(2) and V(1).
+    {
+        U16x8 st0[JPT][4];
+        uint32_t id0[JPT][4];
+        load_ids(-2, id0);  // K(0) (the V half names tile -1 and is skipped)
+        load_tile(-2, id0, st0);
+        store_tile(-2, st0);
+        load_ids(-1, id0);  // K(1), V(0)
+        load_tile(-1, id0, st0);
+        store_tile(-1, st0);
+        // Retire every prologue load here. Left pending on some path, they
+        // make the wait-count pass stall the loop's first use of reused
+        // registers until the next tile's prefetch lands (vmcnt is in-order).
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     }
-    if (ntiles > 2) load_ids(2 * BK, id_a);
-    store_tile(0, st_a);
+    U16x8 stage[JPT][4];
+    uint32_t ids[JPT][4];
+    load_ids(0, ids);
+    load_tile(0, ids, stage);
+    load_ids(1, ids);
     __syncthreads();
-    // step(i): `held` has tile i+1, `spare` is free, `ids` are tile i+2's.
-    auto step = [&](int i, const U16x8 (&held)[JPT][4], U16x8 (&spare)[JPT][4],
-                    const uint32_t (&ids)[JPT][4], uint32_t (&ids_out)[JPT][4]) {
-        if (i + 2 < ntiles) {
-            load_tile((i + 2) * BK, ids, spare);
-            if (i + 3 < ntiles) load_ids((i + 3) * BK, ids_out);
+    if (wt > 0) {
+        scores(0);
+        if (matrix_first) softmax(0);
+    }
+
+    for (int i = 0; i < ntiles; ++i) {
+        // First half: tile i's P.V and tile i+1's S (matrix first), or
+        // tile i's softmax (vector first).
+        if (matrix_first) {
+            if (i < wt) {
+                pv(i);
+                if (i + 1 < wt) scores(i + 1);
+            }
+        } else if (i < wt) {
+            softmax(i);
         }
-        compute(int64_t(i) * BK, i & 1);
-        if (i + 1 < ntiles) store_tile((i + 1) & 1, held);
         __syncthreads();
-    };
-    for (int i = 0; i < ntiles; i += 2) {
-        step(i, st_b, st_a, id_a, id_b);
-        if (i + 1 < ntiles) step(i + 1, st_a, st_b, id_b, id_a);
+        // Second half: the roles swap.
+        if (matrix_first) {
+            if (i + 1 < wt) softmax(i + 1);
+        } else if (i < wt) {
+            pv(i);
+            if (i + 1 < wt) scores(i + 1);
+        }
+        // Staging: K(i+2) -> the buffer of K(i) and V(i+1) -> the buffer of
+        // V(i-1); both were last read before the previous barrier.
+        store_tile(i, stage);
+        load_tile(i + 1, ids, stage);
+        load_ids(i + 2, ids);
+        __syncthreads();
     }
     if (!wave_active) return;
 
@@ -423,8 +474,14 @@ extern "C" int tvllm_paged_prefill(
         args.scale_log2 = scale * kLog2e;
         args.block_shift = (block_size & (block_size - 1)) == 0
                                ? __builtin_ctzll(uint64_t(block_size)) : -1;
-        if (waves == 8) paged_prefill_d128<T, 8><<<int(grid), 512, 0, s>>>(args);
-        else paged_prefill_d128<T, 4><<<int(grid), 256, 0, s>>>(args);
+        const bool quad = args.block_shift >= 2;
+        if (waves == 8) {
+            if (quad) paged_prefill_d128<T, 8, true><<<int(grid), 512, 0, s>>>(args);
+            else paged_prefill_d128<T, 8, false><<<int(grid), 512, 0, s>>>(args);
+        } else {
+            if (quad) paged_prefill_d128<T, 4, true><<<int(grid), 256, 0, s>>>(args);
+            else paged_prefill_d128<T, 4, false><<<int(grid), 256, 0, s>>>(args);
+        }
         return launch_status("paged_prefill");
     });
 }
