@@ -337,26 +337,24 @@ paged_prefill_d128(PrefillArgs<T> a) {
     // cores and the vector ALUs work at the same time.
     const bool matrix_first = wave < W / 2;
 
-    // Prologue: K(0), K(1), V(0) into LDS; registers then hold K(2) and V(1).
-    {
-        U16x8 st0[JPT][4];
-        uint32_t id0[JPT][4];
-        load_ids(-2, id0);  // K(0) (the V half names tile -1 and is skipped)
-        load_tile(-2, id0, st0);
-        store_tile(-2, st0);
-        load_ids(-1, id0);  // K(1), V(0)
-        load_tile(-1, id0, st0);
-        store_tile(-1, st0);
-        // Retire every prologue load here. Left pending on some path, they
-        // make the wait-count pass stall the loop's first use of reused
-        // registers until the next tile's prefetch lands (vmcnt is in-order).
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    }
+    // Prologue: K(0), K(1), V(0) into LDS, and K(2), V(1) into registers,
+    // with the three tiles' block ids and rows fetched concurrently. (The
+    // first staging call also writes V(0) into the spare V buffer.)
     U16x8 stage[JPT][4];
     uint32_t ids[JPT][4];
-    load_ids(0, ids);
-    load_tile(0, ids, stage);
-    load_ids(1, ids);
+    {
+        U16x8 st0[JPT][4], st1[JPT][4];
+        uint32_t id0[JPT][4], id1[JPT][4];
+        load_ids(-2, id0);
+        load_ids(-1, id1);
+        load_ids(0, ids);
+        load_tile(-2, id0, st0);
+        load_tile(-1, id1, st1);
+        load_tile(0, ids, stage);
+        load_ids(1, ids);
+        store_tile(-2, st0);
+        store_tile(-1, st1);
+    }
     __syncthreads();
     if (wt > 0) {
         scores(0);
