@@ -108,6 +108,22 @@ int tvllm_rms_norm(const void* input, int64_t tokens, int64_t heads,
                    int64_t residual_stride, void* out, void* residual_out,
                    float eps, int dtype, tvllm_stream_t stream);
 
+/* add+RMSNorm whose input x is the sum of fp32 split-K partial products:
+ * x[t, c] = round(sum_p partials[p * partial_stride + t * width + c]), then
+ * residual_out = round(x + residual) and out = RMSNorm(residual_out) with
+ * the rounding points of tvllm_rms_norm. width % 8 == 0, width <= 8192,
+ * 1..64 partials; residual rows with stride residual_stride.
+ * Replaces: the rounding of the down projection's output (F.linear, reference
+ *           models/qwen3.py MLP) fused with torch.ops.tinyvllm_cuda.add_rms_norm
+ *           (reference tinyvllm/kernels/pointwise.cu:549-616); no reference
+ *           counterpart for the split-K decomposition itself. */
+int tvllm_add_rms_norm_partials(const float* partials, int64_t num_partials,
+                                int64_t partial_stride, int64_t tokens,
+                                int64_t width, const void* weight,
+                                const void* residual, int64_t residual_stride,
+                                void* out, void* residual_out, float eps,
+                                int dtype, tvllm_stream_t stream);
+
 /* out[r, c] = round(round(silu(x[r, c])) * x[r, c + width / 2]) for rows
  * laid out like tvllm_rms_norm's input; out is dense [count, width / 2].
  * Replaces: torch.ops.tinyvllm_cuda.silu_and_mul

@@ -226,6 +226,52 @@ def test_rms_norm_and_add(device, width):
     assert_bf16_close(y2.cpu(), ey)
 
 
+@pytest.mark.parametrize("splits,tokens,width", [(4, 64, 4096), (8, 200, 1024),
+                                                (1, 5, 5120), (3, 33, 8192)])
+def test_add_rms_norm_partials(device, splits, tokens, width):
+    """x = round(sequential fp32 sum of the split-K partials), then add+RMSNorm:
+    the rounded residual sum is bit-exact, the normed output within bf16."""
+    from tinyvllm.kernels.pointwise import add_rms_norm_partials
+
+    g = torch.Generator().manual_seed(splits * 1000 + tokens)
+    parts = torch.randn(splits, tokens, width, generator=g)
+    r = torch.randn(tokens, width, generator=g).to(torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(width, generator=g)).to(torch.bfloat16)
+    x = parts[0].clone()
+    for p in range(1, splits):
+        x = x + parts[p]
+    x = x.to(torch.bfloat16)
+    y, merged = add_rms_norm_partials(parts.to(device), r.to(device), w.to(device))
+    ey, em = OP.add_rms_norm(x, r, w)
+    assert torch.equal(merged.cpu(), em)
+    assert_bf16_close(y.cpu(), ey)
+
+
+@pytest.mark.parametrize("rows", [8, 64, 200, 600])
+def test_split_k_down_projection_matches_linear(device, rows):
+    """SplitKLinear (torch.bmm over reduction slices, fp32 partials) summed by
+    RMSNorm.add equals F.linear followed by add_rms_norm within bf16."""
+    from tinyvllm.layers import RMSNorm, SplitKLinear, SplitKPartials
+
+    torch.manual_seed(rows)
+    lin = SplitKLinear(3072, 1024, device=device, dtype=torch.bfloat16)
+    torch.nn.init.normal_(lin.weight, std=0.02)
+    norm = RMSNorm(1024, device=device, dtype=torch.bfloat16)
+    x = torch.randn(rows, 3072, device=device, dtype=torch.bfloat16)
+    res = torch.randn(rows, 1024, device=device, dtype=torch.bfloat16)
+    y = lin(x)
+    assert isinstance(y, SplitKPartials) == (lin.splits_for(rows) > 1)
+    ref = torch.nn.functional.linear(x.float(), lin.weight.float())
+    dense = y.materialize() if isinstance(y, SplitKPartials) else y
+    assert_bf16_close(dense.float().cpu(), ref.to(torch.bfloat16).float().cpu())
+    out, merged = norm.add(y, res)
+    eo, em = norm.add(ref.to(torch.bfloat16), res)
+    # Different accumulation orders may flip one bf16 rounding of sums of
+    # magnitude up to ~8 (ulp 0.03-0.06): allow two ulps there, L1 as usual.
+    assert_bf16_close(merged.float().cpu(), em.float().cpu(), max_abs=0.07)
+    assert_bf16_close(out.float().cpu(), eo.float().cpu(), max_abs=0.07)
+
+
 def test_rms_norm_3d_strided_and_fp32(device):
     from tinyvllm.kernels.pointwise import rms_norm
 

@@ -183,6 +183,62 @@ int launch_rms(const void* x, int64_t rows, int64_t heads, int width,
     return launch_status(RESIDUAL ? "add_rms_norm" : "rms_norm");
 }
 
+// add+RMSNorm whose x is the sum of fp32 split-K partial products
+// (partials[p][row][c], p < nparts): x = round(sum_p partials), then exactly
+// the add+RMSNorm above. One 256-thread workgroup per row; NV chunks of 8.
+template <typename T, int NV>
+__global__ void __launch_bounds__(256)
+add_rms_norm_partials_kernel(const float* __restrict__ parts, int nparts,
+                             int64_t part_stride, int width,
+                             const T* __restrict__ weight,
+                             const T* __restrict__ residual,
+                             int64_t residual_stride, T* __restrict__ out,
+                             T* __restrict__ residual_out, float eps) {
+    const int64_t row = blockIdx.x;
+    const int t = threadIdx.x;
+    float v[NV][8], wv[NV][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int c = (n * 256 + t) * 8;
+        const bool ok = c < width;  // width % 8 == 0 (checked on the host)
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (ok) {
+            const float* src = parts + row * int64_t(width) + c;
+            for (int p = 0; p < nparts; ++p) {
+                const float4 a = *reinterpret_cast<const float4*>(src + p * part_stride);
+                const float4 b = *reinterpret_cast<const float4*>(src + p * part_stride + 4);
+                acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+                acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+            }
+        }
+        float rv[8];
+        load8<T, true>(weight + c, ok ? 8 : 0, wv[n]);
+        load8<T, true>(residual + row * residual_stride + c, ok ? 8 : 0, rv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[n][i] = ok ? rnd<T>(rnd<T>(acc[i]) + rv[i]) : 0.f;
+            ss += v[n][i] * v[n][i];
+        }
+    }
+    ss = wave_sum(ss);
+    __shared__ float partial[4];
+    if ((t & 63) == 0) partial[t >> 6] = ss;
+    __syncthreads();
+    ss = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inv = rsqrtf(ss * (1.0f / float(width)) + eps);
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int c = (n * 256 + t) * 8;
+        if (c >= width) continue;
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = rnd<T>(rnd<T>(v[n][i] * inv) * wv[n][i]);
+        store8<T, true>(out + row * int64_t(width) + c, 8, y);
+        store8<T, true>(residual_out + row * int64_t(width) + c, 8, v[n]);
+    }
+}
+
 // --------------------------------------------------------- SiLU * up ----
 
 template <typename T, bool VEC>
@@ -333,6 +389,44 @@ extern "C" int tvllm_rms_norm(const void* input, int64_t tokens, int64_t heads,
         return launch_rms<T, false>(input, rows, heads, int(width), token_stride,
                                     head_stride, weight, nullptr, 0, out, nullptr,
                                     eps, s);
+    });
+}
+
+extern "C" int tvllm_add_rms_norm_partials(
+    const float* partials, int64_t num_partials, int64_t partial_stride,
+    int64_t tokens, int64_t width, const void* weight, const void* residual,
+    int64_t residual_stride, void* out, void* residual_out, float eps, int dtype,
+    tvllm_stream_t stream) {
+    TVLLM_CHECK(tokens >= 0 && width > 0 && width % 8 == 0 && width <= 8 * 256 * 4,
+                "add_rms_norm_partials: width must be a multiple of 8, at most 8192");
+    TVLLM_CHECK(num_partials >= 1 && num_partials <= 64,
+                "add_rms_norm_partials: 1..64 partial products");
+    TVLLM_CHECK(tokens <= INT32_MAX, "add_rms_norm_partials: too many rows");
+    if (tokens == 0) return TVLLM_OK;
+    TVLLM_CHECK(partials && weight && residual && out && residual_out,
+                "add_rms_norm_partials: null pointer");
+    TVLLM_CHECK(partial_stride >= tokens * width && partial_stride % 4 == 0 &&
+                    aligned16(partials) && residual_stride % 8 == 0 && aligned16(weight) &&
+                    aligned16(residual) && aligned16(out) && aligned16(residual_out),
+                "add_rms_norm_partials: operands must be 16-byte aligned dense rows");
+    hipStream_t s = as_hip(stream);
+    return dispatch_half(dtype, [&]<int DT>() {
+        using T = typename Elem<DT>::T;
+        const T* wp = static_cast<const T*>(weight);
+        const T* rp = static_cast<const T*>(residual);
+        T* op = static_cast<T*>(out);
+        T* rop = static_cast<T*>(residual_out);
+        const int np = int(num_partials), w = int(width);
+        if (width <= 2048)
+            add_rms_norm_partials_kernel<T, 1><<<int(tokens), 256, 0, s>>>(
+                partials, np, partial_stride, w, wp, rp, residual_stride, op, rop, eps);
+        else if (width <= 4096)
+            add_rms_norm_partials_kernel<T, 2><<<int(tokens), 256, 0, s>>>(
+                partials, np, partial_stride, w, wp, rp, residual_stride, op, rop, eps);
+        else
+            add_rms_norm_partials_kernel<T, 4><<<int(tokens), 256, 0, s>>>(
+                partials, np, partial_stride, w, wp, rp, residual_stride, op, rop, eps);
+        return launch_status("add_rms_norm_partials");
     });
 }
 

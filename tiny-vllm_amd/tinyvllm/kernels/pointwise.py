@@ -82,6 +82,37 @@ def add_rms_norm(
     return out, merged
 
 
+def add_rms_norm_partials(
+    partials: torch.Tensor,
+    residual: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float = 1e-6,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """add_rms_norm whose x is ``round(partials.sum(0))``: the fp32 split-K
+    partial products [splits, tokens, width] of a projection, summed and
+    rounded to the residual's dtype inside the kernel (no reference
+    counterpart; it replaces F.linear's rounding + add_rms_norm)."""
+    lib = load_kernels()
+    device = require_gpu(partials, residual, weight)
+    if (partials.dtype != torch.float32 or partials.dim() != 3
+            or not partials.is_contiguous()):
+        raise RuntimeError("partials must be contiguous fp32 [splits, tokens, width]")
+    splits, tokens, width = partials.shape
+    if (residual.dim() != 2 or tuple(residual.shape) != (tokens, width)
+            or residual.stride(-1) != 1 or residual.dtype not in (torch.float16, torch.bfloat16)):
+        raise RuntimeError("residual must be a half-precision [tokens, width] tensor")
+    _check_weight(residual, weight)
+    out = torch.empty((tokens, width), dtype=residual.dtype, device=device)
+    merged = torch.empty((tokens, width), dtype=residual.dtype, device=device)
+    if out.numel():
+        check(lib.tvllm_add_rms_norm_partials(
+            partials.data_ptr(), splits, tokens * width, tokens, width, weight.data_ptr(),
+            residual.data_ptr(), residual.stride(0), out.data_ptr(), merged.data_ptr(),
+            float(eps), dtype_code(residual.dtype), stream_of(device),
+        ))
+    return out, merged
+
+
 def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     """Fuse the activation and gate/up product, preserving intermediate rounding."""
     lib = load_kernels()

@@ -13,7 +13,9 @@ import torch.nn.functional as F
 from torch import nn
 
 from tinyvllm._validation import _check_positive_int
-from tinyvllm.kernels.pointwise import add_rms_norm, rms_norm, silu_and_mul
+from tinyvllm.kernels.pointwise import (
+    add_rms_norm, add_rms_norm_partials, rms_norm, silu_and_mul,
+)
 
 
 class PackedLinear(nn.Module):
@@ -82,6 +84,52 @@ class PackedLinear(nn.Module):
             self.weight[start:start + size].copy_(loaded_weight)
 
 
+class SplitKPartials:
+    """fp32 partial products [splits, tokens, out_features] of a split-K
+    projection; the consumer (RMSNorm.add) sums and rounds them."""
+
+    __slots__ = ("partials", "dtype")
+
+    def __init__(self, partials: torch.Tensor, dtype: torch.dtype) -> None:
+        self.partials = partials
+        self.dtype = dtype
+
+    @property
+    def shape(self) -> torch.Size:
+        return self.partials.shape[1:]
+
+    def materialize(self) -> torch.Tensor:
+        """The projection's output as F.linear would return it."""
+        return self.partials.sum(0).to(self.dtype)
+
+
+class SplitKLinear(nn.Linear):
+    """Bias-free nn.Linear for a projection with a long reduction axis (the
+    MLP down projection). For skinny inputs - the decode batch - hipBLASLt's
+    single GEMM leaves most of the GPU idle, so the product runs as a batched
+    torch.bmm over ``splits`` slices of the reduction axis with fp32 outputs,
+    returned as SplitKPartials for RMSNorm.add to sum inside its kernel.
+    Other inputs take F.linear. (Measured on MI355X, 4096x12288 bf16: 37 us
+    -> 24 us at 64 rows, 67 us -> 28 us at 128 rows.)"""
+
+    def __init__(self, in_features: int, out_features: int, *, device=None,
+                 dtype=None) -> None:
+        super().__init__(in_features, out_features, bias=False, device=device, dtype=dtype)
+
+    def splits_for(self, rows: int) -> int:
+        s = 4 if 32 <= rows <= 128 else 8 if 128 < rows <= 512 else 1
+        return s if self.in_features % (8 * s) == 0 else 1
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor | SplitKPartials:
+        s = self.splits_for(x.shape[0]) if x.dim() == 2 else 1
+        if s == 1:
+            return F.linear(x, self.weight)
+        rows, k = x.shape
+        xs = x.view(rows, s, k // s).transpose(0, 1)
+        ws = self.weight.view(self.out_features, s, k // s).permute(1, 2, 0)
+        return SplitKPartials(torch.bmm(xs, ws, out_dtype=torch.float32), x.dtype)
+
+
 class RMSNorm(nn.Module):
     """Qwen3 RMSNorm, fp32 variance accumulation (reference layers.py:129-164)."""
 
@@ -103,9 +151,12 @@ class RMSNorm(nn.Module):
         return rms_norm(x, self.weight, self.eps)
 
     def add(
-        self, x: torch.Tensor, residual: torch.Tensor,
+        self, x: torch.Tensor | SplitKPartials, residual: torch.Tensor,
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """(norm(x + residual), x + residual), both rounded to the storage type."""
+        """(norm(x + residual), x + residual), both rounded to the storage type;
+        split-K partials are summed and rounded first, inside the kernel."""
+        if isinstance(x, SplitKPartials):
+            return add_rms_norm_partials(x.partials, residual, self.weight, self.eps)
         return add_rms_norm(x, residual, self.weight, self.eps)
 
 

@@ -22,7 +22,9 @@ from torch import nn
 
 from tinyvllm._validation import _check_positive_int
 from tinyvllm.kernels.pointwise import qk_norm_rope
-from tinyvllm.layers import PackedLinear, RMSNorm, RotaryEmbedding, SiluAndMul
+from tinyvllm.layers import (
+    PackedLinear, RMSNorm, RotaryEmbedding, SiluAndMul, SplitKLinear, SplitKPartials,
+)
 from tinyvllm.runtime.contracts import AttentionBackend
 
 _REQUIRED_FIELDS = frozenset({
@@ -170,11 +172,13 @@ class Qwen3MLP(nn.Module):
             config.hidden_size, (config.intermediate_size, config.intermediate_size),
             shard_names=("gate", "up"), device=device, dtype=dtype,
         )
-        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size,
-                                   bias=False, device=device, dtype=dtype)
+        self.down_proj = SplitKLinear(config.intermediate_size, config.hidden_size,
+                                      device=device, dtype=dtype)
         self.act_fn = SiluAndMul()
 
-    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor | SplitKPartials:
+        """Returns SplitKPartials for decode-sized batches (consumed by the
+        next RMSNorm.add)."""
         return self.down_proj(self.act_fn(self.gate_up_proj(hidden_states)))
 
 
