@@ -124,7 +124,7 @@ def measured_traffic() -> int | None:
 
 def attention_roofline(executor, workload, cfg, iters: int = 30) -> dict:
     """Time the paged decode kernel on layer 0 of the live cache with the
-    live step metadata, with HIP events on the stream it launches on."""
+    live step metadata (graph-replayed, HIP events on the replay stream)."""
     import torch
 
     from tinyvllm.kernels.paged_decode import paged_decode_attention
@@ -133,23 +133,17 @@ def attention_roofline(executor, workload, cfg, iters: int = 30) -> dict:
     batch = workload.batch_for_step()
     model_input = runner.decode_inputs.prepare(batch, [0] * batch.num_items)
     meta = model_input.kv.decode
-    stream = torch.cuda.current_stream()
     q = torch.randn(batch.num_items, cfg.num_attention_heads, cfg.head_dim,
                     dtype=torch.bfloat16, device=runner.device)
     out = torch.empty_like(q)
     scale = cfg.head_dim ** -0.5
-    for _ in range(3):
-        paged_decode_attention(q, runner.kv_cache, 0, meta, out, scale=scale,
-                               workspace=runner.decode_workspace)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    stream.synchronize()
-    start.record(stream)
-    for _ in range(iters):
-        paged_decode_attention(q, runner.kv_cache, 0, meta, out, scale=scale,
-                               workspace=runner.decode_workspace)
-    end.record(stream)
-    end.synchronize()
-    seconds = start.elapsed_time(end) / 1e3 / iters
+    # The decode step replays this kernel inside a hipGraph; time it the same
+    # way: `iters` launches captured in one graph, replayed between HIP events
+    # on the replay stream.
+    with torch.inference_mode():  # the runner's cache and inputs are inference tensors
+        seconds = _event_time(lambda: paged_decode_attention(
+            q, runner.kv_cache, 0, meta, out, scale=scale,
+            workspace=runner.decode_workspace), iters)
     lengths = batch.context_lens_after
     pages = sum(math.ceil(l / workload.bs) for l in lengths)
     rows, hq, hkv, d = batch.num_items, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
@@ -278,7 +272,7 @@ def kernel_only(args) -> None:
                       "decode_launches": args.steps, "copy_bytes": src.numel() * 2}))
 
 
-def summarize_profile(directory: str, tail: int = 33) -> None:
+def summarize_profile(directory: str, tail: int = 30) -> None:
     """Print a short text summary of a rocprofv3 --kernel-trace --stats run
     (kernel_stats.csv) and, when present, PMC counter averages per kernel."""
     import csv
