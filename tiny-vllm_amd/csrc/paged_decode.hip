@@ -82,6 +82,22 @@ __device__ __forceinline__ uint32_t shfl_u32(uint32_t v, int src) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// V rows are streamed exactly once per step and each load instruction covers
+// whole rows (16 lanes x 16 bytes): non-temporal loads measure ~13% more read
+// bandwidth on MI355X for such streams (7.1 vs 6.3 TB/s). K loads touch each
+// 128-byte line from two instructions (the MFMA operand layout), so they stay
+// ordinary loads: a non-temporal first touch would refetch the line.
+__device__ __forceinline__ U16x8 load_stream(const U16x8* p) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    U16x8 r;
+    r.w[0] = t[0];
+    r.w[1] = t[1];
+    r.w[2] = t[2];
+    r.w[3] = t[3];
+    return r;
+}
+
 template <typename T>
 struct DecodeArgs {
     const T* q;
@@ -201,7 +217,7 @@ paged_decode_d128(DecodeArgs<T> a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t vr = shfl_u32(my_row, 16 * j + 4 * quad + i);
-                    vreg[j][i] = a.v[vr + col];
+                    vreg[j][i] = load_stream(a.v + vr + col);
                 }
         };
 

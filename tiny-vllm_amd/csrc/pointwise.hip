@@ -186,7 +186,9 @@ int launch_rms(const void* x, int64_t rows, int64_t heads, int width,
 // add+RMSNorm whose x is the sum of fp32 split-K partial products
 // (partials[p][row][c], p < nparts): x = round(sum_p partials), then exactly
 // the add+RMSNorm above. One 256-thread workgroup per row; NV chunks of 8.
-template <typename T, int NV>
+// NP > 0 fixes the partial count at compile time so that every load of a
+// thread is in flight at once (the sum order stays p = 0, 1, ...).
+template <typename T, int NV, int NP>
 __global__ void __launch_bounds__(256)
 add_rms_norm_partials_kernel(const float* __restrict__ parts, int nparts,
                              int64_t part_stride, int width,
@@ -205,7 +207,10 @@ add_rms_norm_partials_kernel(const float* __restrict__ parts, int nparts,
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (ok) {
             const float* src = parts + row * int64_t(width) + c;
-            for (int p = 0; p < nparts; ++p) {
+            const int np = NP > 0 ? NP : nparts;
+#pragma unroll
+            for (int p = 0; p < (NP > 0 ? NP : 64); ++p) {
+                if (NP == 0 && p >= np) break;
                 const float4 a = *reinterpret_cast<const float4*>(src + p * part_stride);
                 const float4 b = *reinterpret_cast<const float4*>(src + p * part_stride + 4);
                 acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
@@ -417,15 +422,19 @@ extern "C" int tvllm_add_rms_norm_partials(
         T* op = static_cast<T*>(out);
         T* rop = static_cast<T*>(residual_out);
         const int np = int(num_partials), w = int(width);
-        if (width <= 2048)
-            add_rms_norm_partials_kernel<T, 1><<<int(tokens), 256, 0, s>>>(
-                partials, np, partial_stride, w, wp, rp, residual_stride, op, rop, eps);
-        else if (width <= 4096)
-            add_rms_norm_partials_kernel<T, 2><<<int(tokens), 256, 0, s>>>(
-                partials, np, partial_stride, w, wp, rp, residual_stride, op, rop, eps);
-        else
-            add_rms_norm_partials_kernel<T, 4><<<int(tokens), 256, 0, s>>>(
-                partials, np, partial_stride, w, wp, rp, residual_stride, op, rop, eps);
+        auto go = [&]<int NV>() {
+#define TVLLM_PARTS(NP)                                                            \
+    add_rms_norm_partials_kernel<T, NV, NP><<<int(tokens), 256, 0, s>>>(           \
+        partials, np, partial_stride, w, wp, rp, residual_stride, op, rop, eps)
+            if (np == 4) TVLLM_PARTS(4);
+            else if (np == 8) TVLLM_PARTS(8);
+            else if (np == 2) TVLLM_PARTS(2);
+            else TVLLM_PARTS(0);
+#undef TVLLM_PARTS
+        };
+        if (width <= 2048) go.template operator()<1>();
+        else if (width <= 4096) go.template operator()<2>();
+        else go.template operator()<4>();
         return launch_status("add_rms_norm_partials");
     });
 }
