@@ -511,7 +511,9 @@ def op_c2(args) -> dict:
 def op_prefill(args) -> dict:
     """Chunked-prefill paged attention at the C4 chunk shape: 512-query chunks
     of 2048-token prompts (the last chunk sees 2048 keys), Qwen3-8B heads
-    (32Q/8KV, D128), 4 items; MFMA roofline (flops of the causal region)."""
+    (32Q/8KV, D128), 4 items; and a C5 shape: 8 chunks of 512 queries at
+    24576 tokens of history with Qwen3-32B heads (64Q/8KV). MFMA roofline
+    (flops of the causal region)."""
     import torch
 
     from oracle import attention as OA
@@ -521,9 +523,10 @@ def op_prefill(args) -> dict:
 
     device = torch.device("cuda", 0)
     result = {}
-    for name, items, qlen, ctx in (("c4_chunk512_ctx2048_x4", 4, 512, 2048),
-                                   ("c4_chunk512_ctx512_x4", 4, 512, 512)):
-        hq, hkv, d, bs = 32, 8, 128, 16
+    for name, items, qlen, ctx, hq in (("c4_chunk512_ctx2048_x4", 4, 512, 2048, 32),
+                                       ("c4_chunk512_ctx512_x4", 4, 512, 512, 32),
+                                       ("c5_chunk512_ctx24576_x8_qwen3-32b", 8, 512, 24576, 64)):
+        hkv, d, bs = 8, 128, 16
         g = torch.Generator().manual_seed(0)
         pages = ctx // bs
         pool = items * pages
