@@ -73,3 +73,33 @@ def test_engine_sampling_is_seeded_and_in_vocab(device):
     assert runs[0] == runs[1]
     assert all(0 <= t < CFG.vocab_size for out in runs[0] for t in out)
     assert runs[0][0] != runs[0][1]
+
+
+def test_llm_from_engine_config_checkpoint(device, tmp_path):
+    """The drop-in entry point: EngineConfig(model=<HF checkpoint dir>) ->
+    LLM -> greedy token ids, checked against the oracle model."""
+    from checkpoint_util import write_checkpoint
+    from tinyvllm import SamplingParams
+    from tinyvllm.config import EngineConfig
+    from tinyvllm.serving.llm import LLM
+
+    weights = OM.random_weights(CFG, seed=9, dtype=torch.bfloat16, std=0.2)
+    write_checkpoint(tmp_path, CFG, weights, shards=2)
+
+    class NoText:  # token-id use only; LLM never calls it with ids
+        def decode(self, ids):
+            return ""
+
+    config = EngineConfig(model=tmp_path, max_model_len=512, max_num_seqs=4,
+                          max_num_batched_tokens=256, prefill_chunk_size=64,
+                          prefill_reserve_tokens=32, kv_cache_memory_bytes=8 << 20)
+    g = torch.Generator().manual_seed(10)
+    prompts = [torch.randint(0, CFG.vocab_size, (n,), generator=g).tolist() for n in (9, 130)]
+    new = 10
+    with LLM(config, tokenizer=NoText()) as llm:
+        outs = llm.generate_token_ids(prompts, SamplingParams(max_new_tokens=new,
+                                                              ignore_eos=True))
+    agree = sum(teacher_forced_agreement(weights, p, o.output_token_ids)
+                for p, o in zip(prompts, outs))
+    assert agree / (new * len(prompts)) >= 0.99
+    assert all(o.finish_reason == "length" and len(o.output_token_ids) == new for o in outs)
