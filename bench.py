@@ -383,7 +383,8 @@ def _hbm(bytes_: int, seconds: float) -> dict:
 def op_c1(args) -> dict:
     """C1: the paged-decode op alone at Qwen3-0.6B shapes (8 rows, 16Q/8KV
     heads, D128, L ~ U[64,1024], 16-token pages from a 1024-page pool), plus
-    the 8B-shape variant (64 rows, 32Q/8KV, L=2048)."""
+    the 8B-shape variant (64 rows, 32Q/8KV, L=2048) and the C5 decode shape
+    (16 rows, 64Q/8KV, L ~ U[16k,32k]: workgroup-level split-K + merge)."""
     import torch
 
     from oracle import attention as OA
@@ -395,7 +396,9 @@ def op_c1(args) -> dict:
     result = {}
     for name, rows, hq, lengths_fn, pool in (
             ("c1_qwen3-0.6b_bs8", 8, 16, lambda g: torch.randint(64, 1025, (8,), generator=g), 1024),
-            ("qwen3-8b_bs64_ctx2048", 64, 32, lambda g: torch.full((64,), 2048), 64 * 128)):
+            ("qwen3-8b_bs64_ctx2048", 64, 32, lambda g: torch.full((64,), 2048), 64 * 128),
+            ("c5_qwen3-32b_bs16_ctx16k-32k", 16, 64,
+             lambda g: torch.randint(16384, 32769, (16,), generator=g), 16 * 2048)):
         g = torch.Generator().manual_seed(0)
         lengths = lengths_fn(g)
         pages = [math.ceil(int(l) / 16) for l in lengths]

@@ -113,6 +113,7 @@ struct DecodeArgs {
     int heads, kv_heads, group, block_size;
     int splits;         // waves per KV head per workgroup
     int grid_splits;    // workgroups per (row, KV head group)
+    int num_rows;       // rows of the batch (balanced spans scan their lengths)
     int heads_per_wg;   // KV heads per workgroup
     float scale_log2;   // softmax scale * log2(e): scores live in base 2
     float* part_o;      // [rows, heads, grid_splits, 128] (grid_splits > 1)
@@ -157,7 +158,21 @@ paged_decode_d128(DecodeArgs<T> a) {
     const int bs = a.block_size;
     const int64_t pages = (length + bs - 1) / bs;
     const int total_splits = a.splits * a.grid_splits;
-    const int64_t per_split = (pages + total_splits - 1) / total_splits;
+    // One workgroup per row (grid_splits == 1): the row's pages are divided
+    // evenly among its waves. Several workgroups per row (long contexts):
+    // every row uses the same span, sized from the longest row of the batch,
+    // so the workgroups of shorter rows past their end exit at once and the
+    // dispatcher balances the remaining ones across the CUs.
+    int64_t span_pages = pages;
+    if (a.grid_splits > 1) {
+        int64_t longest = 0;
+        for (int i = lane; i < a.num_rows; i += 64) longest = max(longest, a.lengths[i]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            longest = max(longest, static_cast<int64_t>(__shfl_xor(longest, off, 64)));
+        span_pages = (longest + bs - 1) / bs;
+    }
+    const int64_t per_split = (span_pages + total_splits - 1) / total_splits;
     const int64_t p_begin = int64_t(gsplit * a.splits + split) * per_split;
     const int64_t p_end = min(pages, p_begin + per_split);
     const int64_t t_begin = p_begin * bs;
@@ -656,6 +671,7 @@ extern "C" int tvllm_paged_decode(
         args.block_size = int(block_size);
         args.splits = int(plan.waves);
         args.grid_splits = int(plan.grid);
+        args.num_rows = int(num_rows);
         args.heads_per_wg = hpg;
         args.scale_log2 = scale_log2;
         args.part_o = static_cast<float*>(workspace);
