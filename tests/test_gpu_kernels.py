@@ -399,3 +399,34 @@ def test_decode_benchmark_and_long_context_shapes(device, rows, heads, ctx, max_
                              pool_blocks=rows * pages + 8, lengths=[ctx] * rows)
     out, expect = _run_decode(case, device, max_context_len=max_ctx)
     assert_bf16_close(out, expect)
+
+
+@pytest.mark.parametrize("lengths,heads,kv_heads", [
+    # workgroup-level splits with one span for all rows: empty and tiny rows
+    # next to long ones (their spare workgroups exit early)
+    ([0, 5, 30000, 17, 9000, 0], 64, 8),
+    ([20000, 1, 20000, 333], 32, 8),
+])
+def test_decode_mixed_long_context_splits(device, lengths, heads, kv_heads):
+    pool = sum(-(-n // 16) for n in lengths) + 8
+    case = paged_decode_case(seed=sum(lengths) % 997, batch=len(lengths), heads=heads,
+                             kv_heads=kv_heads, pool_blocks=pool, lengths=lengths)
+    out, expect = _run_decode(case, device, max_context_len=32768)
+    for r, n in enumerate(lengths):
+        if n == 0:
+            assert (out[r] == 0).all()
+    assert_bf16_close(out, expect)
+
+
+def test_decode_many_rows_long_context_splits(device):
+    """80 rows with workgroup-level splits (MQA: one KV head, few units)."""
+    g = torch.Generator().manual_seed(77)
+    lengths = torch.randint(1, 3000, (80,), generator=g).tolist()
+    lengths[3] = 0
+    pool = sum(-(-n // 16) for n in lengths) + 8
+    case = paged_decode_case(seed=78, batch=80, heads=8, kv_heads=1, pool_blocks=pool,
+                             lengths=lengths)
+    out, expect = _run_decode(case, device, max_context_len=4096)
+    assert (out[3] == 0).all()
+    assert_bf16_close(out, expect)
+
