@@ -123,32 +123,40 @@ def measured_traffic() -> int | None:
 
 
 def attention_roofline(executor, workload, cfg, iters: int = 30) -> dict:
-    """Time the paged decode kernel on layer 0 of the live cache with the
-    live step metadata (graph-replayed, HIP events on the replay stream)."""
+    """Time the decode step's attention kernel - QK-norm + RoPE + KV write +
+    split-K paged decode in one launch, as every decode layer runs it - on
+    layer 0 of the live cache with the live step metadata (graph-replayed,
+    HIP events on the replay stream)."""
     import torch
 
-    from tinyvllm.kernels.paged_decode import paged_decode_attention
+    from tinyvllm.kernels.paged_decode import paged_decode_qk_norm_rope
 
     runner = executor.runner
     batch = workload.batch_for_step()
     model_input = runner.decode_inputs.prepare(batch, [0] * batch.num_items)
     meta = model_input.kv.decode
-    q = torch.randn(batch.num_items, cfg.num_attention_heads, cfg.head_dim,
-                    dtype=torch.bfloat16, device=runner.device)
+    rows, hq, hkv, d = (batch.num_items, cfg.num_attention_heads, cfg.num_key_value_heads,
+                        cfg.head_dim)
+    qkv = torch.randn(rows, (hq + 2 * hkv) * d, dtype=torch.bfloat16, device=runner.device)
+    q = qkv[:, :hq * d].view(rows, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(rows, hkv, d)
+    layer = runner.model.model.layers[0].self_attn
+    cos, sin = runner.model.model.rotary_emb(model_input.positions, torch.bfloat16)
     out = torch.empty_like(q)
     scale = cfg.head_dim ** -0.5
-    # The decode step replays this kernel inside a hipGraph; time it the same
-    # way: `iters` launches captured in one graph, replayed between HIP events
-    # on the replay stream.
     with torch.inference_mode():  # the runner's cache and inputs are inference tensors
-        seconds = _event_time(lambda: paged_decode_attention(
-            q, runner.kv_cache, 0, meta, out, scale=scale,
-            workspace=runner.decode_workspace), iters)
+        seconds = _event_time(lambda: paged_decode_qk_norm_rope(
+            q, k, v, layer.q_norm.weight, layer.k_norm.weight, cos, sin, layer.q_norm.eps,
+            layer.k_norm.eps, runner.kv_cache, 0, meta, model_input.kv.slot_mapping, out,
+            scale=scale, workspace=runner.decode_workspace), iters)
     lengths = batch.context_lens_after
     pages = sum(math.ceil(l / workload.bs) for l in lengths)
-    rows, hq, hkv, d = batch.num_items, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-    algorithmic = (sum(lengths) * hkv * d * 2 * 2 + 2 * rows * hq * d * 2
-                   + 8 * pages + 8 * (3 * rows + 1))
+    # KV read once per KV head; q/k/v projections read, output and the new
+    # K/V rows written; RoPE tables, slots and block tables.
+    algorithmic = (sum(lengths) * hkv * d * 2 * 2 + rows * (hq + 2 * hkv) * d * 2
+                   + rows * hq * d * 2 + rows * 2 * hkv * d * 2 + rows * d * 2 * 2
+                   + 8 * pages + 8 * (4 * rows + 1))
     achieved = algorithmic / seconds / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -229,23 +237,24 @@ def cpu_baseline(cfg, batch: int, context: int, reps: int = 2) -> dict:
 
 
 def kernel_only(args) -> None:
-    """The decode-attention kernel alone at the workload's shape (one layer of
-    KV, the step's metadata), plus a 1 GiB device copy for counter
-    calibration. Used for rocprofv3 PMC passes, which profile dispatches
-    launched outside graphs."""
+    """The decode step's attention kernel (QK-norm + RoPE + KV write + split-K
+    paged decode) alone at the workload's shape (one layer of KV, one step's
+    metadata), plus a 1 GiB device copy for counter calibration. Used for
+    rocprofv3 PMC passes, which profile dispatches launched outside graphs."""
     import torch
 
-    from tinyvllm.kernels.paged_decode import decode_workspace_bytes, paged_decode_attention
+    from tinyvllm.kernels.paged_decode import decode_workspace_bytes, paged_decode_qk_norm_rope
+    from tinyvllm.layers import RotaryEmbedding
     from tinyvllm.paged_kv import PagedKVCache
     from tinyvllm.runtime.contracts import SingleQueryMetadata
 
     cfg = qwen3_config(args.model, max_position=40960)
     device = torch.device("cuda", 0)
     bs, rows, ctx = 16, args.batch, args.context + 1
+    hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     pages = math.ceil(ctx / bs)
     cache = PagedKVCache(num_layers=1, num_blocks=rows * pages, block_size=bs,
-                         num_kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
-                         device=device, dtype=torch.bfloat16)
+                         num_kv_heads=hkv, head_dim=d, device=device, dtype=torch.bfloat16)
     gen = torch.Generator(device=device).manual_seed(1)
     cache.key.normal_(generator=gen)
     cache.value.normal_(generator=gen)
@@ -254,15 +263,21 @@ def kernel_only(args) -> None:
     meta = SingleQueryMetadata(torch.arange(rows, device=device), perm,
                                torch.arange(rows + 1, device=device) * pages,
                                torch.full((rows,), ctx, device=device), max_len)
-    ws_bytes = decode_workspace_bytes(rows, cfg.num_attention_heads, cfg.num_key_value_heads,
-                                      cfg.head_dim, max_len, bs)
+    ws_bytes = decode_workspace_bytes(rows, hq, hkv, d, max_len, bs)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
-    q = torch.randn(rows, cfg.num_attention_heads, cfg.head_dim, dtype=torch.bfloat16,
-                    device=device)
+    qkv = torch.randn(rows, (hq + 2 * hkv) * d, dtype=torch.bfloat16, device=device)
+    q = qkv[:, :hq * d].view(rows, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(rows, hkv, d)
+    w = torch.ones(d, dtype=torch.bfloat16, device=device)
+    positions = torch.full((rows,), ctx - 1, device=device)
+    cos, sin = RotaryEmbedding(d, 40960, base=cfg.rope_theta, device=device)(
+        positions, torch.bfloat16)
+    slots = perm.view(rows, pages)[:, (ctx - 1) // bs] * bs + (ctx - 1) % bs
     out = torch.empty_like(q)
     for _ in range(args.steps):
-        paged_decode_attention(q, cache, 0, meta, out, scale=cfg.head_dim ** -0.5,
-                               workspace=ws)
+        paged_decode_qk_norm_rope(q, k, v, w, w, cos, sin, 1e-6, 1e-6, cache, 0, meta, slots,
+                                  out, scale=d ** -0.5, workspace=ws)
     src = torch.empty(1 << 29, dtype=torch.bfloat16, device=device)  # 1 GiB
     dst = torch.empty_like(src)
     for _ in range(3):

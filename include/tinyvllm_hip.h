@@ -93,6 +93,29 @@ int tvllm_paged_decode(const void* q, int64_t q_token_stride,
                        void* workspace, int64_t workspace_bytes,
                        int dtype, tvllm_stream_t stream);
 
+/* tvllm_qk_norm_rope's fused KV write followed by tvllm_paged_decode, in
+ * one kernel, for a step whose rows are all decode rows: q, k, v are the raw
+ * projections (element strides, last 1); each workgroup normalises and
+ * rotates its query heads in registers, and the wave whose page range holds
+ * a row's newest token (position lengths[r] - 1) writes that token's rotated
+ * K row and its V row to slot slots[rows[r]] (-1 skips) before reading it.
+ * The K rows written are bit-identical to tvllm_qk_norm_rope's. cos, sin:
+ * contiguous [tokens, 64]; q_weight, k_weight: [128]. head_dim must be 128.
+ * Replaces: the decode-step sequence qk_norm_rope + store_kv + paged_decode
+ *           (reference tinyvllm/models/qwen3.py:284-293,
+ *            runtime/attention.py:219-285); no single reference counterpart. */
+int tvllm_paged_decode_qk_norm_rope(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k,
+    int64_t k_token_stride, int64_t k_head_stride, const void* v, int64_t v_token_stride,
+    int64_t v_head_stride, const void* q_weight, const void* k_weight, const void* cos,
+    const void* sin, float q_eps, float k_eps, const int64_t* slots, void* k_cache,
+    void* v_cache, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const int64_t* rows, const int64_t* blocks, const int64_t* offsets,
+    const int64_t* lengths, int64_t num_rows, int64_t num_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t num_slots, int64_t block_size, int64_t max_context_len,
+    float scale, void* workspace, int64_t workspace_bytes, int dtype,
+    tvllm_stream_t stream);
+
 /* RMSNorm over rows of width `width`, optionally after a residual add:
  *   x = residual ? round(x + residual) : x
  *   out = round(round(x * rsqrt(mean(x^2) + eps)) * weight)

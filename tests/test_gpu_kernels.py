@@ -430,3 +430,78 @@ def test_decode_many_rows_long_context_splits(device):
     assert (out[3] == 0).all()
     assert_bf16_close(out, expect)
 
+
+
+@pytest.mark.parametrize("heads,kv_heads,lengths,max_ctx", [
+    (32, 8, [2049, 1, 700, 0, 16, 17], 4096),   # one workgroup per row, padding row
+    (64, 8, [5000, 33, 1], 32768),               # group 8; workgroup-level splits
+    (16, 8, [30000, 2], 32768),                  # the new token in the last workgroup
+])
+def test_decode_fused_qk_norm_rope_kv_write(device, heads, kv_heads, lengths, max_ctx):
+    """Fused decode step == qk_norm_rope_store + paged_decode: the cache after
+    the step is bit-identical (rotated K, copied V, slot -1 untouched) and the
+    attention output matches the unfused path and the oracle."""
+    from tinyvllm.kernels.paged_decode import paged_decode_attention, paged_decode_qk_norm_rope
+    from tinyvllm.kernels.pointwise import qk_norm_rope_store
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    g = torch.Generator().manual_seed(sum(lengths) % 1009 + heads)
+    bs, d = 16, 128
+    rows = len(lengths)
+    pages = [max(1, -(-n // bs)) for n in lengths]
+    pool = sum(pages) + 4
+    perm = torch.randperm(pool, generator=g)
+    blocks, offsets = [], [0]
+    for p in pages:
+        blocks += perm[offsets[-1]:offsets[-1] + p].tolist()
+        offsets.append(offsets[-1] + p)
+    slots = [blocks[offsets[r] + (n - 1) // bs] * bs + (n - 1) % bs if n > 0 else -1
+             for r, n in enumerate(lengths)]
+    kc = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
+    width = (heads + 2 * kv_heads) * d
+    qkv = torch.randn(rows, width, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.05 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.05 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    pos = torch.tensor([max(n - 1, 0) for n in lengths])
+    cos, sin = OP.rope_tables(pos, d, 1e6, torch.bfloat16)
+    G = lambda t: t.to(device)  # noqa: E731
+    gqkv = G(qkv)
+    q = gqkv[:, :heads * d].view(rows, heads, d)
+    k = gqkv[:, heads * d:(heads + kv_heads) * d].view(rows, kv_heads, d)
+    v = gqkv[:, (heads + kv_heads) * d:].view(rows, kv_heads, d)
+    meta = SingleQueryMetadata(G(torch.arange(rows)), G(torch.tensor(blocks)),
+                               G(torch.tensor(offsets)), G(torch.tensor(lengths)), max_ctx)
+    gslots = G(torch.tensor(slots))
+    scale = d ** -0.5
+
+    cache_a = _Cache(G(kc), G(vc), bs)
+    q_rot, _ = qk_norm_rope_store(q, k, v, G(qw), G(kw), G(cos), G(sin), 1e-6, 1e-6,
+                                  cache_a.key[0], cache_a.value[0], gslots)
+    out_a = torch.zeros(rows, heads, d, dtype=torch.bfloat16, device=device)
+    paged_decode_attention(q_rot, cache_a, 0, meta, out_a, scale=scale)
+
+    cache_b = _Cache(G(kc), G(vc), bs)
+    out_b = torch.zeros(rows, heads, d, dtype=torch.bfloat16, device=device)
+    paged_decode_qk_norm_rope(q, k, v, G(qw), G(kw), G(cos), G(sin), 1e-6, 1e-6,
+                              cache_b, 0, meta, gslots, out_b, scale=scale)
+    torch.cuda.synchronize()
+    assert torch.equal(cache_a.key[0].cpu(), cache_b.key[0].cpu())
+    assert torch.equal(cache_a.value[0].cpu(), cache_b.value[0].cpu())
+    assert_bf16_close(out_b.cpu(), out_a.cpu())
+    # and against the oracle of the whole step
+    q_ref, k_ref = OP.qk_norm_rope(qkv[:, :heads * d].view(rows, heads, d),
+                                   qkv[:, heads * d:(heads + kv_heads) * d].view(rows, kv_heads, d),
+                                   qw, kw, cos, sin)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    for r, sl in enumerate(slots):
+        if sl >= 0:
+            kc_ref[sl] = k_ref[r]
+            vc_ref[sl] = qkv[r, (heads + kv_heads) * d:].view(kv_heads, d)
+    expect = torch.zeros(rows, heads, d, dtype=torch.bfloat16)
+    OA.decode_attention(q_ref, kc_ref, vc_ref, torch.arange(rows), torch.tensor(blocks),
+                        torch.tensor(offsets), torch.tensor(lengths), bs, scale, expect)
+    assert_bf16_close(out_b.cpu(), expect)
+    for r, n in enumerate(lengths):
+        if n == 0:
+            assert (out_b[r].cpu() == 0).all()

@@ -118,6 +118,21 @@ struct DecodeArgs {
     float scale_log2;   // softmax scale * log2(e): scores live in base 2
     float* part_o;      // [rows, heads, grid_splits, 128] (grid_splits > 1)
     float* part_ml;     // [rows, heads, grid_splits, 2]
+    // Fused QK-norm + RoPE + KV write (FUSED kernels only): q above is the
+    // raw projection; the row's new K/V come from kraw/vraw (token strides,
+    // head strides), are normalised/rotated and written to slot slots[tok].
+    const T* kraw;
+    int64_t krts, krhs;
+    const T* vraw;
+    int64_t vrts, vrhs;
+    const T* qw;
+    const T* kw;
+    const T* cos_t;     // [tokens, 64]
+    const T* sin_t;
+    float q_eps, k_eps;
+    T* kcache;          // writable views of k / v
+    T* vcache;
+    const int64_t* slots;
 };
 
 constexpr int kMaxWaves = 8;  // 2 resident waves per SIMD at <= 256 VGPRs
@@ -127,11 +142,81 @@ __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);  // v_exp_f32; inputs here are <= 0
 }
 
+// Fused QK-norm + RoPE for the decode step (head_dim 128), with the
+// rounding points of the standalone kernel (reference pointwise.cu:325-450):
+//   n = round(round(x * rsqrt(mean(x^2) + eps)) * w);
+//   o1 = round(round(n1*cos) - round(n2*sin)), o2 = round(round(n2*cos) + round(n1*sin)).
+// Query: in place on the MFMA B operand (lane = head col, quad; dims c*32 +
+// quad*8 + e), the sum of squares reduced over the four quads.
+template <typename T>
+__device__ __forceinline__ void rope_query(U16x8 (&qb)[4], const T* __restrict__ w,
+                                           const T* __restrict__ cs,
+                                           const T* __restrict__ sn, float eps, int quad) {
+    float x[4][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        unpack8<T>(qb[c], x[c]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[c][e] * x[c][e];
+    }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    const float inv = rsqrtf(ss * (1.0f / 128.f) + eps);
+    float wv[4][8], cv[2][8], sv[2][8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        unpack8<T>(*reinterpret_cast<const U16x8*>(w + c * 32 + quad * 8), wv[c]);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        unpack8<T>(*reinterpret_cast<const U16x8*>(cs + c * 32 + quad * 8), cv[c]);
+        unpack8<T>(*reinterpret_cast<const U16x8*>(sn + c * 32 + quad * 8), sv[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        float o1[8], o2[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float n1 = rnd<T>(rnd<T>(x[c][e] * inv) * wv[c][e]);
+            const float n2 = rnd<T>(rnd<T>(x[c + 2][e] * inv) * wv[c + 2][e]);
+            o1[e] = rnd<T>(n1 * cv[c][e]) - rnd<T>(n2 * sv[c][e]);
+            o2[e] = rnd<T>(n2 * cv[c][e]) + rnd<T>(n1 * sv[c][e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            qb[c].w[e] = pack2<T>(o1[2 * e], o1[2 * e + 1]);
+            qb[c + 2].w[e] = pack2<T>(o2[2 * e], o2[2 * e + 1]);
+        }
+    }
+}
+
+// New K row: normalised and rotated exactly as the standalone kernel does
+// (lane l owns the pair (l, l + 64), one wave-wide sum of squares), written
+// with the V row into the cache slot.
+template <typename T>
+__device__ __forceinline__ void write_new_kv(const T* __restrict__ k, const T* __restrict__ v,
+                                             const T* __restrict__ w, const T* __restrict__ cs,
+                                             const T* __restrict__ sn, float eps,
+                                             T* __restrict__ kdst, T* __restrict__ vdst,
+                                             int lane) {
+    const float x1 = to_f<T>(k[lane]), x2 = to_f<T>(k[lane + 64]);
+    const float w1 = to_f<T>(w[lane]), w2 = to_f<T>(w[lane + 64]);
+    const float c = to_f<T>(cs[lane]), s = to_f<T>(sn[lane]);
+    const float ss = wave_sum(x1 * x1 + x2 * x2);
+    const float inv = rsqrtf(ss * (1.0f / 128.f) + eps);
+    const float n1 = rnd<T>(rnd<T>(x1 * inv) * w1);
+    const float n2 = rnd<T>(rnd<T>(x2 * inv) * w2);
+    kdst[lane] = static_cast<T>(rnd<T>(n1 * c) - rnd<T>(n2 * s));
+    kdst[lane + 64] = static_cast<T>(rnd<T>(n2 * c) + rnd<T>(n1 * s));
+    vdst[lane] = v[lane];
+    vdst[lane + 64] = v[lane + 64];
+}
+
 // GP: group size rounded up to a power of two (<= 16); NT: 16-token MFMA
 // tiles per iteration. Wave w of a workgroup owns KV head
 // (group of the workgroup) * heads_per_wg + w / splits and page range
 // w % splits of its row.
-template <typename T, int GP, int NT, int MAXW>
+template <typename T, int GP, int NT, int MAXW, bool FUSED>
 __global__ void __launch_bounds__(64 * MAXW)
 paged_decode_d128(DecodeArgs<T> a) {
     constexpr int D = 128;
@@ -206,6 +291,25 @@ paged_decode_d128(DecodeArgs<T> a) {
                 }
             }
         }
+        if constexpr (FUSED) {
+            // The row's new token (position length - 1) is written by the
+            // wave whose page range holds it, before that wave reads it.
+            if (t_begin <= length - 1 && length - 1 < t_end) {
+                const int64_t slot = a.slots[row];
+                if (slot >= 0) {
+                    write_new_kv<T>(a.kraw + row * a.krts + kvh * a.krhs,
+                                    a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
+                                    a.cos_t + row * 64, a.sin_t + row * 64, a.k_eps,
+                                    a.kcache + (slot * a.kv_heads + kvh) * D,
+                                    a.vcache + (slot * a.kv_heads + kvh) * D, lane);
+                    // Only this wave reads the row, and no CU has it cached
+                    // (caches start clean per dispatch): a workgroup-scope
+                    // release (store completion, no cache write-back) orders
+                    // the stores before this wave's loads.
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                }
+            }
+        }
 
         // Lane x resolves the cache row (16-byte units) of chunk token t0 + x,
         // clamped to the last valid token so masked lanes read mapped memory.
@@ -243,6 +347,13 @@ paged_decode_d128(DecodeArgs<T> a) {
             const uint32_t first = resolve(t_begin);
             load_k(first);
             load_v(first);
+        }
+        if constexpr (FUSED) {
+            // QK-norm + RoPE of the raw query while the first K/V rows are in
+            // flight, in the B-operand layout: lane (head col, quad) holds dims
+            // c*32 + quad*8 + e; the RoPE pair of dim d < 64 is d + 64, two
+            // k-slices up in the same lane.
+            rope_query<T>(qb, a.qw, a.cos_t + row * 64, a.sin_t + row * 64, a.q_eps, quad);
         }
         for (int64_t t0 = t_begin; t0 < t_end; t0 += CH) {
             const bool has_next = t0 + CH < t_end;
@@ -601,14 +712,30 @@ extern "C" int64_t tvllm_paged_decode_workspace_size(int64_t num_rows,
     return num_rows * num_heads * p.grid * (head_dim + 2) * int64_t(sizeof(float));
 }
 
-extern "C" int tvllm_paged_decode(
+namespace tvllm {
+namespace {
+
+struct FusedIn {
+    const void* k;
+    int64_t kts, khs;
+    const void* v;
+    int64_t vts, vhs;
+    const void* qw;
+    const void* kw;
+    const void* cos;
+    const void* sin;
+    float q_eps, k_eps;
+    const int64_t* slots;
+};
+
+int paged_decode_impl(
     const void* q, int64_t q_token_stride, int64_t q_head_stride,
     const void* k_cache, const void* v_cache, void* out, int64_t out_token_stride,
     int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
     const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
     int64_t block_size, int64_t max_context_len, float scale, void* workspace,
-    int64_t workspace_bytes, int dtype, tvllm_stream_t stream) {
+    int64_t workspace_bytes, int dtype, tvllm_stream_t stream, const FusedIn* fused) {
     TVLLM_CHECK(head_dim > 0 && head_dim <= 256 && num_heads > 0 && num_kv_heads > 0,
                 "paged_decode: invalid attention head geometry");
     TVLLM_CHECK(num_heads % num_kv_heads == 0 && block_size > 0 &&
@@ -626,9 +753,13 @@ extern "C" int tvllm_paged_decode(
 
     return dispatch_half(dtype, [&]<int DT>() {
         using T = typename Elem<DT>::T;
-        if (!fast_path(head_dim, group, q, q_token_stride, q_head_stride, out,
-                       out_token_stride, out_head_stride, k_cache, v_cache,
-                       num_slots, num_kv_heads)) {
+        const bool fast = fast_path(head_dim, group, q, q_token_stride, q_head_stride, out,
+                                    out_token_stride, out_head_stride, k_cache, v_cache,
+                                    num_slots, num_kv_heads);
+        TVLLM_CHECK(fused == nullptr || fast,
+                    "paged_decode_qk_norm_rope: needs head_dim 128, group <= 16 and "
+                    "16-byte aligned rows");
+        if (!fast) {
             paged_decode_generic<T><<<int(num_rows * num_heads), 64, 0, s>>>(
                 static_cast<const T*>(q), q_token_stride, q_head_stride,
                 static_cast<const T*>(k_cache), static_cast<const T*>(v_cache),
@@ -677,24 +808,48 @@ extern "C" int tvllm_paged_decode(
         args.part_o = static_cast<float*>(workspace);
         args.part_ml = need ? args.part_o + num_rows * num_heads * plan.grid * head_dim
                             : nullptr;
+        args.kraw = nullptr;
+        args.vraw = nullptr;
+        args.slots = nullptr;
+        if (fused) {
+            args.kraw = static_cast<const T*>(fused->k);
+            args.krts = fused->kts;
+            args.krhs = fused->khs;
+            args.vraw = static_cast<const T*>(fused->v);
+            args.vrts = fused->vts;
+            args.vrhs = fused->vhs;
+            args.qw = static_cast<const T*>(fused->qw);
+            args.kw = static_cast<const T*>(fused->kw);
+            args.cos_t = static_cast<const T*>(fused->cos);
+            args.sin_t = static_cast<const T*>(fused->sin);
+            args.q_eps = fused->q_eps;
+            args.k_eps = fused->k_eps;
+            args.kcache = static_cast<T*>(const_cast<void*>(k_cache));
+            args.vcache = static_cast<T*>(const_cast<void*>(v_cache));
+            args.slots = fused->slots;
+        }
 
-#define TVLLM_DEC(GP)                                                           \
-    do {                                                                        \
-        if (tuning().tiles == 4 && threads <= 256)                              \
-            paged_decode_d128<T, GP, 4, 4><<<int(grid), threads, 0, s>>>(args); \
-        else                                                                    \
-            paged_decode_d128<T, GP, 2, kMaxWaves>                              \
-                <<<int(grid), threads, 0, s>>>(args);                           \
+        auto launch = [&]<bool F>() {
+#define TVLLM_DEC(GP)                                                                \
+    do {                                                                             \
+        if (tuning().tiles == 4 && threads <= 256)                                   \
+            paged_decode_d128<T, GP, 4, 4, F><<<int(grid), threads, 0, s>>>(args);    \
+        else                                                                         \
+            paged_decode_d128<T, GP, 2, kMaxWaves, F>                                \
+                <<<int(grid), threads, 0, s>>>(args);                                \
     } while (0)
-        // Groups above 4 carry 64+ accumulator registers per lane: one
-        // 16-token tile per iteration keeps them within 256 VGPRs.
-        if (group <= 1) TVLLM_DEC(1);
-        else if (group <= 2) TVLLM_DEC(2);
-        else if (group <= 4) TVLLM_DEC(4);
-        else if (group <= 8)
-            paged_decode_d128<T, 8, 1, kMaxWaves><<<int(grid), threads, 0, s>>>(args);
-        else
-            paged_decode_d128<T, 16, 1, kMaxWaves><<<int(grid), threads, 0, s>>>(args);
+            // Groups above 4 carry 64+ accumulator registers per lane: one
+            // 16-token tile per iteration keeps them within 256 VGPRs.
+            if (group <= 1) TVLLM_DEC(1);
+            else if (group <= 2) TVLLM_DEC(2);
+            else if (group <= 4) TVLLM_DEC(4);
+            else if (group <= 8)
+                paged_decode_d128<T, 8, 1, kMaxWaves, F><<<int(grid), threads, 0, s>>>(args);
+            else
+                paged_decode_d128<T, 16, 1, kMaxWaves, F><<<int(grid), threads, 0, s>>>(args);
+        };
+        if (fused) launch.template operator()<true>();
+        else launch.template operator()<false>();
 #undef TVLLM_DEC
         const int st = launch_status("paged_decode");
         if (st != TVLLM_OK || plan.grid <= 1) return st;
@@ -703,4 +858,47 @@ extern "C" int tvllm_paged_decode(
             out_head_stride, int(num_heads), int(plan.grid), int(head_dim));
         return launch_status("paged_decode merge");
     });
+}
+
+}  // namespace
+}  // namespace tvllm
+
+extern "C" int tvllm_paged_decode(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride,
+    const void* k_cache, const void* v_cache, void* out, int64_t out_token_stride,
+    int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
+    const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
+    int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
+    int64_t block_size, int64_t max_context_len, float scale, void* workspace,
+    int64_t workspace_bytes, int dtype, tvllm_stream_t stream) {
+    return paged_decode_impl(q, q_token_stride, q_head_stride, k_cache, v_cache, out,
+                             out_token_stride, out_head_stride, rows, blocks, offsets,
+                             lengths, num_rows, num_heads, num_kv_heads, head_dim,
+                             num_slots, block_size, max_context_len, scale, workspace,
+                             workspace_bytes, dtype, stream, nullptr);
+}
+
+extern "C" int tvllm_paged_decode_qk_norm_rope(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride, const void* k,
+    int64_t k_token_stride, int64_t k_head_stride, const void* v, int64_t v_token_stride,
+    int64_t v_head_stride, const void* q_weight, const void* k_weight, const void* cos,
+    const void* sin, float q_eps, float k_eps, const int64_t* slots, void* k_cache,
+    void* v_cache, void* out, int64_t out_token_stride, int64_t out_head_stride,
+    const int64_t* rows, const int64_t* blocks, const int64_t* offsets,
+    const int64_t* lengths, int64_t num_rows, int64_t num_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t num_slots, int64_t block_size, int64_t max_context_len,
+    float scale, void* workspace, int64_t workspace_bytes, int dtype,
+    tvllm_stream_t stream) {
+    TVLLM_CHECK(head_dim == 128, "paged_decode_qk_norm_rope: head_dim must be 128");
+    TVLLM_CHECK(num_rows == 0 || (k && v && q_weight && k_weight && cos && sin && slots),
+                "paged_decode_qk_norm_rope: null pointer");
+    TVLLM_CHECK(aligned16(q_weight) && aligned16(cos) && aligned16(sin),
+                "paged_decode_qk_norm_rope: weights and RoPE tables must be 16-byte aligned");
+    const FusedIn f{k, k_token_stride, k_head_stride, v, v_token_stride, v_head_stride,
+                    q_weight, k_weight, cos, sin, q_eps, k_eps, slots};
+    return paged_decode_impl(q, q_token_stride, q_head_stride, k_cache, v_cache, out,
+                             out_token_stride, out_head_stride, rows, blocks, offsets,
+                             lengths, num_rows, num_heads, num_kv_heads, head_dim,
+                             num_slots, block_size, max_context_len, scale, workspace,
+                             workspace_bytes, dtype, stream, &f);
 }

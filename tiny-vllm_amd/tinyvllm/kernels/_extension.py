@@ -35,6 +35,11 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_paged_decode": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64,
                                   _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                   _I64, _I64, _I64, _F32, _P, _I64, _INT, _P]),
+    "tvllm_paged_decode_qk_norm_rope": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64,
+                                               _I64, _P, _P, _P, _P, _F32, _F32, _P, _P,
+                                               _P, _P, _I64, _I64, _P, _P, _P, _P, _I64,
+                                               _I64, _I64, _I64, _I64, _I64, _I64, _F32,
+                                               _P, _I64, _INT, _P]),
     "tvllm_rms_norm": (_INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64,
                               _P, _P, _F32, _INT, _P]),
     "tvllm_silu_and_mul": (_INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _INT, _P]),

@@ -79,3 +79,80 @@ def paged_decode_attention(
         workspace.data_ptr() if need else None, need,
         dtype_code(q.dtype), stream_of(device),
     ))
+
+
+def paged_decode_qk_norm_rope(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    query_weight: torch.Tensor,
+    key_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    query_eps: float,
+    key_eps: float,
+    cache: PagedKVCache,
+    layer_idx: int,
+    metadata: SingleQueryMetadata,
+    slots: torch.Tensor,
+    output: torch.Tensor,
+    *,
+    scale: float,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """One decode step's QK-norm + RoPE, slot-mapped KV write and paged
+    attention in one kernel (no reference counterpart: it replaces
+    qk_norm_rope + store_kv + paged_decode_attention when every row is a
+    decode row). ``q``/``k``/``v`` are the raw projections [tokens, heads,
+    128]; ``cos``/``sin`` the [tokens, 1, 64] RoPE tables; ``slots`` the
+    write slot of each token (-1 skips); ``metadata.query_rows`` index those
+    tokens. The K rows written equal ``qk_norm_rope_store``'s bit for bit."""
+    lib = load_kernels()
+    kc, vc = cache.key[layer_idx], cache.value[layer_idx]
+    m = metadata
+    device = require_gpu(q, k, v, query_weight, key_weight, cos, sin, slots, kc, output,
+                         m.query_rows, m.block_table_ids, m.block_table_offsets,
+                         m.context_lens)
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape or q.shape[2] != 128:
+        raise RuntimeError("Q/K/V must be [tokens, heads, 128] tensors")
+    if q.dtype not in (torch.float16, torch.bfloat16) or any(
+            t.dtype != q.dtype for t in (k, v, query_weight, key_weight, cos, sin, kc, output)):
+        raise RuntimeError("Q/K/V, weights, RoPE tables and cache must share a half dtype")
+    if any(t.stride(-1) != 1 for t in (q, k, v, output)) or output.shape != q.shape:
+        raise RuntimeError("Q/K/V/output rows must have unit last stride")
+    if (query_weight.shape != (128,) or key_weight.shape != (128,)
+            or not query_weight.is_contiguous() or not key_weight.is_contiguous()):
+        raise RuntimeError("norm weights must be contiguous [128]")
+    tokens = q.shape[0]
+    for table in (cos, sin):
+        if table.numel() != tokens * 64 or not table.is_contiguous():
+            raise RuntimeError("RoPE tables must be contiguous [tokens, 1, 64]")
+    if (slots.dtype != torch.long or slots.dim() != 1 or not slots.is_contiguous()
+            or slots.numel() != tokens):
+        raise RuntimeError("slots must be contiguous int64 [tokens]")
+    for tensor in (m.query_rows, m.block_table_ids, m.block_table_offsets, m.context_lens):
+        if tensor.dtype != torch.long or tensor.dim() != 1 or not tensor.is_contiguous():
+            raise RuntimeError("metadata must be contiguous GPU int64 vectors")
+    num_rows = m.query_rows.numel()
+    if m.context_lens.numel() != num_rows or m.block_table_offsets.numel() != num_rows + 1:
+        raise RuntimeError("metadata lengths must align")
+    if num_rows == 0:
+        return
+    heads = q.shape[1]
+    max_len = m.max_context_len or cache.num_slots
+    need = int(lib.tvllm_paged_decode_workspace_size(
+        num_rows, heads, cache.num_kv_heads, 128, max_len, cache.block_size))
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    check(lib.tvllm_paged_decode_qk_norm_rope(
+        q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1), query_weight.data_ptr(),
+        key_weight.data_ptr(), cos.data_ptr(), sin.data_ptr(), float(query_eps),
+        float(key_eps), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), output.data_ptr(),
+        output.stride(0), output.stride(1), m.query_rows.data_ptr(),
+        m.block_table_ids.data_ptr(), m.block_table_offsets.data_ptr(),
+        m.context_lens.data_ptr(), num_rows, heads, cache.num_kv_heads, 128,
+        cache.num_slots, cache.block_size, max_len, float(scale),
+        workspace.data_ptr() if need else None, need, dtype_code(q.dtype),
+        stream_of(device),
+    ))

@@ -2,7 +2,9 @@
 (reference: tinyvllm/runtime/attention.py:12-348).
 
 ``HipAttention`` (the default, "hip") runs everything on the gfx950 kernels:
-  * ``prepare_qkv``: QK-norm + RoPE with the slot-mapped KV write fused in;
+  * decode-only steps: one kernel per layer does QK-norm + RoPE, the
+    slot-mapped KV write and split-K paged decode attention;
+  * other steps, ``prepare_qkv``: QK-norm + RoPE with the KV write fused in;
   * decode rows (query length 1): split-K paged decode attention;
   * multi-query rows (fresh prompts and chunks with history): MFMA paged
     prefill attention, reading the just-written chunk from the cache too.
@@ -16,7 +18,7 @@ import torch
 import torch.nn.functional as F
 
 from tinyvllm.kernels.kv_store import store_kv
-from tinyvllm.kernels.paged_decode import paged_decode_attention
+from tinyvllm.kernels.paged_decode import paged_decode_attention, paged_decode_qk_norm_rope
 from tinyvllm.kernels.paged_prefill import paged_prefill_attention
 from tinyvllm.kernels.pointwise import qk_norm_rope, qk_norm_rope_store
 from tinyvllm.paged_kv import PagedKVCache
@@ -34,10 +36,16 @@ class HipAttention:
         self.cache = cache
         self.decode_workspace = decode_workspace
         self._written_layer = -1
+        self._fused = None
 
     def prepare_qkv(self, layer_idx, q, k, v, q_weight, k_weight, cos, sin, q_eps, k_eps):
-        """Normalise/rotate Q and K and write K/V into their cache slots in
-        one kernel; returns (q, None, None) - K/V now live in the cache."""
+        """Decode-only steps: keep the raw Q/K/V for the fused decode kernel
+        (QK-norm + RoPE + KV write + attention in one launch). Otherwise
+        normalise/rotate Q and K and write K/V into their cache slots in one
+        kernel and return (q, None, None) - K/V now live in the cache."""
+        if self.kv.prefill is None and self.kv.decode is not None:
+            self._fused = (layer_idx, k, v, q_weight, k_weight, cos, sin, q_eps, k_eps)
+            return q, None, None
         q, _ = qk_norm_rope_store(
             q, k, v, q_weight, k_weight, cos, sin, q_eps, k_eps,
             self.cache.key[layer_idx], self.cache.value[layer_idx], self.kv.slot_mapping,
@@ -47,9 +55,17 @@ class HipAttention:
 
     def __call__(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor | None,
                  v: torch.Tensor | None, *, scale: float) -> torch.Tensor:
+        output = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        fused, self._fused = self._fused, None
+        if fused is not None and fused[0] == layer_idx:
+            _, k_raw, v_raw, qw, kw, cos, sin, q_eps, k_eps = fused
+            paged_decode_qk_norm_rope(q, k_raw, v_raw, qw, kw, cos, sin, q_eps, k_eps,
+                                      self.cache, layer_idx, self.kv.decode,
+                                      self.kv.slot_mapping, output, scale=scale,
+                                      workspace=self.decode_workspace)
+            return output
         if self._written_layer != layer_idx:
             store_kv(self.cache, layer_idx, self.kv.slot_mapping, k, v)
-        output = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         if self.kv.decode is not None:
             paged_decode_attention(q, self.cache, layer_idx, self.kv.decode, output,
                                    scale=scale, workspace=self.decode_workspace)
