@@ -578,7 +578,7 @@ def op_prefill(args) -> dict:
     return result
 
 
-OPS = {"c1": op_c1, "c2": op_c2, "prefill": op_prefill}
+OPS = {"c1": op_c1, "c2": op_c2, "prefill": op_prefill, "published": lambda args: published(args)}
 
 
 E2E = {
@@ -661,6 +661,106 @@ def end_to_end(name: str, args) -> None:
             k: v for k, v in spec.items() if k != "model"}},
     }), flush=True)
     engine.close()
+
+
+# The reference's published serving scenarios (README performance.svg /
+# arrivals-performance.svg: Qwen3-0.6B bf16, CUDA graphs + prefix caching,
+# 896 MiB of KV; RTX 5060 Laptop), with its numbers: (TTFT ms, TPOT ms/tok,
+# output tok/s).
+PUBLISHED = {
+    "1 request, 64->128": (dict(prompts=[64], new=128), (7.12, 4.73, 210.8)),
+    "4 requests, 64->128": (dict(prompts=[64] * 4, new=128), (13.31, 4.90, 805.3)),
+    "16 requests, 64->128": (dict(prompts=[64] * 16, new=128), (37.18, 5.75, 2668.8)),
+    "Long 4 req, 1024->32": (dict(prompts=[1024] * 4, new=32), (82.80, 6.27, 345.9)),
+    "Mixed 4 req, 64/512->64": (dict(prompts=[64, 512] * 2, new=64), (39.52, 5.48, 655.9)),
+    "Arrivals 16 req, 64/512->64, 20 ms": (dict(prompts=[64, 512] * 8, new=64, gap_ms=20.0),
+                                          (22.76, 8.34, 1369.4)),
+    "Shared prefix cold, 4x832->64": (dict(prompts=[832] * 4, new=64, shared=768),
+                                      (61.75, 5.73, 604.9)),
+    "Shared prefix warm, 4x832->64": (dict(prompts=[832] * 4, new=64, shared=768, warm=True),
+                                      (19.26, 5.74, 672.2)),
+}
+
+
+def run_requests(engine, prompts, new: int, gap_ns: int):
+    """Submit ``prompts`` (arrivals ``gap_ns`` apart), step the engine to
+    completion; (mean TTFT ms, mean TPOT ms/token, output tok/s)."""
+    import numpy as np
+    import torch
+
+    from tinyvllm import SamplingParams
+
+    params = SamplingParams(max_new_tokens=new, ignore_eos=True)
+    torch.cuda.synchronize()
+    start = time.monotonic_ns()
+    for i, prompt in enumerate(prompts):
+        engine.submit(prompt, params, arrival_ns=start + i * gap_ns)
+    done = []
+    while engine.has_unfinished():
+        events = engine.step()
+        done += events.completion_events
+        if not events.token_events and not events.completion_events:
+            arrival = engine.scheduler.next_arrival_ns
+            if arrival is not None:
+                time.sleep(max(0.0, (arrival - time.monotonic_ns()) / 1e9))
+    end = max(e.finished_ns for e in done)
+    ttft = [(e.first_token_ns - e.arrival_ns) / 1e6 for e in done]
+    tpot = [(e.finished_ns - e.first_token_ns) / 1e6 / max(1, len(e.output_token_ids) - 1)
+            for e in done]
+    out = sum(len(e.output_token_ids) for e in done)
+    return float(np.mean(ttft)), float(np.mean(tpot)), out / ((end - start) / 1e9)
+
+
+def published(args) -> dict:
+    """The reference's published Qwen3-0.6B serving scenarios through this
+    engine (random-init weights, random token ids, greedy, ignore_eos):
+    mean TTFT and TPOT over requests and output tok/s over the makespan,
+    median of ``replays``; the reference's numbers (other hardware) beside."""
+    import numpy as np
+    import torch
+
+    from tinyvllm.bootstrap import build_engine
+    from tinyvllm.models.qwen3 import Qwen3ForCausalLM
+    from tinyvllm.paged_kv import PagedKVCache
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    cfg = qwen3_config("qwen3-0.6b", max_position=40960)
+    model = Qwen3ForCausalLM.random_init(cfg, device=device, dtype=torch.bfloat16, seed=0)
+    per_block = PagedKVCache.bytes_per_block(
+        num_layers=cfg.num_hidden_layers, block_size=16, num_kv_heads=cfg.num_key_value_heads,
+        head_dim=cfg.head_dim, dtype=torch.bfloat16)
+    blocks = (896 << 20) // per_block  # the reference's equal KV storage
+    engine = build_engine(model, max_model_len=2048, max_num_seqs=64, num_blocks=blocks,
+                          max_num_batched_tokens=4096, prefill_chunk_size=512)
+    rng = np.random.default_rng(0)
+    replays = 3
+    result = {}
+    for name, (spec, ref) in PUBLISHED.items():
+        runs = []
+        for rep in range(replays + 1):  # the first pass warms up (not counted)
+            engine.reset_prefix_cache()
+            shared = rng.integers(0, cfg.vocab_size, size=spec.get("shared", 0)).tolist()
+
+            def prompts():
+                return [shared + rng.integers(0, cfg.vocab_size,
+                                              size=n - len(shared)).tolist()
+                        for n in spec["prompts"]]
+
+            if spec.get("warm"):  # the shared prefix is computed once, untimed
+                run_requests(engine, prompts(), spec["new"], 0)
+            runs.append(run_requests(engine, prompts(), spec["new"],
+                                     int(spec.get("gap_ms", 0.0) * 1e6)))
+        runs = runs[1:]
+        med = [float(np.median([r[i] for r in runs])) for i in range(3)]
+        result[name] = {"ttft_ms": round(med[0], 2), "tpot_ms": round(med[1], 3),
+                        "out_tok_s": round(med[2], 1),
+                        "reference_rtx5060_laptop": {"ttft_ms": ref[0], "tpot_ms": ref[1],
+                                                     "out_tok_s": ref[2]},
+                        "out_tok_s_vs_reference": round(med[2] / ref[2], 2)}
+        print(f"[published] {name}: {result[name]}", file=sys.stderr, flush=True)
+    engine.close()
+    return result
 
 
 def main() -> None:

@@ -67,6 +67,16 @@ int64_t tvllm_paged_decode_workspace_size(int64_t num_rows, int64_t num_heads,
                                           int64_t max_context_len,
                                           int64_t block_size);
 
+/* The split-K decomposition tvllm_paged_decode uses for this geometry,
+ * packed as (waves per KV head << 16) | (workgroups per row << 8) | (KV heads
+ * per workgroup); 0 for the generic path. It depends on max_context_len, so a
+ * caller that bakes launches (graph capture) can tell when a tighter context
+ * bound would change it. No reference counterpart (the reference kernel has
+ * no split-K). */
+int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
+                                      int64_t num_kv_heads, int64_t head_dim,
+                                      int64_t max_context_len, int64_t block_size);
+
 /* Single-query paged attention for decode rows.
  * For r < num_rows, h < num_heads:
  *   out[rows[r], h] = softmax_t(scale * q[rows[r], h] . k_t) @ v_t,

@@ -696,6 +696,18 @@ bool fast_path(int64_t head_dim, int64_t group, const void* q, int64_t qts,
 
 using namespace tvllm;
 
+extern "C" int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
+                                                 int64_t num_kv_heads, int64_t head_dim,
+                                                 int64_t max_context_len,
+                                                 int64_t block_size) {
+    (void)num_heads;
+    if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || head_dim != 128 ||
+        max_context_len <= 0)
+        return 0;
+    const SplitPlan p = plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
+    return (p.waves << 16) | (p.grid << 8) | int64_t(p.heads);
+}
+
 extern "C" int64_t tvllm_paged_decode_workspace_size(int64_t num_rows,
                                                      int64_t num_heads,
                                                      int64_t num_kv_heads,

@@ -32,6 +32,7 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_store_kv": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, _P,
                               _I64, _I64, _I64, _I64, _INT, _P]),
     "tvllm_paged_decode_workspace_size": (_I64, [_I64] * 6),
+    "tvllm_paged_decode_split_plan": (_I64, [_I64] * 6),
     "tvllm_paged_decode": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64,
                                   _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                   _I64, _I64, _I64, _F32, _P, _I64, _INT, _P]),

@@ -21,6 +21,17 @@ def decode_workspace_bytes(
     ))
 
 
+def decode_split_plan(
+    num_rows: int, num_heads: int, num_kv_heads: int, head_dim: int,
+    max_context_len: int, block_size: int,
+) -> int:
+    """Opaque id of the split-K decomposition for this geometry (equal ids:
+    identical launches)."""
+    return int(load_kernels().tvllm_paged_decode_split_plan(
+        num_rows, num_heads, num_kv_heads, head_dim, max_context_len, block_size,
+    ))
+
+
 def paged_decode_attention(
     q: torch.Tensor,
     cache: PagedKVCache,

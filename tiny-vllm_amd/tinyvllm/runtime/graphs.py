@@ -14,10 +14,19 @@ from __future__ import annotations
 
 import torch
 
+from tinyvllm.kernels.paged_decode import decode_split_plan
 from tinyvllm.kernels.sampling import sample
 from tinyvllm.paged_kv import PagedKVCache
 from tinyvllm.runtime.attention import HipAttention
 from tinyvllm.runtime.inputs import DecodeInputs
+
+
+def context_buckets(max_model_len: int) -> tuple[int, ...]:
+    """Context bounds a bucket's graphs are captured for: the decode kernel's
+    split-K plan depends on the bound, and a graph baked for max_model_len
+    over-splits short contexts (few rows at 64 tokens would run 64 splits
+    and a merge launch per layer)."""
+    return tuple(sorted({b for b in (256, 1024, 4096) if b < max_model_len} | {max_model_len}))
 
 
 def bucket_sizes(limit: int) -> tuple[int, ...]:
@@ -36,7 +45,9 @@ class DecodeGraphs:
 
     def __init__(self, stream: torch.cuda.Stream) -> None:
         self.stream = stream
-        self.entries: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
+        # size -> [(context bound, graph, logits, tokens)] ascending by bound
+        self.entries: dict[int, list[tuple[int, torch.cuda.CUDAGraph, torch.Tensor,
+                                           torch.Tensor]]] = {}
         self.tokens: torch.Tensor | None = None
         self.pool = None
 
@@ -68,25 +79,8 @@ class DecodeGraphs:
         try:
             with torch.cuda.stream(side):
                 for size in reversed(sizes):
-                    model_input = inputs.view(size)
-                    params = inputs.sampling_views(size)
-                    out = self.tokens[:size]
-
-                    def step():
-                        attention = HipAttention(model_input, cache, decode_workspace=workspace)
-                        hidden = model(model_input.input_ids, model_input.positions,
-                                       attention=attention)
-                        logits = model.compute_logits(hidden)
-                        sample(logits, *params, out=out)
-                        return logits
-
-                    for _ in range(2):
-                        step()
-                    side.synchronize()
-                    graph = torch.cuda.CUDAGraph()
-                    with torch.cuda.graph(graph, pool=self.pool, stream=side):
-                        logits = step()
-                    self.entries[size] = (graph, logits, out)
+                    for bound in self._bounds(model, inputs, cache, size):
+                        self._capture_one(model, inputs, cache, workspace, size, bound, side)
         finally:
             side.synchronize()
             # Leave the padding state behind for the first real batch.
@@ -95,18 +89,62 @@ class DecodeGraphs:
             torch.cuda.current_stream(inputs.device).synchronize()
         self.entries = dict(sorted(self.entries.items()))
 
+    @staticmethod
+    def _bounds(model, inputs: DecodeInputs, cache: PagedKVCache, size: int) -> list[int]:
+        """Context bounds needing their own graph at this size: within a run
+        of bounds with the same split plan, the largest serves them all."""
+        cfg = model.config
+        bounds: list[int] = []
+        last = None
+        for bound in reversed(context_buckets(inputs.max_model_len)):
+            plan = decode_split_plan(size, cfg.num_attention_heads, cache.num_kv_heads,
+                                     cache.head_dim, bound, cache.block_size)
+            if plan != last:
+                bounds.append(bound)
+                last = plan
+        return sorted(bounds)
+
+    def _capture_one(self, model, inputs, cache, workspace, size, bound, side) -> None:
+        model_input = inputs.view(size, max_context_len=bound)
+        params = inputs.sampling_views(size)
+        out = self.tokens[:size]
+
+        def step():
+            attention = HipAttention(model_input, cache, decode_workspace=workspace)
+            hidden = model(model_input.input_ids, model_input.positions, attention=attention)
+            logits = model.compute_logits(hidden)
+            sample(logits, *params, out=out)
+            return logits
+
+        for _ in range(2):
+            step()
+        side.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=self.pool, stream=side):
+            logits = step()
+        self.entries.setdefault(size, []).append((bound, graph, logits, out))
+        self.entries[size].sort(key=lambda e: e[0])
+
     def bucket(self, count: int) -> int | None:
         for size in self.entries:
             if count <= size:
                 return size
         return None
 
-    def replay(self, count: int) -> tuple[torch.Tensor, torch.Tensor] | None:
-        """Replay the smallest graph that fits; (logits[:count], tokens[:count])."""
+    def replay(self, count: int, max_context: int | None = None
+               ) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """Replay the smallest graph that fits ``count`` rows whose contexts
+        are at most ``max_context`` (None: the largest bound);
+        (logits[:count], tokens[:count])."""
         size = self.bucket(count)
         if size is None:
             return None
-        graph, logits, tokens = self.entries[size]
+        entries = self.entries[size]
+        chosen = entries[-1] if max_context is None else next(
+            (e for e in entries if max_context <= e[0]), None)
+        if chosen is None:
+            return None
+        _, graph, logits, tokens = chosen
         graph.replay()
         return logits[:count], tokens[:count]
 

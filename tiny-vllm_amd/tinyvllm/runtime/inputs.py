@@ -128,10 +128,13 @@ class DecodeInputs:
         self.device_data[:size].copy_(self.host[:size], non_blocking=True)
         self.upload_done.record(self.stream)
         self.uploaded = True
-        return self.view(count, table_size)
+        return self.view(count, table_size, max(batch.context_lens_after))
 
-    def view(self, count: int, table_size: int | None = None) -> ModelInput:
-        """Borrow fixed storage; graph capture uses the full table capacity."""
+    def view(self, count: int, table_size: int | None = None,
+             max_context_len: int | None = None) -> ModelInput:
+        """Borrow fixed storage; graph capture uses the full table capacity.
+        ``max_context_len`` bounds every row's context (default: the
+        engine's max_model_len); it only sizes the decode split-K plan."""
         d = self.d
         table = d["blocks"] if table_size is None else d["blocks"][:table_size]
         rows = self.rows[:count]
@@ -146,7 +149,7 @@ class DecodeInputs:
                     block_table_ids=table,
                     block_table_offsets=d["offsets"][:count + 1],
                     context_lens=d["lengths"][:count],
-                    max_context_len=self.max_model_len,
+                    max_context_len=max_context_len or self.max_model_len,
                 ),
             ),
         )

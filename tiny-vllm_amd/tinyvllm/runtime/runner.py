@@ -243,7 +243,8 @@ class ModelRunner:
             model_input = self.decode_inputs.prepare(batch, counters)
             if model_input is not None:
                 if self.decode_graphs is not None:
-                    replayed = self.decode_graphs.replay(batch.num_items)
+                    replayed = self.decode_graphs.replay(
+                        batch.num_items, max(batch.context_lens_after))
                     if replayed is not None:
                         return replayed
                 attention = HipAttention(model_input, cache,
