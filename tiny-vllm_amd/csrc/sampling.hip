@@ -223,7 +223,25 @@ __device__ __forceinline__ void thread_argmax(const T* row, int64_t vocab, float
     if constexpr (VEC) {
         const int64_t nvec = vocab / 8;
         const U16x8* rv = reinterpret_cast<const U16x8*>(row);
-        for (int64_t c = threadIdx.x; c < nvec; c += kThreads) {
+        // Four independent 16-byte loads in flight per thread, then compare
+        // in index order (ties keep the lower index either way).
+        constexpr int U = 4;
+        int64_t c = threadIdx.x;
+        for (; c + (U - 1) * kThreads < nvec; c += U * kThreads) {
+            U16x8 raw[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) raw[u] = rv[c + u * kThreads];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                float x[8];
+                unpack8<T>(raw[u], x);
+                const int64_t base = (c + u * kThreads) * 8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (better(x[e], base + e, best, bi)) { best = x[e]; bi = base + e; }
+            }
+        }
+        for (; c < nvec; c += kThreads) {
             float x[8];
             unpack8<T>(rv[c], x);
 #pragma unroll
