@@ -505,3 +505,33 @@ def test_decode_fused_qk_norm_rope_kv_write(device, heads, kv_heads, lengths, ma
     for r, n in enumerate(lengths):
         if n == 0:
             assert (out_b[r].cpu() == 0).all()
+
+
+def test_decode_shared_prefix_pages_long_context(device):
+    """C5 layout: every row's table starts with the same 256 read-only pages
+    (a 4096-token prefix shared through the prefix cache), then private pages;
+    contexts up to 31k tokens, so the rows run workgroup-level splits over
+    shared pages. Two rows with the same query and the same table must give
+    bit-identical outputs wherever they sit in the batch."""
+    g = torch.Generator().manual_seed(91)
+    bs, prefix_pages, heads, kv_heads = 16, 256, 64, 8
+    lengths = [20000, 4096, 31000, 4100, 16500, 4096]
+    pool = prefix_pages + sum(-(-n // bs) - prefix_pages for n in lengths) + 4
+    perm = torch.randperm(pool, generator=g).tolist()
+    shared, rest = perm[:prefix_pages], perm[prefix_pages:]
+    blocks, offsets = [], [0]
+    for n in lengths:
+        own = -(-n // bs) - prefix_pages
+        blocks += shared + rest[:own]
+        rest = rest[own:]
+        offsets.append(len(blocks))
+    k = torch.randn(pool * bs, kv_heads, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(pool * bs, kv_heads, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(len(lengths), heads, 128, generator=g).to(torch.bfloat16)
+    q[5] = q[1]   # rows 1 and 5: same query, same (prefix-only) table
+    case = dict(q=q, k=k, v=v, rows=torch.arange(len(lengths)),
+                blocks=torch.tensor(blocks), offsets=torch.tensor(offsets),
+                lengths=torch.tensor(lengths), block_size=bs, scale=128 ** -0.5)
+    out, expect = _run_decode(case, device, max_context_len=32768)
+    assert_bf16_close(out, expect)
+    assert torch.equal(out[1].view(torch.int16), out[5].view(torch.int16))
