@@ -311,13 +311,44 @@ paged_decode_d128(DecodeArgs<T> a) {
             }
         }
 
+        // The wave's range is walked in groups of 64 * IDR pages. Lane p
+        // holds the block ids of pages p, p + 64, ... of the group in
+        // registers (fetched once per group; only the low word: ids < 2^32,
+        // as slots * heads * 16 fits in 32 bits, checked on the host), so
+        // the chunk loop has no dependent id load in front of its K/V loads
+        // - waiting for one would also wait for every V load issued before
+        // it - and its body is one basic block, which keeps the compiler
+        // from sinking the next chunk's loads down to their use.
+        constexpr int IDR = 4;
+        const uint32_t* const ids32 = reinterpret_cast<const uint32_t*>(a.blocks);
+        const uint32_t ubs = uint32_t(bs);
+        const int64_t group_tokens = int64_t(64 * IDR) * bs;
+        int64_t g_begin = t_begin;
+        int64_t g_end = min(t_end, g_begin + group_tokens);
+        uint32_t g_page = 0;
+        uint32_t gid[IDR];
+        auto load_group = [&]() {
+            g_page = uint32_t(g_begin / bs);
+            const uint32_t last = uint32_t((g_end - 1) / bs);
+#pragma unroll
+            for (int r = 0; r < IDR; ++r)
+                gid[r] = ids32[2 * (table + min(g_page + uint32_t(lane + 64 * r), last))];
+        };
         // Lane x resolves the cache row (16-byte units) of chunk token t0 + x,
-        // clamped to the last valid token so masked lanes read mapped memory.
+        // clamped to the group's last token so masked lanes read mapped
+        // memory (past the group: the same cached row again).
         auto resolve = [&](int64_t t0) -> uint32_t {
-            const int64_t t = min(t0 + (lane % CH), t_end - 1);
-            const int64_t page = t / bs;
-            const int64_t slot = a.blocks[table + page] * bs + (t - page * bs);
-            return static_cast<uint32_t>((slot * a.kv_heads + kvh) * ROW16);
+            const uint32_t t = uint32_t(min(t0 + (lane % CH), g_end - 1));
+            const uint32_t page = t / ubs;
+            const uint32_t rel = page - g_page;
+            uint32_t id = shfl_u32(gid[0], int(rel & 63u));
+#pragma unroll
+            for (int r = 1; r < IDR; ++r) {
+                const uint32_t other = shfl_u32(gid[r], int(rel & 63u));
+                id = (rel >> 6) == uint32_t(r) ? other : id;
+            }
+            const uint64_t slot = uint64_t(id) * ubs + (t - page * ubs);
+            return static_cast<uint32_t>((slot * uint64_t(a.kv_heads) + uint64_t(kvh)) * ROW16);
         };
         U16x8 kreg[NT][4];  // [tile][k-slice]: token 16*tile + col
         U16x8 vreg[NT][4];  // [tile][i]:       token 16*tile + 4*quad + i
@@ -342,9 +373,12 @@ paged_decode_d128(DecodeArgs<T> a) {
 
         // Software pipeline: the loads of chunk i+1 are issued as soon as the
         // registers of chunk i are consumed (K after Q.K^T, V after P.V), so
-        // every wave keeps HBM requests in flight while it computes.
+        // every wave keeps HBM requests in flight while it computes. The
+        // last chunk of a group loads clamped (cached) rows instead of
+        // branching, so the loop's wait counts never cover a skipped path.
+        load_group();
         {
-            const uint32_t first = resolve(t_begin);
+            const uint32_t first = resolve(g_begin);
             load_k(first);
             load_v(first);
         }
@@ -355,70 +389,88 @@ paged_decode_d128(DecodeArgs<T> a) {
             // k-slices up in the same lane.
             rope_query<T>(qb, a.qw, a.cos_t + row * 64, a.sin_t + row * 64, a.q_eps, quad);
         }
-        for (int64_t t0 = t_begin; t0 < t_end; t0 += CH) {
-            const bool has_next = t0 + CH < t_end;
-            const uint32_t next = has_next ? resolve(t0 + CH) : 0u;
+        // The first chunk's K words pass through an empty asm: otherwise the
+        // compiler merges this load and the loop's load of the next chunk
+        // into one load at the top of the loop body (a phi of two loads
+        // becomes a load of a phi of addresses), which undoes the prefetch.
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) asm volatile("" : "+v"(kreg[j][c].w[w]));
+        for (;;) {
+            for (int64_t t0 = g_begin; t0 < g_end; t0 += CH) {
+                const uint32_t next = resolve(t0 + CH);
 
-            // Scores: s[j][i] = token 16j + 4*quad + i, query head col.
-            float s[NT][4];
+                // Scores: s[j][i] = token 16j + 4*quad + i, query head col.
+                float s[NT][4];
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                for (int j = 0; j < NT; ++j) {
+                    f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(kreg[j][c], qb[c], d);
+                    for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(kreg[j][c], qb[c], d);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int64_t t = t0 + 16 * j + 4 * quad + i;
-                    s[j][i] = t < t_end ? d[i] * a.scale_log2 : -INFINITY;
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t t = t0 + 16 * j + 4 * quad + i;
+                        s[j][i] = t < g_end ? d[i] * a.scale_log2 : -INFINITY;
+                    }
                 }
+                load_k(next);
+
+                float cmax = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[j][i]);
+                cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+                cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+                const float m_new = fmaxf(m_run, cmax);
+                const float alpha = fast_exp2(m_run - m_new);
+                m_run = m_new;
+
+                float pw[NT][4];
+                float psum = 0.f;
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float p = fast_exp2(s[j][i] - m_new);
+                        psum += p;
+                        pw[j][i] = p;
+                    }
+                l_run = l_run * alpha + psum;
+
+                static_for<0, GP>([&](auto gc) {
+                    constexpr int g = decltype(gc)::value;
+                    const float ag = read_lane<g>(alpha);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
+                });
+
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float vv[8];
+                        unpack8<T>(vreg[j][i], vv);
+                        static_for<0, GP>([&](auto gc) {
+                            constexpr int g = decltype(gc)::value;
+                            const float p = row_bcast<g>(pw[j][i]);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vv[e], acc[g][e]);
+                        });
+                    }
+                }
+                load_v(next);
             }
-            if (has_next) load_k(next);
-
-            float cmax = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < NT; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, s[j][i]);
-            cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-            cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-            const float m_new = fmaxf(m_run, cmax);
-            const float alpha = fast_exp2(m_run - m_new);
-            m_run = m_new;
-
-            float pw[NT][4];
-            float psum = 0.f;
-#pragma unroll
-            for (int j = 0; j < NT; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = fast_exp2(s[j][i] - m_new);
-                    psum += p;
-                    pw[j][i] = p;
-                }
-            l_run = l_run * alpha + psum;
-
-            static_for<0, GP>([&](auto gc) {
-                constexpr int g = decltype(gc)::value;
-                const float ag = read_lane<g>(alpha);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
-            });
-
-#pragma unroll
-            for (int j = 0; j < NT; ++j) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float vv[8];
-                    unpack8<T>(vreg[j][i], vv);
-                    static_for<0, GP>([&](auto gc) {
-                        constexpr int g = decltype(gc)::value;
-                        const float p = row_bcast<g>(pw[j][i]);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vv[e], acc[g][e]);
-                    });
-                }
-            }
-            if (has_next) load_v(next);
+            if (g_end >= t_end) break;
+            g_begin = g_end;
+            g_end = min(t_end, g_begin + group_tokens);
+            load_group();
+            const uint32_t first = resolve(g_begin);
+            load_k(first);
+            load_v(first);
         }
 
     }  // t_begin < t_end
