@@ -252,8 +252,8 @@ def cpu_baseline(cfg, batch: int, context: int, reps: int = 2) -> dict:
 
 def kernel_only(args) -> None:
     """The decode step's attention kernel (QK-norm + RoPE + KV write + split-K
-    paged decode) alone at the workload's shape (one layer of KV, one step's
-    metadata), plus a 1 GiB device copy for counter calibration. Used for
+    paged decode) alone at the workload's shape (eight layers of KV visited in
+    turn, one step's metadata), plus a 1 GiB device copy for counter calibration. Used for
     rocprofv3 PMC passes, which profile dispatches launched outside graphs."""
     import torch
 
@@ -267,7 +267,8 @@ def kernel_only(args) -> None:
     bs, rows, ctx = 16, args.batch, args.context + 1
     hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     pages = math.ceil(ctx / bs)
-    cache = PagedKVCache(num_layers=1, num_blocks=rows * pages, block_size=bs,
+    layers = 8  # visited in turn: no launch finds its KV in the memory-side cache
+    cache = PagedKVCache(num_layers=layers, num_blocks=rows * pages, block_size=bs,
                          num_kv_heads=hkv, head_dim=d, device=device, dtype=torch.bfloat16)
     gen = torch.Generator(device=device).manual_seed(1)
     cache.key.normal_(generator=gen)
@@ -289,9 +290,9 @@ def kernel_only(args) -> None:
         positions, torch.bfloat16)
     slots = perm.view(rows, pages)[:, (ctx - 1) // bs] * bs + (ctx - 1) % bs
     out = torch.empty_like(q)
-    for _ in range(args.steps):
-        paged_decode_qk_norm_rope(q, k, v, w, w, cos, sin, 1e-6, 1e-6, cache, 0, meta, slots,
-                                  out, scale=d ** -0.5, workspace=ws)
+    for step in range(args.steps):
+        paged_decode_qk_norm_rope(q, k, v, w, w, cos, sin, 1e-6, 1e-6, cache, step % layers,
+                                  meta, slots, out, scale=d ** -0.5, workspace=ws)
     src = torch.empty(1 << 29, dtype=torch.bfloat16, device=device)  # 1 GiB
     dst = torch.empty_like(src)
     for _ in range(3):
