@@ -28,7 +28,14 @@ extern "C" {
 
 typedef struct ihipStream_t* tvllm_stream_t; /* == hipStream_t */
 
-enum tvllm_dtype { TVLLM_BF16 = 0, TVLLM_F16 = 1, TVLLM_F32 = 2 };
+enum tvllm_dtype {
+    TVLLM_BF16 = 0,
+    TVLLM_F16 = 1,
+    TVLLM_F32 = 2,
+    /* KV-cache storage only: OCP FP8 E4M3 (max 448) with a per-cache scale,
+     * stored = fp8(clamp(x * (1 / scale), -448, 448)), read as stored * scale. */
+    TVLLM_FP8_E4M3 = 3,
+};
 
 enum tvllm_status {
     TVLLM_OK = 0,
@@ -42,8 +49,10 @@ const char* tvllm_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int tvllm_abi_version(void);
 
-/* Scatter K/V rows into the paged cache: cache[slot[t]] = key[t] (bit copy).
- * slot == -1 skips the row (graph padding).
+/* Scatter K/V rows into the paged cache: cache[slot[t]] = key[t] (bit copy;
+ * cache_dtype == dtype, k_scale = v_scale = 1), or for cache_dtype
+ * TVLLM_FP8_E4M3 the E4M3 byte of clamp(x * (1 / scale), -448, 448) per
+ * element (nearest-even). slot == -1 skips the row (graph padding).
  * key/value: [tokens, kv_heads, head_dim] with the given element strides
  * (last stride must be 1); caches: contiguous [num_slots, kv_heads, head_dim].
  * Replaces: torch.ops.tinyvllm_cuda.store_kv
@@ -55,7 +64,8 @@ int tvllm_store_kv(const void* key, const void* value,
                    void* key_cache, void* value_cache,
                    const int64_t* slots, int64_t num_tokens,
                    int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
-                   int dtype, tvllm_stream_t stream);
+                   int dtype, int cache_dtype, float k_scale, float v_scale,
+                   tvllm_stream_t stream);
 
 /* Bytes of device workspace tvllm_paged_decode needs for this geometry
  * (split-K partial results). 0 means no workspace is needed.
@@ -87,6 +97,9 @@ int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
  * rows, offsets (num_rows + 1), lengths, blocks: int64 device vectors.
  * workspace: >= tvllm_paged_decode_workspace_size(...) bytes (may be NULL
  * when that size is 0). head_dim must be 64 or 128.
+ * cache_dtype: dtype (caches hold q's element type; k_scale = v_scale = 1)
+ * or TVLLM_FP8_E4M3 (caches hold E4M3 bytes, [num_slots, kv_heads, head_dim];
+ * K = stored * k_scale, V = stored * v_scale; head_dim 128, group <= 16).
  * Replaces: torch.ops.tinyvllm_cuda.paged_decode
  *           (reference tinyvllm/kernels/paged_decode.cu:469-669, wrapper
  *            tinyvllm/kernels/paged_decode.py:10-32). */
@@ -101,7 +114,8 @@ int tvllm_paged_decode(const void* q, int64_t q_token_stride,
                        int64_t num_slots, int64_t block_size,
                        int64_t max_context_len, float scale,
                        void* workspace, int64_t workspace_bytes,
-                       int dtype, tvllm_stream_t stream);
+                       int dtype, int cache_dtype, float k_scale, float v_scale,
+                       tvllm_stream_t stream);
 
 /* tvllm_qk_norm_rope's fused KV write followed by tvllm_paged_decode, in
  * one kernel, for a step whose rows are all decode rows: q, k, v are the raw
@@ -109,8 +123,10 @@ int tvllm_paged_decode(const void* q, int64_t q_token_stride,
  * rotates its query heads in registers, and the wave whose page range holds
  * a row's newest token (position lengths[r] - 1) writes that token's rotated
  * K row and its V row to slot slots[rows[r]] (-1 skips) before reading it.
- * The K rows written are bit-identical to tvllm_qk_norm_rope's. cos, sin:
- * contiguous [tokens, 64]; q_weight, k_weight: [128]. head_dim must be 128.
+ * The K rows written are bit-identical to tvllm_qk_norm_rope's (with the
+ * same cache_dtype and scales). cos, sin: contiguous [tokens, 64]; q_weight,
+ * k_weight: [128]. head_dim must be 128. cache_dtype / k_scale / v_scale as
+ * for tvllm_paged_decode.
  * Replaces: the decode-step sequence qk_norm_rope + store_kv + paged_decode
  *           (reference tinyvllm/models/qwen3.py:284-293,
  *            runtime/attention.py:219-285); no single reference counterpart. */
@@ -123,8 +139,8 @@ int tvllm_paged_decode_qk_norm_rope(
     const int64_t* rows, const int64_t* blocks, const int64_t* offsets,
     const int64_t* lengths, int64_t num_rows, int64_t num_heads, int64_t num_kv_heads,
     int64_t head_dim, int64_t num_slots, int64_t block_size, int64_t max_context_len,
-    float scale, void* workspace, int64_t workspace_bytes, int dtype,
-    tvllm_stream_t stream);
+    float scale, void* workspace, int64_t workspace_bytes, int dtype, int cache_dtype,
+    float k_scale, float v_scale, tvllm_stream_t stream);
 
 /* RMSNorm over rows of width `width`, optionally after a residual add:
  *   x = residual ? round(x + residual) : x
@@ -178,7 +194,8 @@ int tvllm_silu_and_mul(const void* input, int64_t tokens, int64_t heads,
  * when key_cache != NULL, the rotated K row and the V row
  * (v: [tokens, num_kv_heads, head_dim] with the given strides) are also
  * written to key_cache/value_cache[slots[t]] (slot -1 skips); k_out may then
- * be NULL.
+ * be NULL. cache_dtype / k_scale / v_scale as for tvllm_store_kv (the FP8
+ * cache stores the E4M3 byte of the rounded rotated K element times 1/k_scale).
  * Replaces: torch.ops.tinyvllm_cuda.qk_norm_rope
  *           (reference tinyvllm/kernels/pointwise.cu:453-546) and, when
  *           fused, the following store_kv (runtime/attention.py:219-233). */
@@ -193,7 +210,8 @@ int tvllm_qk_norm_rope(const void* q, int64_t q_token_stride,
                        const void* v, int64_t v_token_stride,
                        int64_t v_head_stride, void* key_cache,
                        void* value_cache, const int64_t* slots,
-                       int64_t num_slots, int dtype, tvllm_stream_t stream);
+                       int64_t num_slots, int dtype, int cache_dtype,
+                       float k_scale, float v_scale, tvllm_stream_t stream);
 
 /* Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
  * (row stride row_stride elements). NaN compares greater than any number,
@@ -229,6 +247,7 @@ int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
  * come from the paged cache through blocks/block_offsets as in
  * tvllm_paged_decode. Items with q_offsets[i+1] - q_offsets[i] <= 0 are
  * skipped. max_query_len bounds every item's query length (grid size).
+ * cache_dtype / k_scale / v_scale as for tvllm_paged_decode.
  * Replaces: CudaAttention._attend's per-row gather + SDPA for rows with
  * history (reference tinyvllm/runtime/attention.py:102-151, 235-285). */
 int tvllm_paged_prefill(const void* q, int64_t q_token_stride,
@@ -241,7 +260,8 @@ int tvllm_paged_prefill(const void* q, int64_t q_token_stride,
                         int64_t max_query_len, int64_t num_heads,
                         int64_t num_kv_heads, int64_t head_dim,
                         int64_t num_slots, int64_t block_size, float scale,
-                        int dtype, tvllm_stream_t stream);
+                        int dtype, int cache_dtype, float k_scale,
+                        float v_scale, tvllm_stream_t stream);
 
 #ifdef __cplusplus
 }

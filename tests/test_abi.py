@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = load_kernels()
     for name in sorted(declared_symbols()):
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
-    assert lib.tvllm_abi_version() == 1
+    assert lib.tvllm_abi_version() == 2
     assert lib.tvllm_last_error() == b""
 
 
@@ -38,18 +38,28 @@ def test_argument_errors_surface_without_touching_a_gpu():
 
     lib = load_kernels()
     status = lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
-                                4, 8, 128, 64, 7, None)
+                                4, 8, 128, 64, 7, 7, 1.0, 1.0, None)
     assert status == -1
     with pytest.raises(RuntimeError, match="float16 or bfloat16"):
         check(status)
     status = lib.tvllm_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None,
                                     None, None, 1, 6, 4, 128, 64, 16, 64, 1.0,
-                                    None, 0, 0, None)
+                                    None, 0, 0, 0, 1.0, 1.0, None)
     with pytest.raises(RuntimeError, match="GQA"):
         check(status)
     # Zero-sized work is a no-op that never dereferences pointers.
     assert lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
-                              0, 8, 128, 64, 0, None) == 0
+                              0, 8, 128, 64, 0, 0, 1.0, 1.0, None) == 0
+    # KV scales belong to FP8 caches; a 16-bit cache must keep them at 1.
+    status = lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
+                                0, 8, 128, 64, 0, 0, 2.0, 1.0, None)
+    with pytest.raises(RuntimeError, match="FP8 cache only"):
+        check(status)
+    status = lib.tvllm_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None,
+                                    None, None, 1, 8, 8, 128, 64, 16, 64, 1.0,
+                                    None, 0, 0, 1, 1.0, 1.0, None)
+    with pytest.raises(RuntimeError, match="cache dtype"):
+        check(status)
 
 
 def test_decode_workspace_sizes():

@@ -17,7 +17,7 @@ from oracle import pointwise as OP
 pytestmark = pytest.mark.gpu
 
 
-def _Cache(k, v, block_size):
+def _Cache(k, v, block_size, k_scale=1.0, v_scale=1.0):
     """A one-layer PagedKVCache wrapping existing K/V tensors."""
     from tinyvllm.paged_kv import PagedKVCache
 
@@ -27,6 +27,8 @@ def _Cache(k, v, block_size):
     cache.num_slots, cache.num_kv_heads, cache.head_dim = k.shape
     cache.num_blocks = cache.num_slots // block_size
     cache.device, cache.dtype = k.device, k.dtype
+    cache.fp8 = k.dtype == torch.float8_e4m3fn
+    cache.k_scale, cache.v_scale = float(k_scale), float(v_scale)
     return cache
 
 

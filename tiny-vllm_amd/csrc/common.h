@@ -124,6 +124,65 @@ __device__ __forceinline__ void unpack8(const U16x8& v, float (&out)[8]) {
     }
 }
 
+// ------------------------------------------------------ fp8 KV cache --
+// Cache rows may be stored as OCP FP8 E4M3 (max 448, no infinities) with a
+// per-cache scale: stored = fp8(clamp(x * inv_scale, -448, 448)), nearest-
+// even (the v_cvt_pk_fp8_f32 rounding, identical to torch's float8_e4m3fn
+// cast); read back as stored * scale. Decoding an E4M3 value to f32, bf16 or
+// f16 is exact.
+
+constexpr float kFp8Max = 448.f;
+
+__device__ __forceinline__ float fp8_clamp(float x) {
+    return fminf(fmaxf(x, -kFp8Max), kFp8Max);  // NaN stays NaN
+}
+
+// Four floats (already scaled) -> four E4M3 bytes, element 0 in byte 0.
+__device__ __forceinline__ uint32_t fp8x4_pack(float a, float b, float c, float d) {
+    uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(a), fp8_clamp(b), 0u, false);
+    return __builtin_amdgcn_cvt_pk_fp8_f32(fp8_clamp(c), fp8_clamp(d), w, true);
+}
+
+// Eight E4M3 bytes (element 0 in the low byte of w.x) -> eight floats.
+__device__ __forceinline__ void fp8x8_unpack(uint2 w, float (&out)[8]) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false);
+    const f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
+    const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, false);
+    const f32x2_t d = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, true);
+    out[0] = a[0]; out[1] = a[1]; out[2] = b[0]; out[3] = b[1];
+    out[4] = c[0]; out[5] = c[1]; out[6] = d[0]; out[7] = d[1];
+}
+
+// Eight E4M3 bytes -> eight 16-bit elements of type T (exact).
+template <typename T>
+__device__ __forceinline__ U16x8 fp8x8_widen(uint2 w) {
+    U16x8 r;
+    if constexpr (__is_same(T, __bf16)) {
+        r.w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, 1.f, false));
+        r.w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, 1.f, true));
+        r.w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, 1.f, false));
+        r.w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, 1.f, true));
+    } else {
+        r.w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.x, 1.f, false));
+        r.w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.x, 1.f, true));
+        r.w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.y, 1.f, false));
+        r.w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.y, 1.f, true));
+    }
+    return r;
+}
+
+// Eight 16-bit elements -> eight E4M3 bytes of x * inv_scale.
+template <typename T>
+__device__ __forceinline__ uint2 fp8x8_narrow(const U16x8& v, float inv_scale) {
+    float x[8];
+    unpack8<T>(v, x);
+    uint2 r;
+    r.x = fp8x4_pack(x[0] * inv_scale, x[1] * inv_scale, x[2] * inv_scale, x[3] * inv_scale);
+    r.y = fp8x4_pack(x[4] * inv_scale, x[5] * inv_scale, x[6] * inv_scale, x[7] * inv_scale);
+    return r;
+}
+
 // ------------------------------------------------------- wave64 reduces --
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -1,7 +1,9 @@
-// Paged KV-cache scatter: cache[slot[t]] = row t of K and V (bit copy).
+// Paged KV-cache scatter: cache[slot[t]] = row t of K and V (bit copy), or,
+// for an FP8 E4M3 cache, fp8(clamp(x / scale)) of every element.
 //
 // Reference behaviour: tinyvllm/kernels/kv_store.cu:27-90 (kernel) and
 // :101-232 (host checks). slot == -1 marks graph padding and is skipped.
+// (The FP8 cache has no reference counterpart.)
 //
 // Layout: one token row is kv_heads * head_dim 16-bit words (2 KiB for
 // Qwen3's 8 x 128). Each thread copies one 16-byte chunk of K and of V; the
@@ -29,6 +31,47 @@ store_kv_vec(const U16x8* __restrict__ key, const U16x8* __restrict__ value,
     if (slot < 0) return;
     key_cache[slot * width8 + chunk] = key[token * key_stride8 + chunk];
     value_cache[slot * width8 + chunk] = value[token * value_stride8 + chunk];
+}
+
+// FP8 cache, vector path: each thread narrows one 16-byte source chunk into
+// one 8-byte cache chunk.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+store_kv_vec_fp8(const U16x8* __restrict__ key, const U16x8* __restrict__ value,
+                 int64_t key_stride8, int64_t value_stride8,
+                 uint2* __restrict__ key_cache, uint2* __restrict__ value_cache,
+                 const int64_t* __restrict__ slots, int64_t tokens, int width8,
+                 float k_inv, float v_inv) {
+    const int64_t idx = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t token = idx / width8;
+    const int chunk = int(idx - token * width8);
+    if (token >= tokens) return;
+    const int64_t slot = slots[token];
+    if (slot < 0) return;
+    key_cache[slot * width8 + chunk] = fp8x8_narrow<T>(key[token * key_stride8 + chunk], k_inv);
+    value_cache[slot * width8 + chunk] =
+        fp8x8_narrow<T>(value[token * value_stride8 + chunk], v_inv);
+}
+
+// FP8 cache, any strides: element-wise.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+store_kv_any_fp8(const T* __restrict__ key, const T* __restrict__ value, int64_t kts,
+                 int64_t khs, int64_t vts, int64_t vhs, uint8_t* __restrict__ key_cache,
+                 uint8_t* __restrict__ value_cache, const int64_t* __restrict__ slots,
+                 int64_t tokens, int64_t heads, int64_t head_dim, float k_inv, float v_inv) {
+    const int64_t width = heads * head_dim;
+    const int64_t token = blockIdx.x;
+    if (token >= tokens) return;
+    const int64_t slot = slots[token];
+    if (slot < 0) return;
+    for (int64_t e = threadIdx.x; e < width; e += kThreads) {
+        const int64_t h = e / head_dim, d = e - h * head_dim;
+        const float kx = to_f<T>(key[token * kts + h * khs + d]) * k_inv;
+        const float vx = to_f<T>(value[token * vts + h * vhs + d]) * v_inv;
+        key_cache[slot * width + e] = uint8_t(fp8x4_pack(kx, 0.f, 0.f, 0.f));
+        value_cache[slot * width + e] = uint8_t(fp8x4_pack(vx, 0.f, 0.f, 0.f));
+    }
 }
 
 // Generic path: arbitrary head strides (last stride 1), element-wise.
@@ -62,9 +105,17 @@ extern "C" int tvllm_store_kv(const void* key, const void* value,
                               void* value_cache, const int64_t* slots,
                               int64_t num_tokens, int64_t num_kv_heads,
                               int64_t head_dim, int64_t num_slots, int dtype,
+                              int cache_dtype, float k_scale, float v_scale,
                               tvllm_stream_t stream) {
     TVLLM_CHECK(dtype == TVLLM_BF16 || dtype == TVLLM_F16,
                 "store_kv: KV store requires float16 or bfloat16");
+    const bool f8 = cache_dtype == TVLLM_FP8_E4M3;
+    TVLLM_CHECK(f8 || cache_dtype == dtype,
+                "store_kv: KV cache dtype must match the rows or be FP8 E4M3");
+    TVLLM_CHECK(k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY,
+                "store_kv: KV scales must be positive and finite");
+    TVLLM_CHECK(f8 || (k_scale == 1.f && v_scale == 1.f),
+                "store_kv: KV scales apply to an FP8 cache only");
     TVLLM_CHECK(num_tokens >= 0 && num_kv_heads > 0 && head_dim > 0,
                 "store_kv: KV head geometry mismatch");
     TVLLM_CHECK(num_tokens <= num_slots && num_tokens <= INT32_MAX,
@@ -82,6 +133,29 @@ extern "C" int tvllm_store_kv(const void* key, const void* value,
                      aligned16(value) && aligned16(key_cache) &&
                      aligned16(value_cache);
     hipStream_t s = as_hip(stream);
+    if (f8) {
+        const float k_inv = 1.f / k_scale, v_inv = 1.f / v_scale;
+        return dispatch_half(dtype, [&]<int DT>() {
+            using T = typename Elem<DT>::T;
+            if (vec) {
+                const int width8 = int(width / 8);
+                const int64_t total = num_tokens * width8;
+                const int blocks = int((total + kThreads - 1) / kThreads);
+                store_kv_vec_fp8<T><<<blocks, kThreads, 0, s>>>(
+                    static_cast<const U16x8*>(key), static_cast<const U16x8*>(value),
+                    key_token_stride / 8, value_token_stride / 8,
+                    static_cast<uint2*>(key_cache), static_cast<uint2*>(value_cache), slots,
+                    num_tokens, width8, k_inv, v_inv);
+            } else {
+                store_kv_any_fp8<T><<<int(num_tokens), kThreads, 0, s>>>(
+                    static_cast<const T*>(key), static_cast<const T*>(value),
+                    key_token_stride, key_head_stride, value_token_stride, value_head_stride,
+                    static_cast<uint8_t*>(key_cache), static_cast<uint8_t*>(value_cache), slots,
+                    num_tokens, num_kv_heads, head_dim, k_inv, v_inv);
+            }
+            return launch_status("store_kv");
+        });
+    }
     if (vec) {
         const int width8 = int(width / 8);
         const int64_t total = num_tokens * width8;

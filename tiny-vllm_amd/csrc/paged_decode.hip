@@ -97,13 +97,18 @@ __device__ __forceinline__ U16x8 load_stream(const U16x8* p) {
     r.w[3] = t[3];
     return r;
 }
+__device__ __forceinline__ uint2 load_stream(const uint2* p) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    return make_uint2(t[0], t[1]);
+}
 
 template <typename T>
 struct DecodeArgs {
     const T* q;
     int64_t qts, qhs;
-    const U16x8* k;  // cache rows in 16-byte units
-    const U16x8* v;
+    const void* k;  // cache rows: 16 units of 8 elements (16 B, or 8 B for FP8)
+    const void* v;
     T* out;
     int64_t ots, ohs;
     const int64_t* rows;
@@ -115,7 +120,10 @@ struct DecodeArgs {
     int grid_splits;    // workgroups per (row, KV head group)
     int num_rows;       // rows of the batch (balanced spans scan their lengths)
     int heads_per_wg;   // KV heads per workgroup
-    float scale_log2;   // softmax scale * log2(e): scores live in base 2
+    float scale_log2;   // softmax scale * log2(e) (* k_scale for FP8): base-2 scores
+    float v_scale;      // FP8 cache: V dequantisation scale (1 otherwise)
+    float k_inv_scale;  // FP8 cache: 1 / scale of the new rows written (fused)
+    float v_inv_scale;
     float* part_o;      // [rows, heads, grid_splits, 128] (grid_splits > 1)
     float* part_ml;     // [rows, heads, grid_splits, 2]
     // Fused QK-norm + RoPE + KV write (FUSED kernels only): q above is the
@@ -130,8 +138,8 @@ struct DecodeArgs {
     const T* cos_t;     // [tokens, 64]
     const T* sin_t;
     float q_eps, k_eps;
-    T* kcache;          // writable views of k / v
-    T* vcache;
+    void* kcache;       // writable views of k / v
+    void* vcache;
     const int64_t* slots;
 };
 
@@ -193,12 +201,14 @@ __device__ __forceinline__ void rope_query(U16x8 (&qb)[4], const T* __restrict__
 // New K row: normalised and rotated exactly as the standalone kernel does
 // (lane l owns the pair (l, l + 64), one wave-wide sum of squares), written
 // with the V row into the cache slot.
-template <typename T>
+// FP8 cache (F8): the rounded K element and the V element are quantised
+// with the cache's inverse scales, as the standalone kernels do.
+template <typename T, bool F8>
 __device__ __forceinline__ void write_new_kv(const T* __restrict__ k, const T* __restrict__ v,
                                              const T* __restrict__ w, const T* __restrict__ cs,
                                              const T* __restrict__ sn, float eps,
-                                             T* __restrict__ kdst, T* __restrict__ vdst,
-                                             int lane) {
+                                             void* __restrict__ kdst, void* __restrict__ vdst,
+                                             float k_inv, float v_inv, int lane) {
     const float x1 = to_f<T>(k[lane]), x2 = to_f<T>(k[lane + 64]);
     const float w1 = to_f<T>(w[lane]), w2 = to_f<T>(w[lane + 64]);
     const float c = to_f<T>(cs[lane]), s = to_f<T>(sn[lane]);
@@ -206,21 +216,43 @@ __device__ __forceinline__ void write_new_kv(const T* __restrict__ k, const T* _
     const float inv = rsqrtf(ss * (1.0f / 128.f) + eps);
     const float n1 = rnd<T>(rnd<T>(x1 * inv) * w1);
     const float n2 = rnd<T>(rnd<T>(x2 * inv) * w2);
-    kdst[lane] = static_cast<T>(rnd<T>(n1 * c) - rnd<T>(n2 * s));
-    kdst[lane + 64] = static_cast<T>(rnd<T>(n2 * c) + rnd<T>(n1 * s));
-    vdst[lane] = v[lane];
-    vdst[lane + 64] = v[lane + 64];
+    const float o1 = rnd<T>(rnd<T>(n1 * c) - rnd<T>(n2 * s));
+    const float o2 = rnd<T>(rnd<T>(n2 * c) + rnd<T>(n1 * s));
+    if constexpr (F8) {
+        uint8_t* kd = static_cast<uint8_t*>(kdst);
+        uint8_t* vd = static_cast<uint8_t*>(vdst);
+        const uint32_t kq = fp8x4_pack(o1 * k_inv, o2 * k_inv, 0.f, 0.f);
+        const uint32_t vq = fp8x4_pack(to_f<T>(v[lane]) * v_inv, to_f<T>(v[lane + 64]) * v_inv,
+                                       0.f, 0.f);
+        kd[lane] = uint8_t(kq);
+        kd[lane + 64] = uint8_t(kq >> 8);
+        vd[lane] = uint8_t(vq);
+        vd[lane + 64] = uint8_t(vq >> 8);
+    } else {
+        T* kd = static_cast<T*>(kdst);
+        T* vd = static_cast<T*>(vdst);
+        kd[lane] = static_cast<T>(o1);
+        kd[lane + 64] = static_cast<T>(o2);
+        vd[lane] = v[lane];
+        vd[lane + 64] = v[lane + 64];
+    }
 }
 
 // GP: group size rounded up to a power of two (<= 16); NT: 16-token MFMA
 // tiles per iteration. Wave w of a workgroup owns KV head
 // (group of the workgroup) * heads_per_wg + w / splits and page range
 // w % splits of its row.
-template <typename T, int GP, int NT, int MAXW, bool FUSED>
+// F8: the cache holds FP8 E4M3 rows (8-byte units; K widened exactly to T
+// for the MFMA, V to f32 for P.V, the scales folded into the softmax scale
+// and the final normalisation).
+template <typename T, int GP, int NT, int MAXW, bool FUSED, bool F8>
 __global__ void __launch_bounds__(64 * MAXW)
 paged_decode_d128(DecodeArgs<T> a) {
     constexpr int D = 128;
-    constexpr int ROW16 = D / 8;  // 16-byte units per cache row of one head
+    constexpr int ROW16 = D / 8;  // 8-element units per cache row of one head
+    using Unit = std::conditional_t<F8, uint2, U16x8>;  // 8 cached elements
+    const Unit* const kc = static_cast<const Unit*>(a.k);
+    const Unit* const vc = static_cast<const Unit*>(a.v);
     constexpr int CH = 16 * NT;   // tokens per iteration
     static_assert(CH <= 64, "one lane resolves one token of an iteration");
     const int lane = threadIdx.x & 63;
@@ -297,11 +329,14 @@ paged_decode_d128(DecodeArgs<T> a) {
             if (t_begin <= length - 1 && length - 1 < t_end) {
                 const int64_t slot = a.slots[row];
                 if (slot >= 0) {
-                    write_new_kv<T>(a.kraw + row * a.krts + kvh * a.krhs,
-                                    a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
-                                    a.cos_t + row * 64, a.sin_t + row * 64, a.k_eps,
-                                    a.kcache + (slot * a.kv_heads + kvh) * D,
-                                    a.vcache + (slot * a.kv_heads + kvh) * D, lane);
+                    constexpr int EB = F8 ? 1 : int(sizeof(T));  // bytes per element
+                    const int64_t off = (slot * a.kv_heads + kvh) * D * EB;
+                    write_new_kv<T, F8>(a.kraw + row * a.krts + kvh * a.krhs,
+                                        a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
+                                        a.cos_t + row * 64, a.sin_t + row * 64, a.k_eps,
+                                        static_cast<char*>(a.kcache) + off,
+                                        static_cast<char*>(a.vcache) + off, a.k_inv_scale,
+                                        a.v_inv_scale, lane);
                     // Only this wave reads the row, and no CU has it cached
                     // (caches start clean per dispatch): a workgroup-scope
                     // release (store completion, no cache write-back) orders
@@ -350,16 +385,20 @@ paged_decode_d128(DecodeArgs<T> a) {
             const uint64_t slot = uint64_t(id) * ubs + (t - page * ubs);
             return static_cast<uint32_t>((slot * uint64_t(a.kv_heads) + uint64_t(kvh)) * ROW16);
         };
-        U16x8 kreg[NT][4];  // [tile][k-slice]: token 16*tile + col
-        U16x8 vreg[NT][4];  // [tile][i]:       token 16*tile + 4*quad + i
+        Unit kreg[NT][4];  // [tile][k-slice]: token 16*tile + col
+        Unit vreg[NT][4];  // [tile][i]:       token 16*tile + 4*quad + i
         auto load_k = [&](uint32_t my_row) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
                 const uint32_t kr = shfl_u32(my_row, 16 * j + col);
-                const U16x8* kp = a.k + kr + quad;
+                const Unit* kp = kc + kr + quad;
 #pragma unroll
                 for (int c = 0; c < 4; ++c) kreg[j][c] = kp[c * 4];
             }
+        };
+        auto k_operand = [&](int j, int c) -> U16x8 {
+            if constexpr (F8) return fp8x8_widen<T>(kreg[j][c]);
+            else return kreg[j][c];
         };
         auto load_v = [&](uint32_t my_row) {
 #pragma unroll
@@ -367,7 +406,7 @@ paged_decode_d128(DecodeArgs<T> a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t vr = shfl_u32(my_row, 16 * j + 4 * quad + i);
-                    vreg[j][i] = load_stream(a.v + vr + col);
+                    vreg[j][i] = load_stream(vc + vr + col);
                 }
         };
 
@@ -396,9 +435,15 @@ paged_decode_d128(DecodeArgs<T> a) {
 #pragma unroll
         for (int j = 0; j < NT; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
+            for (int c = 0; c < 4; ++c) {
+                if constexpr (F8) {
+                    asm volatile("" : "+v"(kreg[j][c].x));
+                    asm volatile("" : "+v"(kreg[j][c].y));
+                } else {
 #pragma unroll
-                for (int w = 0; w < 4; ++w) asm volatile("" : "+v"(kreg[j][c].w[w]));
+                    for (int w = 0; w < 4; ++w) asm volatile("" : "+v"(kreg[j][c].w[w]));
+                }
+            }
         for (;;) {
             for (int64_t t0 = g_begin; t0 < g_end; t0 += CH) {
                 const uint32_t next = resolve(t0 + CH);
@@ -409,7 +454,7 @@ paged_decode_d128(DecodeArgs<T> a) {
                 for (int j = 0; j < NT; ++j) {
                     f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(kreg[j][c], qb[c], d);
+                    for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(k_operand(j, c), qb[c], d);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int64_t t = t0 + 16 * j + 4 * quad + i;
@@ -453,7 +498,8 @@ paged_decode_d128(DecodeArgs<T> a) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         float vv[8];
-                        unpack8<T>(vreg[j][i], vv);
+                        if constexpr (F8) fp8x8_unpack(vreg[j][i], vv);
+                        else unpack8<T>(vreg[j][i], vv);
                         static_for<0, GP>([&](auto gc) {
                             constexpr int g = decltype(gc)::value;
                             const float p = row_bcast<g>(pw[j][i]);
@@ -555,7 +601,8 @@ paged_decode_d128(DecodeArgs<T> a) {
         if (mx == -INFINITY) den = 1.f;  // zero-length row: zeros
         U16x8 packed;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) packed.w[e] = pack2<T>(num[2 * e] / den, num[2 * e + 1] / den);
+        for (int e = 0; e < 4; ++e)
+            packed.w[e] = pack2<T>(num[2 * e] * a.v_scale / den, num[2 * e + 1] * a.v_scale / den);
         *reinterpret_cast<U16x8*>(a.out + row * a.ots + (h0 + g) * a.ohs + col * 8) = packed;
     });
 }
@@ -565,7 +612,8 @@ template <typename T>
 __global__ void __launch_bounds__(64)
 paged_decode_merge(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                    T* __restrict__ out, const int64_t* __restrict__ rows,
-                   int64_t ots, int64_t ohs, int heads, int splits, int head_dim) {
+                   int64_t ots, int64_t ohs, int heads, int splits, int head_dim,
+                   float v_scale) {
     const int id = blockIdx.x;
     const int r = id / heads;
     const int h = id - r * heads;
@@ -588,7 +636,7 @@ paged_decode_merge(const float* __restrict__ part_o, const float* __restrict__ p
             const float m = part_ml[(base + s) * 2];
             if (m != -INFINITY) num += exp2f(m - mx) * part_o[(base + s) * head_dim + d];
         }
-        o[d] = static_cast<T>(num / denom);
+        o[d] = static_cast<T>(num * v_scale / denom);
     }
 }
 
@@ -799,7 +847,8 @@ int paged_decode_impl(
     const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
     int64_t block_size, int64_t max_context_len, float scale, void* workspace,
-    int64_t workspace_bytes, int dtype, tvllm_stream_t stream, const FusedIn* fused) {
+    int64_t workspace_bytes, int dtype, int cache_dtype, float k_scale, float v_scale,
+    tvllm_stream_t stream, const FusedIn* fused) {
     TVLLM_CHECK(head_dim > 0 && head_dim <= 256 && num_heads > 0 && num_kv_heads > 0,
                 "paged_decode: invalid attention head geometry");
     TVLLM_CHECK(num_heads % num_kv_heads == 0 && block_size > 0 &&
@@ -808,6 +857,13 @@ int paged_decode_impl(
     TVLLM_CHECK(num_rows >= 0 && num_rows <= INT32_MAX / num_heads,
                 "paged_decode: decode grid is too large");
     TVLLM_CHECK(max_context_len > 0, "paged_decode: max_context_len must be positive");
+    const bool f8 = cache_dtype == TVLLM_FP8_E4M3;
+    TVLLM_CHECK(f8 || cache_dtype == dtype,
+                "paged_decode: KV cache dtype must match the query dtype or be FP8 E4M3");
+    TVLLM_CHECK(k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY,
+                "paged_decode: KV scales must be positive and finite");
+    TVLLM_CHECK(f8 || (k_scale == 1.f && v_scale == 1.f),
+                "paged_decode: KV scales apply to an FP8 cache only");
     if (num_rows == 0) return TVLLM_OK;
     TVLLM_CHECK(q && k_cache && v_cache && out && rows && blocks && offsets && lengths,
                 "paged_decode: null pointer");
@@ -822,6 +878,9 @@ int paged_decode_impl(
                                     num_slots, num_kv_heads);
         TVLLM_CHECK(fused == nullptr || fast,
                     "paged_decode_qk_norm_rope: needs head_dim 128, group <= 16 and "
+                    "16-byte aligned rows");
+        TVLLM_CHECK(!f8 || fast,
+                    "paged_decode: an FP8 KV cache needs head_dim 128, group <= 16 and "
                     "16-byte aligned rows");
         if (!fast) {
             paged_decode_generic<T><<<int(num_rows * num_heads), 64, 0, s>>>(
@@ -851,8 +910,8 @@ int paged_decode_impl(
         args.q = static_cast<const T*>(q);
         args.qts = q_token_stride;
         args.qhs = q_head_stride;
-        args.k = static_cast<const U16x8*>(k_cache);
-        args.v = static_cast<const U16x8*>(v_cache);
+        args.k = k_cache;
+        args.v = v_cache;
         args.out = static_cast<T*>(out);
         args.ots = out_token_stride;
         args.ohs = out_head_stride;
@@ -868,7 +927,10 @@ int paged_decode_impl(
         args.grid_splits = int(plan.grid);
         args.num_rows = int(num_rows);
         args.heads_per_wg = hpg;
-        args.scale_log2 = scale_log2;
+        args.scale_log2 = scale_log2 * k_scale;
+        args.v_scale = v_scale;
+        args.k_inv_scale = 1.f / k_scale;
+        args.v_inv_scale = 1.f / v_scale;
         args.part_o = static_cast<float*>(workspace);
         args.part_ml = need ? args.part_o + num_rows * num_heads * plan.grid * head_dim
                             : nullptr;
@@ -888,18 +950,18 @@ int paged_decode_impl(
             args.sin_t = static_cast<const T*>(fused->sin);
             args.q_eps = fused->q_eps;
             args.k_eps = fused->k_eps;
-            args.kcache = static_cast<T*>(const_cast<void*>(k_cache));
-            args.vcache = static_cast<T*>(const_cast<void*>(v_cache));
+            args.kcache = const_cast<void*>(k_cache);
+            args.vcache = const_cast<void*>(v_cache);
             args.slots = fused->slots;
         }
 
-        auto launch = [&]<bool F>() {
+        auto launch = [&]<bool F, bool F8>() {
 #define TVLLM_DEC(GP)                                                                \
     do {                                                                             \
         if (tuning().tiles == 4 && threads <= 256)                                   \
-            paged_decode_d128<T, GP, 4, 4, F><<<int(grid), threads, 0, s>>>(args);    \
+            paged_decode_d128<T, GP, 4, 4, F, F8><<<int(grid), threads, 0, s>>>(args); \
         else                                                                         \
-            paged_decode_d128<T, GP, 2, kMaxWaves, F>                                \
+            paged_decode_d128<T, GP, 2, kMaxWaves, F, F8>                            \
                 <<<int(grid), threads, 0, s>>>(args);                                \
     } while (0)
             // Groups above 4 carry 64+ accumulator registers per lane: one
@@ -908,18 +970,22 @@ int paged_decode_impl(
             else if (group <= 2) TVLLM_DEC(2);
             else if (group <= 4) TVLLM_DEC(4);
             else if (group <= 8)
-                paged_decode_d128<T, 8, 1, kMaxWaves, F><<<int(grid), threads, 0, s>>>(args);
+                paged_decode_d128<T, 8, 1, kMaxWaves, F, F8>
+                    <<<int(grid), threads, 0, s>>>(args);
             else
-                paged_decode_d128<T, 16, 1, kMaxWaves, F><<<int(grid), threads, 0, s>>>(args);
+                paged_decode_d128<T, 16, 1, kMaxWaves, F, F8>
+                    <<<int(grid), threads, 0, s>>>(args);
         };
-        if (fused) launch.template operator()<true>();
-        else launch.template operator()<false>();
+        if (fused && f8) launch.template operator()<true, true>();
+        else if (fused) launch.template operator()<true, false>();
+        else if (f8) launch.template operator()<false, true>();
+        else launch.template operator()<false, false>();
 #undef TVLLM_DEC
         const int st = launch_status("paged_decode");
         if (st != TVLLM_OK || plan.grid <= 1) return st;
         paged_decode_merge<T><<<int(num_rows * num_heads), 64, 0, s>>>(
             args.part_o, args.part_ml, static_cast<T*>(out), rows, out_token_stride,
-            out_head_stride, int(num_heads), int(plan.grid), int(head_dim));
+            out_head_stride, int(num_heads), int(plan.grid), int(head_dim), v_scale);
         return launch_status("paged_decode merge");
     });
 }
@@ -934,12 +1000,14 @@ extern "C" int tvllm_paged_decode(
     const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
     int64_t block_size, int64_t max_context_len, float scale, void* workspace,
-    int64_t workspace_bytes, int dtype, tvllm_stream_t stream) {
+    int64_t workspace_bytes, int dtype, int cache_dtype, float k_scale, float v_scale,
+    tvllm_stream_t stream) {
     return paged_decode_impl(q, q_token_stride, q_head_stride, k_cache, v_cache, out,
                              out_token_stride, out_head_stride, rows, blocks, offsets,
                              lengths, num_rows, num_heads, num_kv_heads, head_dim,
                              num_slots, block_size, max_context_len, scale, workspace,
-                             workspace_bytes, dtype, stream, nullptr);
+                             workspace_bytes, dtype, cache_dtype, k_scale, v_scale, stream,
+                             nullptr);
 }
 
 extern "C" int tvllm_paged_decode_qk_norm_rope(
@@ -951,8 +1019,8 @@ extern "C" int tvllm_paged_decode_qk_norm_rope(
     const int64_t* rows, const int64_t* blocks, const int64_t* offsets,
     const int64_t* lengths, int64_t num_rows, int64_t num_heads, int64_t num_kv_heads,
     int64_t head_dim, int64_t num_slots, int64_t block_size, int64_t max_context_len,
-    float scale, void* workspace, int64_t workspace_bytes, int dtype,
-    tvllm_stream_t stream) {
+    float scale, void* workspace, int64_t workspace_bytes, int dtype, int cache_dtype,
+    float k_scale, float v_scale, tvllm_stream_t stream) {
     TVLLM_CHECK(head_dim == 128, "paged_decode_qk_norm_rope: head_dim must be 128");
     TVLLM_CHECK(num_rows == 0 || (k && v && q_weight && k_weight && cos && sin && slots),
                 "paged_decode_qk_norm_rope: null pointer");
@@ -964,5 +1032,6 @@ extern "C" int tvllm_paged_decode_qk_norm_rope(
                              out_token_stride, out_head_stride, rows, blocks, offsets,
                              lengths, num_rows, num_heads, num_kv_heads, head_dim,
                              num_slots, block_size, max_context_len, scale, workspace,
-                             workspace_bytes, dtype, stream, &f);
+                             workspace_bytes, dtype, cache_dtype, k_scale, v_scale, stream,
+                             &f);
 }

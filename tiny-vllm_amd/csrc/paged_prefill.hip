@@ -81,8 +81,8 @@ template <typename T>
 struct PrefillArgs {
     const T* q;
     int64_t qts, qhs;
-    const T* k;
-    const T* v;
+    const void* k;  // cache rows: T elements, or FP8 E4M3 bytes (F8 kernels)
+    const void* v;
     T* out;
     int64_t ots, ohs;
     const int64_t* q_offsets;
@@ -90,7 +90,8 @@ struct PrefillArgs {
     const int64_t* block_offsets;
     const int64_t* context_lens;
     int heads, kv_heads, block_size, block_shift, q_tiles, grid;
-    float scale_log2;
+    float scale_log2;  // softmax scale * log2(e) (* k_scale for an FP8 cache)
+    float v_scale;     // FP8 cache: V dequantisation scale (1 otherwise)
 };
 
 __device__ __forceinline__ float as_f(uint32_t x) { return __uint_as_float(x); }
@@ -106,9 +107,13 @@ __device__ __forceinline__ float pair_sum(float x) {
     return as_f(r[0]) + as_f(r[1]);
 }
 
-template <typename T, int W, bool QUAD>
+// F8: K/V rows are FP8 E4M3 bytes; staging loads 8 bytes per 8-element
+// piece and widens them exactly to T before the LDS store.
+template <typename T, int W, bool QUAD, bool F8>
 __global__ void __launch_bounds__(64 * W, 8 / W)  // two waves per SIMD
 paged_prefill_d128(PrefillArgs<T> a) {
+    using SU = std::conditional_t<F8, uint2, U16x8>;  // one staged piece
+    constexpr int EB = F8 ? 1 : int(sizeof(T));        // bytes per cached element
     constexpr int NTH = 64 * W;
     constexpr int BQ = 32 * W;           // queries per workgroup
     constexpr int JOBS = 2 * 16 * 16;    // (K|V) x 16 token quads x 16 pieces
@@ -206,31 +211,38 @@ paged_prefill_d128(PrefillArgs<T> a) {
             }
         }
     };
-    auto load_tile = [&](int tile_base, const uint32_t (&ids)[JPT][4], U16x8 (&stage)[JPT][4]) {
+    auto load_tile = [&](int tile_base, const uint32_t (&ids)[JPT][4], SU (&stage)[JPT][4]) {
 #pragma unroll
         for (int r = 0; r < JPT; ++r) {
             bool is_v;
             int tq, piece;
             job_coords(r, is_v, tq, piece);
             const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
-            const T* src = (is_v ? a.v : a.k) + kvh * D + piece * 8;
+            const char* src = static_cast<const char*>(is_v ? a.v : a.k) +
+                              int64_t(kvh * D + piece * 8) * EB;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int t = min(t0 + 4 * tq + e, end1);
                 uint32_t slot;
                 if constexpr (quad_pages) slot = ids[r][0] * uint32_t(bs) + uint32_t(t & (bs - 1));
                 else slot = ids[r][e] * uint32_t(bs) + uint32_t(t % bs);
-                stage[r][e] = *reinterpret_cast<const U16x8*>(src + uint64_t(slot) * slot_elems);
+                stage[r][e] = *reinterpret_cast<const SU*>(src + uint64_t(slot) * slot_elems * EB);
             }
         }
     };
-    auto store_tile = [&](int tile_base, const U16x8 (&stage)[JPT][4]) {
+    auto store_tile = [&](int tile_base, const SU (&raw)[JPT][4]) {
 #pragma unroll
         for (int r = 0; r < JPT; ++r) {
             bool is_v;
             int tq, piece;
             job_coords(r, is_v, tq, piece);
             const int buf = (tile_base + lead_of(is_v)) & 1;
+            U16x8 pc[4];  // the job's four token pieces as T elements
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (F8) pc[e] = fp8x8_widen<T>(raw[r][e]);
+                else pc[e] = raw[r][e];
+            }
             if (is_v) {
                 // V^T: dim row (piece*8 + dd), the quad's 4 tokens -> one 8-byte write;
                 // v_perm picks the low (even dd) or high (odd dd) halves of two words.
@@ -238,15 +250,15 @@ paged_prefill_d128(PrefillArgs<T> a) {
                 for (int dd = 0; dd < 8; ++dd) {
                     const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
                     uint2 w;
-                    w.x = __builtin_amdgcn_perm(stage[r][1].w[dd >> 1], stage[r][0].w[dd >> 1], sel);
-                    w.y = __builtin_amdgcn_perm(stage[r][3].w[dd >> 1], stage[r][2].w[dd >> 1], sel);
+                    w.x = __builtin_amdgcn_perm(pc[1].w[dd >> 1], pc[0].w[dd >> 1], sel);
+                    w.y = __builtin_amdgcn_perm(pc[3].w[dd >> 1], pc[2].w[dd >> 1], sel);
                     *reinterpret_cast<uint2*>(&vt[buf][(piece * 8 + dd) * V_LD + vt_pos(tq)]) = w;
                 }
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     *reinterpret_cast<U16x8*>(&ks[buf][(4 * tq + e) * K_LD + piece * 8]) =
-                        stage[r][e];
+                        pc[e];
             }
         }
     };
@@ -340,10 +352,10 @@ paged_prefill_d128(PrefillArgs<T> a) {
     // Prologue: K(0), K(1), V(0) into LDS, and K(2), V(1) into registers,
     // with the three tiles' block ids and rows fetched concurrently. (The
     // first staging call also writes V(0) into the spare V buffer.)
-    U16x8 stage[JPT][4];
+    SU stage[JPT][4];
     uint32_t ids[JPT][4];
     {
-        U16x8 st0[JPT][4], st1[JPT][4];
+        SU st0[JPT][4], st1[JPT][4];
         uint32_t id0[JPT][4], id1[JPT][4];
         load_ids(-2, id0);
         load_ids(-1, id1);
@@ -392,7 +404,7 @@ paged_prefill_d128(PrefillArgs<T> a) {
     const float l = pair_sum(l_run);
     const int64_t qi = wq0 + col;
     if (qi >= q_len) return;
-    const float inv = 1.f / l;
+    const float inv = a.v_scale / l;
     T* orow = a.out + (q_begin + qi) * a.ots + h * a.ohs + 4 * half;
 #pragma unroll
     for (int n = 0; n < 4; ++n)
@@ -417,8 +429,15 @@ extern "C" int tvllm_paged_prefill(
     const int64_t* block_offsets, const int64_t* context_lens, int64_t num_items,
     int64_t max_query_len, int64_t num_heads, int64_t num_kv_heads,
     int64_t head_dim, int64_t num_slots, int64_t block_size, float scale,
-    int dtype, tvllm_stream_t stream) {
+    int dtype, int cache_dtype, float k_scale, float v_scale, tvllm_stream_t stream) {
     TVLLM_CHECK(head_dim == 128, "paged_prefill: head_dim must be 128");
+    const bool f8 = cache_dtype == TVLLM_FP8_E4M3;
+    TVLLM_CHECK(f8 || cache_dtype == dtype,
+                "paged_prefill: KV cache dtype must match Q or be FP8 E4M3");
+    TVLLM_CHECK(k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY,
+                "paged_prefill: KV scales must be positive and finite");
+    TVLLM_CHECK(f8 || (k_scale == 1.f && v_scale == 1.f),
+                "paged_prefill: KV scales apply to an FP8 cache only");
     TVLLM_CHECK(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
                 "paged_prefill: invalid GQA geometry");
     TVLLM_CHECK(block_size > 0 && num_slots % block_size == 0,
@@ -455,8 +474,8 @@ extern "C" int tvllm_paged_prefill(
         args.q = static_cast<const T*>(q);
         args.qts = q_token_stride;
         args.qhs = q_head_stride;
-        args.k = static_cast<const T*>(k_cache);
-        args.v = static_cast<const T*>(v_cache);
+        args.k = k_cache;
+        args.v = v_cache;
         args.out = static_cast<T*>(out);
         args.ots = out_token_stride;
         args.ohs = out_head_stride;
@@ -469,17 +488,22 @@ extern "C" int tvllm_paged_prefill(
         args.block_size = int(block_size);
         args.q_tiles = int(q_tiles);
         args.grid = int(grid);
-        args.scale_log2 = scale * kLog2e;
+        args.scale_log2 = scale * kLog2e * k_scale;
+        args.v_scale = v_scale;
         args.block_shift = (block_size & (block_size - 1)) == 0
                                ? __builtin_ctzll(uint64_t(block_size)) : -1;
         const bool quad = args.block_shift >= 2;
-        if (waves == 8) {
-            if (quad) paged_prefill_d128<T, 8, true><<<int(grid), 512, 0, s>>>(args);
-            else paged_prefill_d128<T, 8, false><<<int(grid), 512, 0, s>>>(args);
-        } else {
-            if (quad) paged_prefill_d128<T, 4, true><<<int(grid), 256, 0, s>>>(args);
-            else paged_prefill_d128<T, 4, false><<<int(grid), 256, 0, s>>>(args);
-        }
+        auto go = [&]<bool F8>() {
+            if (waves == 8) {
+                if (quad) paged_prefill_d128<T, 8, true, F8><<<int(grid), 512, 0, s>>>(args);
+                else paged_prefill_d128<T, 8, false, F8><<<int(grid), 512, 0, s>>>(args);
+            } else {
+                if (quad) paged_prefill_d128<T, 4, true, F8><<<int(grid), 256, 0, s>>>(args);
+                else paged_prefill_d128<T, 4, false, F8><<<int(grid), 256, 0, s>>>(args);
+            }
+        };
+        if (f8) go.template operator()<true>();
+        else go.template operator()<false>();
         return launch_status("paged_prefill");
     });
 }

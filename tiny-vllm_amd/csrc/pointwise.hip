@@ -274,8 +274,9 @@ silu_mul_kernel(const T* __restrict__ x, int64_t rows, int64_t heads, int half,
 // One wave per (token, head) row. Rows [0, T*Hq) are query heads, rows
 // [T*Hq, T*(Hq+Hkv)) key heads; a key-row wave also copies the matching V
 // row into the cache when the KV write is fused. Lane l owns the rotation
-// pairs (d, d + D/2) for d = l, l + 64, ...; NP pairs per lane.
-template <typename T, int NP>
+// pairs (d, d + D/2) for d = l, l + 64, ...; NP pairs per lane. F8: the
+// cache holds FP8 E4M3 bytes, x -> fp8(clamp(round_T(x) * inv_scale)).
+template <typename T, int NP, bool F8>
 __global__ void __launch_bounds__(256)
 qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
                     const T* __restrict__ k, int64_t kts, int64_t khs,
@@ -284,9 +285,9 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
                     int64_t tokens, int heads, int kv_heads, int head_dim,
                     float q_eps, float k_eps, T* __restrict__ q_out,
                     T* __restrict__ k_out, const T* __restrict__ v, int64_t vts,
-                    int64_t vhs, T* __restrict__ key_cache,
-                    T* __restrict__ value_cache,
-                    const int64_t* __restrict__ slots) {
+                    int64_t vhs, void* __restrict__ key_cache,
+                    void* __restrict__ value_cache,
+                    const int64_t* __restrict__ slots, float k_inv, float v_inv) {
     const int lane = threadIdx.x & 63;
     const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int64_t q_rows = tokens * heads;
@@ -322,12 +323,17 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
     const float inv = rsqrtf(ss * (1.0f / float(head_dim)) + eps);
 
     int64_t slot = -1;
-    T* dst;
+    T* dst = nullptr;
+    uint8_t* dst8 = nullptr;  // FP8 cache row
     if (is_q) {
         dst = q_out + r * head_dim;
     } else if (key_cache != nullptr) {
         slot = slots[tok];
-        dst = slot >= 0 ? key_cache + (slot * kv_heads + h) * head_dim : nullptr;
+        if (slot >= 0) {
+            const int64_t off = (slot * kv_heads + h) * head_dim;
+            if constexpr (F8) dst8 = static_cast<uint8_t*>(key_cache) + off;
+            else dst = static_cast<T*>(key_cache) + off;
+        }
     } else {
         dst = k_out + r * head_dim;
     }
@@ -349,6 +355,13 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
             dst[d] = static_cast<T>(o1);
             dst[d + half] = static_cast<T>(o2);
         }
+        if constexpr (F8) {
+            if (dst8 != nullptr) {
+                const uint32_t b = fp8x4_pack(rnd<T>(o1) * k_inv, rnd<T>(o2) * k_inv, 0.f, 0.f);
+                dst8[d] = uint8_t(b);
+                dst8[d + half] = uint8_t(b >> 8);
+            }
+        }
         if (dense_k != nullptr) {
             dense_k[d] = static_cast<T>(o1);
             dense_k[d + half] = static_cast<T>(o2);
@@ -357,8 +370,15 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
 
     if (!is_q && key_cache != nullptr && slot >= 0) {
         const T* vsrc = v + tok * vts + h * vhs;
-        T* vdst = value_cache + (slot * kv_heads + h) * head_dim;
-        for (int d = lane; d < head_dim; d += 64) vdst[d] = vsrc[d];
+        const int64_t off = (slot * kv_heads + h) * head_dim;
+        if constexpr (F8) {
+            uint8_t* vdst = static_cast<uint8_t*>(value_cache) + off;
+            for (int d = lane; d < head_dim; d += 64)
+                vdst[d] = uint8_t(fp8x4_pack(to_f<T>(vsrc[d]) * v_inv, 0.f, 0.f, 0.f));
+        } else {
+            T* vdst = static_cast<T*>(value_cache) + off;
+            for (int d = lane; d < head_dim; d += 64) vdst[d] = vsrc[d];
+        }
     }
 }
 
@@ -479,9 +499,17 @@ extern "C" int tvllm_qk_norm_rope(
     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, float q_eps,
     float k_eps, void* q_out, void* k_out, const void* v, int64_t v_token_stride,
     int64_t v_head_stride, void* key_cache, void* value_cache,
-    const int64_t* slots, int64_t num_slots, int dtype, tvllm_stream_t stream) {
+    const int64_t* slots, int64_t num_slots, int dtype, int cache_dtype, float k_scale,
+    float v_scale, tvllm_stream_t stream) {
     TVLLM_CHECK(tokens >= 0 && num_heads > 0 && num_kv_heads > 0,
                 "qk_norm_rope: Q/K must have positive head counts");
+    const bool f8 = cache_dtype == TVLLM_FP8_E4M3;
+    TVLLM_CHECK(f8 || cache_dtype == dtype,
+                "qk_norm_rope: KV cache dtype must match Q/K or be FP8 E4M3");
+    TVLLM_CHECK(k_scale > 0.f && v_scale > 0.f && k_scale < INFINITY && v_scale < INFINITY,
+                "qk_norm_rope: KV scales must be positive and finite");
+    TVLLM_CHECK(f8 || (k_scale == 1.f && v_scale == 1.f),
+                "qk_norm_rope: KV scales apply to an FP8 cache only");
     TVLLM_CHECK(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 1024,
                 "qk_norm_rope: RoPE input must have an even head_dim <= 1024");
     TVLLM_CHECK(tokens * (num_heads + num_kv_heads) <= INT32_MAX * int64_t(4),
@@ -500,8 +528,10 @@ extern "C" int tvllm_qk_norm_rope(
         using T = typename Elem<DT>::T;
         const int blocks = int((rows + 3) / 4);
         const int half = int(head_dim / 2);
+        const float k_inv = 1.f / k_scale, v_inv = 1.f / v_scale;
+        auto go = [&]<bool F8>() {
 #define TVLLM_QKR(NP)                                                            \
-    qk_norm_rope_kernel<T, NP><<<blocks, 256, 0, s>>>(                           \
+    qk_norm_rope_kernel<T, NP, F8><<<blocks, 256, 0, s>>>(                       \
         static_cast<const T*>(q), q_token_stride, q_head_stride,                 \
         static_cast<const T*>(k), k_token_stride, k_head_stride,                 \
         static_cast<const T*>(q_weight), static_cast<const T*>(k_weight),        \
@@ -509,12 +539,15 @@ extern "C" int tvllm_qk_norm_rope(
         int(num_heads), int(num_kv_heads), int(head_dim), q_eps, k_eps,          \
         static_cast<T*>(q_out), static_cast<T*>(k_out),                          \
         static_cast<const T*>(v), v_token_stride, v_head_stride,                 \
-        static_cast<T*>(key_cache), static_cast<T*>(value_cache), slots)
-        if (half <= 64) TVLLM_QKR(1);
-        else if (half <= 128) TVLLM_QKR(2);
-        else if (half <= 256) TVLLM_QKR(4);
-        else TVLLM_QKR(8);
+        key_cache, value_cache, slots, k_inv, v_inv)
+            if (half <= 64) TVLLM_QKR(1);
+            else if (half <= 128) TVLLM_QKR(2);
+            else if (half <= 256) TVLLM_QKR(4);
+            else TVLLM_QKR(8);
 #undef TVLLM_QKR
+        };
+        if (f8) go.template operator()<true>();
+        else go.template operator()<false>();
         return launch_status("qk_norm_rope");
     });
 }

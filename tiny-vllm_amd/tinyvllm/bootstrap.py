@@ -44,7 +44,8 @@ def build_engine(model, *, max_model_len: int, max_num_seqs: int = 64,
                  prefill_reserve_tokens: int = 128, prefill_reserve_requests: int = 1,
                  attention_backend: str = "hip", enforce_eager: bool = False,
                  enable_prefix_caching: bool = True, eos_token_ids=None,
-                 graph_sizes=None, clock=None) -> "Engine":
+                 graph_sizes=None, clock=None, kv_cache_dtype: torch.dtype | None = None,
+                 kv_scales: tuple[float, float] = (1.0, 1.0)) -> "Engine":
     """Engine around an already built model (random-init benchmarks, tests)."""
     from tinyvllm.engine import Engine
     from tinyvllm.executor import Executor
@@ -53,7 +54,8 @@ def build_engine(model, *, max_model_len: int, max_num_seqs: int = 64,
     executor = Executor(model, block_size=kv_block_size, num_blocks=num_blocks,
                         max_model_len=max_model_len, max_num_seqs=max_num_seqs,
                         attention_backend=attention_backend, enforce_eager=enforce_eager,
-                        graph_sizes=graph_sizes)
+                        graph_sizes=graph_sizes, kv_cache_dtype=kv_cache_dtype,
+                        kv_scales=kv_scales)
     scheduler = Scheduler(
         max_active_requests=max_num_seqs, max_step_requests=max_num_seqs,
         max_scheduled_tokens=max_num_batched_tokens, prefill_chunk_size=prefill_chunk_size,
@@ -77,6 +79,7 @@ def create_engine(config: EngineConfig) -> "Engine":
         raise ValueError("max_model_len exceeds model position capacity")
     device = torch.device("cuda", torch.cuda.current_device())
     dtype = getattr(torch, config.dtype)
+    kv_dtype = torch.float8_e4m3fn if config.kv_cache_dtype == "fp8_e4m3" else dtype
     logger.info("Loading model=%s device=%s dtype=%s attention_backend=%s",
                 config.model, device, config.dtype, config.attention_backend)
     model = Qwen3ForCausalLM.from_pretrained(config.model, device=device, dtype=dtype)
@@ -86,7 +89,7 @@ def create_engine(config: EngineConfig) -> "Engine":
     per_block = PagedKVCache.bytes_per_block(
         num_layers=model_config.num_hidden_layers, block_size=config.kv_block_size,
         num_kv_heads=model_config.num_key_value_heads, head_dim=model_config.head_dim,
-        dtype=dtype)
+        dtype=kv_dtype)
     reserved = 0
     if config.attention_backend != "reference":
         reserved = DecodeInputs.device_bytes(max_num_seqs=config.max_num_seqs,
@@ -105,7 +108,8 @@ def create_engine(config: EngineConfig) -> "Engine":
         prefill_reserve_requests=config.prefill_reserve_requests,
         attention_backend=config.attention_backend, enforce_eager=config.enforce_eager,
         enable_prefix_caching=config.enable_prefix_caching,
-        eos_token_ids=model_config.eos_token_id)
+        eos_token_ids=model_config.eos_token_id, kv_cache_dtype=kv_dtype,
+        kv_scales=(config.kv_k_scale, config.kv_v_scale))
     logger.info("engine ready in %.1fs: %d KV blocks of %d tokens",
                 time.perf_counter() - started, blocks, config.kv_block_size)
     return engine

@@ -10,13 +10,17 @@ from tinyvllm._validation import _check_non_negative_int, _check_positive_int
 
 DType = Literal["bfloat16", "float16"]
 BACKENDS = ("hip", "reference", "cuda")
+KV_CACHE_DTYPES = ("auto", "fp8_e4m3")
 
 
 @dataclass(frozen=True, slots=True)
 class EngineConfig:
     """Same fields and defaults as the reference. ``attention_backend`` is
     "hip" (native kernels, default) or "reference" (torch SDPA gather path);
-    "cuda", the reference's name for its native backend, maps to "hip"."""
+    "cuda", the reference's name for its native backend, maps to "hip".
+    Beyond the reference: ``kv_cache_dtype`` "auto" stores K/V in the model
+    dtype, "fp8_e4m3" in OCP FP8 E4M3 (one byte per element) with the scales
+    ``kv_k_scale``/``kv_v_scale`` (stored = x / scale, saturated to +-448)."""
 
     model: Path
     dtype: DType = "bfloat16"
@@ -32,6 +36,9 @@ class EngineConfig:
     prefill_reserve_requests: int = 1
     enforce_eager: bool = False
     enable_prefix_caching: bool = True
+    kv_cache_dtype: str = "auto"
+    kv_k_scale: float = 1.0
+    kv_v_scale: float = 1.0
 
     def __post_init__(self) -> None:
         model = Path(self.model).expanduser().resolve()
@@ -42,6 +49,15 @@ class EngineConfig:
             raise ValueError(f"unsupported dtype: {self.dtype}")
         if self.attention_backend not in BACKENDS:
             raise ValueError(f"unsupported attention backend: {self.attention_backend}")
+        if self.kv_cache_dtype not in KV_CACHE_DTYPES:
+            raise ValueError(f"unsupported kv_cache_dtype: {self.kv_cache_dtype}")
+        for name in ("kv_k_scale", "kv_v_scale"):
+            value = getattr(self, name)
+            if type(value) not in (int, float) or not 0.0 < value < math.inf:
+                raise ValueError(f"{name} must be a positive finite number")
+        if self.kv_cache_dtype == "auto" and (self.kv_k_scale != 1.0
+                                              or self.kv_v_scale != 1.0):
+            raise ValueError("KV scales apply to kv_cache_dtype fp8_e4m3 only")
         for name in ("enforce_eager", "enable_prefix_caching"):
             if type(getattr(self, name)) is not bool:
                 raise TypeError(f"{name} must be bool")

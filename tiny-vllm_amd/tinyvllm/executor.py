@@ -53,11 +53,14 @@ class Executor:
                  max_model_len: int | None = None, sampler: Sampler | None = None,
                  max_num_seqs: int = 64, attention_backend: str = "hip",
                  enforce_eager: bool = False,
-                 graph_sizes: tuple[int, ...] | None = None) -> None:
+                 graph_sizes: tuple[int, ...] | None = None,
+                 kv_cache_dtype: torch.dtype | None = None,
+                 kv_scales: tuple[float, float] = (1.0, 1.0)) -> None:
         self.runner = ModelRunner(model, block_size=block_size, num_blocks=num_blocks,
                                   max_model_len=max_model_len, max_num_seqs=max_num_seqs,
                                   attention_backend=attention_backend,
-                                  enforce_eager=enforce_eager, graph_sizes=graph_sizes)
+                                  enforce_eager=enforce_eager, graph_sizes=graph_sizes,
+                                  kv_cache_dtype=kv_cache_dtype, kv_scales=kv_scales)
         self.capabilities = ExecutorCapabilities(
             vocab_size=model.config.vocab_size,
             max_model_len=self.runner.max_model_len,

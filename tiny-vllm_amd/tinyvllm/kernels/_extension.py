@@ -19,7 +19,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libtinyvllm_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -30,17 +30,18 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_last_error": (ctypes.c_char_p, []),
     "tvllm_abi_version": (_INT, []),
     "tvllm_store_kv": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, _P,
-                              _I64, _I64, _I64, _I64, _INT, _P]),
+                              _I64, _I64, _I64, _I64, _INT, _INT, _F32, _F32, _P]),
     "tvllm_paged_decode_workspace_size": (_I64, [_I64] * 6),
     "tvllm_paged_decode_split_plan": (_I64, [_I64] * 6),
     "tvllm_paged_decode": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64,
                                   _P, _P, _P, _P, _I64, _I64, _I64, _I64,
-                                  _I64, _I64, _I64, _F32, _P, _I64, _INT, _P]),
+                                  _I64, _I64, _I64, _F32, _P, _I64, _INT, _INT, _F32,
+                                  _F32, _P]),
     "tvllm_paged_decode_qk_norm_rope": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64,
                                                _I64, _P, _P, _P, _P, _F32, _F32, _P, _P,
                                                _P, _P, _I64, _I64, _P, _P, _P, _P, _I64,
                                                _I64, _I64, _I64, _I64, _I64, _I64, _F32,
-                                               _P, _I64, _INT, _P]),
+                                               _P, _I64, _INT, _INT, _F32, _F32, _P]),
     "tvllm_rms_norm": (_INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64,
                               _P, _P, _F32, _INT, _P]),
     "tvllm_silu_and_mul": (_INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _INT, _P]),
@@ -49,19 +50,20 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_qk_norm_rope": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P,
                                   _P, _I64, _I64, _I64, _I64, _F32, _F32, _P,
                                   _P, _P, _I64, _I64, _P, _P, _P, _I64, _INT,
-                                  _P]),
+                                  _INT, _F32, _F32, _P]),
     "tvllm_argmax": (_INT, [_P, _I64, _I64, _I64, _P, _INT, _P]),
     "tvllm_sample_workspace_size": (_I64, [_I64, _I64]),
     "tvllm_sample": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
                             _I64, _INT, _P]),
     "tvllm_paged_prefill": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _P,
                                    _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
-                                   _I64, _I64, _F32, _INT, _P]),
+                                   _I64, _I64, _F32, _INT, _INT, _F32, _F32, _P]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
-DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2,
+               torch.float8_e4m3fn: 3}  # FP8 E4M3: KV-cache storage only
 
 
 @lru_cache(maxsize=1)
@@ -101,6 +103,11 @@ def dtype_code(dtype: torch.dtype) -> int:
         return DTYPE_CODES[dtype]
     except KeyError:
         raise RuntimeError(f"unsupported dtype {dtype}") from None
+
+
+def cache_format(cache) -> tuple[int, float, float]:
+    """(dtype code, k_scale, v_scale) of a PagedKVCache for the C ABI."""
+    return dtype_code(cache.dtype), float(cache.k_scale), float(cache.v_scale)
 
 
 def stream_of(device: torch.device) -> int:

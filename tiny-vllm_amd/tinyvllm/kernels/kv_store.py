@@ -5,7 +5,7 @@ import torch
 
 from tinyvllm._validation import _check_non_negative_int
 from tinyvllm.kernels._extension import (
-    check, dtype_code, load_kernels, require_gpu, stream_of,
+    cache_format, check, dtype_code, load_kernels, require_gpu, stream_of,
 )
 from tinyvllm.paged_kv import PagedKVCache
 
@@ -26,7 +26,7 @@ def store_kv(
     device = require_gpu(key, value, key_cache, value_cache, slots)
     if key.dtype not in (torch.float16, torch.bfloat16):
         raise RuntimeError("KV store requires float16 or bfloat16")
-    for tensor in (value, key_cache, value_cache):
+    for tensor in (value,) if cache.fp8 else (value, key_cache, value_cache):
         if tensor.dtype != key.dtype:
             raise RuntimeError("KV dtype mismatch")
     if key.dim() != 3 or value.dim() != 3:
@@ -45,5 +45,5 @@ def store_kv(
         key.stride(0), key.stride(1), value.stride(0), value.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(), slots.data_ptr(),
         key.shape[0], key.shape[1], key.shape[2], key_cache.shape[0],
-        dtype_code(key.dtype), stream_of(device),
+        dtype_code(key.dtype), *cache_format(cache), stream_of(device),
     ))

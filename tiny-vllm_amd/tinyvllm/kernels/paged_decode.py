@@ -5,7 +5,7 @@ from __future__ import annotations
 import torch
 
 from tinyvllm.kernels._extension import (
-    check, dtype_code, load_kernels, require_gpu, stream_of,
+    cache_format, check, dtype_code, load_kernels, require_gpu, stream_of,
 )
 from tinyvllm.paged_kv import PagedKVCache
 from tinyvllm.runtime.contracts import SingleQueryMetadata
@@ -59,7 +59,7 @@ def paged_decode_attention(
         raise RuntimeError("Q must be a GPU [tokens, heads, dim] tensor")
     if q.dtype not in (torch.float16, torch.bfloat16):
         raise RuntimeError("Q must use float16 or bfloat16")
-    if k.dtype != q.dtype or output.dtype != q.dtype:
+    if (k.dtype != q.dtype and not cache.fp8) or output.dtype != q.dtype:
         raise RuntimeError("Q/K/V/output must share device and dtype")
     if output.shape != q.shape or q.stride(2) != 1 or output.stride(2) != 1:
         raise RuntimeError("output must match Q shape with unit last stride")
@@ -88,7 +88,7 @@ def paged_decode_attention(
         num_rows, heads, cache.num_kv_heads, dim, cache.num_slots,
         cache.block_size, max_len, float(scale),
         workspace.data_ptr() if need else None, need,
-        dtype_code(q.dtype), stream_of(device),
+        dtype_code(q.dtype), *cache_format(cache), stream_of(device),
     ))
 
 
@@ -127,7 +127,8 @@ def paged_decode_qk_norm_rope(
     if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape or q.shape[2] != 128:
         raise RuntimeError("Q/K/V must be [tokens, heads, 128] tensors")
     if q.dtype not in (torch.float16, torch.bfloat16) or any(
-            t.dtype != q.dtype for t in (k, v, query_weight, key_weight, cos, sin, kc, output)):
+            t.dtype != q.dtype for t in (k, v, query_weight, key_weight, cos, sin, output)) \
+            or (kc.dtype != q.dtype and not cache.fp8):
         raise RuntimeError("Q/K/V, weights, RoPE tables and cache must share a half dtype")
     if any(t.stride(-1) != 1 for t in (q, k, v, output)) or output.shape != q.shape:
         raise RuntimeError("Q/K/V/output rows must have unit last stride")
@@ -165,5 +166,5 @@ def paged_decode_qk_norm_rope(
         m.context_lens.data_ptr(), num_rows, heads, cache.num_kv_heads, 128,
         cache.num_slots, cache.block_size, max_len, float(scale),
         workspace.data_ptr() if need else None, need, dtype_code(q.dtype),
-        stream_of(device),
+        *cache_format(cache), stream_of(device),
     ))

@@ -9,7 +9,7 @@ from __future__ import annotations
 import torch
 
 from tinyvllm.kernels._extension import (
-    check, dtype_code, load_kernels, require_gpu, stream_of,
+    cache_format, check, dtype_code, load_kernels, require_gpu, stream_of,
 )
 from tinyvllm.paged_kv import PagedKVCache
 from tinyvllm.runtime.contracts import MultiQueryMetadata
@@ -34,7 +34,7 @@ def paged_prefill_attention(
     if q.dim() != 3 or output.shape != q.shape:
         raise RuntimeError("Q/output must be [tokens, heads, dim] tensors")
     if q.dtype not in (torch.float16, torch.bfloat16) or output.dtype != q.dtype \
-            or k.dtype != q.dtype:
+            or (k.dtype != q.dtype and not cache.fp8):
         raise RuntimeError("Q/K/V/output must share a float16 or bfloat16 dtype")
     if q.stride(2) != 1 or output.stride(2) != 1:
         raise RuntimeError("Q/output rows must have unit last stride")
@@ -54,5 +54,5 @@ def paged_prefill_attention(
         m.block_table_offsets.data_ptr(), m.context_lens.data_ptr(),
         items, m.max_query_len, q.shape[1], cache.num_kv_heads, q.shape[2],
         cache.num_slots, cache.block_size, float(scale),
-        dtype_code(q.dtype), stream_of(device),
+        dtype_code(q.dtype), *cache_format(cache), stream_of(device),
     ))

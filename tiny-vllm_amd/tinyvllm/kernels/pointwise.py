@@ -177,7 +177,7 @@ def qk_norm_rope(
             sin.data_ptr(), query.shape[0], query.shape[1], key.shape[1],
             query.shape[2], float(query_eps), float(key_eps),
             q_out.data_ptr(), k_out.data_ptr(), None, 0, 0, None, None, None, 0,
-            dtype_code(query.dtype), stream_of(device),
+            dtype_code(query.dtype), dtype_code(query.dtype), 1.0, 1.0, stream_of(device),
         ))
     return q_out, k_out
 
@@ -197,12 +197,16 @@ def qk_norm_rope_store(
     slots: torch.Tensor,
     *,
     key_out: bool = False,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """qk_norm_rope with the slot-mapped KV write fused in (no reference
     counterpart: the reference runs store_kv after it,
     runtime/attention.py:219-233). The rotated K and the V rows go straight to
     ``key_cache/value_cache[slots[t]]`` (slot -1 skips). Returns the rotated
-    Q and, if ``key_out``, a dense copy of the rotated K."""
+    Q and, if ``key_out``, a dense copy of the rotated K. An FP8 E4M3 cache
+    (``torch.float8_e4m3fn``) stores ``fp8(clamp(x / scale))`` of each element
+    with the given ``k_scale``/``v_scale``."""
     lib = load_kernels()
     device = require_gpu(query, key, value, query_weight, key_weight, cos, sin,
                          key_cache, value_cache, slots)
@@ -211,7 +215,8 @@ def qk_norm_rope_store(
         raise RuntimeError("V must match K's shape and dtype with unit last stride")
     if (key_cache.dim() != 3 or tuple(key_cache.shape[1:]) != tuple(key.shape[1:])
             or value_cache.shape != key_cache.shape or not key_cache.is_contiguous()
-            or not value_cache.is_contiguous() or key_cache.dtype != key.dtype):
+            or not value_cache.is_contiguous() or value_cache.dtype != key_cache.dtype
+            or key_cache.dtype not in (key.dtype, torch.float8_e4m3fn)):
         raise RuntimeError("KV caches must be contiguous [slots, kv_heads, dim]")
     if slots.dtype != torch.long or slots.dim() != 1 or not slots.is_contiguous() \
             or slots.numel() != key.shape[0]:
@@ -228,6 +233,7 @@ def qk_norm_rope_store(
             q_out.data_ptr(), k_out.data_ptr() if k_out is not None else None,
             value.data_ptr(), value.stride(0), value.stride(1),
             key_cache.data_ptr(), value_cache.data_ptr(), slots.data_ptr(),
-            key_cache.shape[0], dtype_code(query.dtype), stream_of(device),
+            key_cache.shape[0], dtype_code(query.dtype), dtype_code(key_cache.dtype),
+            float(k_scale), float(v_scale), stream_of(device),
         ))
     return q_out, k_out

@@ -10,12 +10,21 @@ of contiguous HBM.
 
 Slots and block ids are validated on the CPU before lowering (ModelRunner);
 this class checks shapes/devices only and never synchronises on GPU values.
+
+Optional FP8 layout (no reference counterpart): ``dtype=torch.float8_e4m3fn``
+keeps the same shapes with one byte per element, half the bytes of bf16.
+Writes store ``fp8(clamp(x * (1 / k_scale), -448, 448))`` (nearest-even),
+reads see ``stored * k_scale`` (likewise ``v_scale`` for V); the kernels fold
+the scales into the softmax scale and the output normalisation.
 """
 from __future__ import annotations
 
 import torch
 
 from tinyvllm._validation import _check_non_negative_int, _check_positive_int
+
+FP8_DTYPE = torch.float8_e4m3fn
+_MODEL_DTYPES = (torch.float16, torch.bfloat16)
 
 
 class PagedKVCache:
@@ -31,6 +40,8 @@ class PagedKVCache:
         head_dim: int,
         device: torch.device | str,
         dtype: torch.dtype,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
     ) -> None:
         for name, value in (
             ("num_layers", num_layers),
@@ -40,11 +51,19 @@ class PagedKVCache:
             ("head_dim", head_dim),
         ):
             _check_positive_int(name, value)
+        for name, value in (("k_scale", k_scale), ("v_scale", v_scale)):
+            if type(value) not in (int, float) or not 0.0 < value < float("inf"):
+                raise ValueError(f"{name} must be a positive finite number")
+        if dtype != FP8_DTYPE and (k_scale != 1.0 or v_scale != 1.0):
+            raise ValueError("KV scales apply to an FP8 cache only")
         device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
         self.device = device
         self.dtype = dtype
+        self.fp8 = dtype == FP8_DTYPE
+        self.k_scale = float(k_scale)
+        self.v_scale = float(v_scale)
         self.num_layers = num_layers
         self.num_blocks = num_blocks
         self.block_size = block_size
@@ -78,7 +97,8 @@ class PagedKVCache:
             raise ValueError("K/V rows do not match the slot mapping")
         if key.device != self.device or value.device != self.device:
             raise ValueError("K/V tensors must use the cache device")
-        if key.dtype != self.dtype or value.dtype != self.dtype:
+        allowed = _MODEL_DTYPES if self.fp8 else (self.dtype,)
+        if key.dtype not in allowed or value.dtype != key.dtype:
             raise ValueError("K/V tensors must use the cache dtype")
         from tinyvllm.kernels.kv_store import store_kv
 
@@ -89,12 +109,14 @@ class PagedKVCache:
         layer_idx: int,
         slots: torch.Tensor,
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """Gather rows ``slots`` of one layer (logical order of the caller)."""
+        """Gather rows ``slots`` of one layer (logical order of the caller);
+        an FP8 cache returns the dequantised rows (float32)."""
         self._check_indices(layer_idx, slots)
-        return (
-            self.key[layer_idx].index_select(0, slots),
-            self.value[layer_idx].index_select(0, slots),
-        )
+        keys = self.key[layer_idx].index_select(0, slots)
+        values = self.value[layer_idx].index_select(0, slots)
+        if self.fp8:
+            return keys.float() * self.k_scale, values.float() * self.v_scale
+        return keys, values
 
     def _check_indices(self, layer_idx: int, slots: torch.Tensor) -> None:
         _check_non_negative_int("layer_idx", layer_idx)

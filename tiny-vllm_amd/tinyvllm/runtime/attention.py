@@ -49,6 +49,7 @@ class HipAttention:
         q, _ = qk_norm_rope_store(
             q, k, v, q_weight, k_weight, cos, sin, q_eps, k_eps,
             self.cache.key[layer_idx], self.cache.value[layer_idx], self.kv.slot_mapping,
+            k_scale=self.cache.k_scale, v_scale=self.cache.v_scale,
         )
         self._written_layer = layer_idx
         return q, None, None
@@ -100,6 +101,7 @@ class SDPAAttention:
         for index, slots in enumerate(self.read_slots):
             start, end = self.q_offsets[index], self.q_offsets[index + 1]
             keys, values = self.cache.read(layer_idx, slots)
+            keys, values = keys.to(q.dtype), values.to(q.dtype)
             before, after = self.before[index], self.after[index]
             query = q[start:end].transpose(0, 1).unsqueeze(0)
             mask = None

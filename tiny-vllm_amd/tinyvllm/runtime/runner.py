@@ -38,7 +38,12 @@ class ModelRunner:
         attention_backend: str = "hip",
         enforce_eager: bool = False,
         graph_sizes: tuple[int, ...] | None = None,
+        kv_cache_dtype: torch.dtype | None = None,
+        kv_scales: tuple[float, float] = (1.0, 1.0),
     ) -> None:
+        """``kv_cache_dtype``: None keeps K/V in the model dtype;
+        ``torch.float8_e4m3fn`` stores them as FP8 E4M3 with ``kv_scales``
+        (k_scale, v_scale) - a layout beyond the reference (hip backend)."""
         if type(enforce_eager) is not bool:
             raise TypeError("enforce_eager must be bool")
         self.model = model.eval()
@@ -59,10 +64,14 @@ class ModelRunner:
         self.kv_cache: PagedKVCache | None = None
         self.decode_workspace: torch.Tensor | None = None
         try:
+            kv_dtype = self.dtype if kv_cache_dtype is None else kv_cache_dtype
+            if kv_dtype not in (self.dtype, torch.float8_e4m3fn):
+                raise ValueError("KV cache dtype must be the model dtype or float8_e4m3fn")
             self.kv_cache = PagedKVCache(
                 num_layers=config.num_hidden_layers, num_blocks=num_blocks,
                 block_size=block_size, num_kv_heads=config.num_key_value_heads,
-                head_dim=config.head_dim, device=self.device, dtype=self.dtype,
+                head_dim=config.head_dim, device=self.device, dtype=kv_dtype,
+                k_scale=float(kv_scales[0]), v_scale=float(kv_scales[1]),
             )
             if self.backend == "hip":
                 self.decode_inputs = DecodeInputs(
