@@ -165,10 +165,11 @@ def attention_roofline(executor, workload, cfg, iters: int = 30,
         seconds = _event_time(call, iters)
     lengths = batch.context_lens_after
     pages = sum(math.ceil(l / workload.bs) for l in lengths)
+    kv = runner.kv_cache.key.element_size()  # 2 (bf16) or 1 (FP8 layout)
     # KV read once per KV head; q/k/v projections read, output and the new
     # K/V rows written; RoPE tables, slots and block tables.
-    algorithmic = (sum(lengths) * hkv * d * 2 * 2 + rows * (hq + 2 * hkv) * d * 2
-                   + rows * hq * d * 2 + rows * 2 * hkv * d * 2 + rows * d * 2 * 2
+    algorithmic = (sum(lengths) * hkv * d * 2 * kv + rows * (hq + 2 * hkv) * d * 2
+                   + rows * hq * d * 2 + rows * 2 * hkv * d * kv + rows * d * 2 * 2
                    + 8 * pages + 8 * (4 * rows + 1))
     achieved = algorithmic / seconds / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
@@ -476,6 +477,35 @@ def op_c1(args) -> dict:
         result[name] = {**_hbm(algorithmic, seconds), "max_abs_err_vs_oracle":
                         round(err.max().item(), 5),
                         "cpu_oracle_us": round(cpu * 1e6, 1)}
+        if rows < 16:
+            continue
+        # The optional FP8 E4M3 cache layout at the same shape (scales 1).
+        del gcache
+        k8, v8 = cache.key[0].to(torch.float8_e4m3fn), cache.value[0].to(torch.float8_e4m3fn)
+        layers8 = max(1, min(64, math.ceil(4e9 / (2 * k8.numel()))))
+        gcache8 = PagedKVCache(num_layers=layers8, num_blocks=pool, block_size=16,
+                               num_kv_heads=8, head_dim=128, device=device,
+                               dtype=torch.float8_e4m3fn)
+        for layer_idx in range(layers8):
+            gcache8.key[layer_idx].copy_(k8)
+            gcache8.value[layer_idx].copy_(v8)
+        calls[0] = 0
+
+        def call8():
+            paged_decode_attention(gq, gcache8, calls[0] % layers8, meta, gout, scale=scale,
+                                   workspace=ws)
+            calls[0] += 1
+
+        seconds8 = _event_time(call8, 200)
+        paged_decode_attention(gq, gcache8, 0, meta, gout, scale=scale, workspace=ws)
+        OA.decode_attention(q, k8.float(), v8.float(), torch.arange(rows), blocks, offsets,
+                            lengths, 16, scale, ref)
+        err8 = (gout.cpu().float() - ref.float()).abs()
+        algorithmic8 = (int(lengths.sum()) * 8 * 128 * 2 + 2 * rows * hq * 128 * 2
+                        + 8 * sum(pages) + 8 * (3 * rows + 1))
+        result[name + "_kv_fp8"] = {**_hbm(algorithmic8, seconds8),
+                                    "max_abs_err_vs_oracle": round(err8.max().item(), 5)}
+        del gcache8
     return result
 
 
@@ -799,6 +829,9 @@ def main() -> None:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kv-cache-dtype", choices=["auto", "fp8_e4m3"], default="auto",
+                    help="decode workload: KV cache in the model dtype (the metric's "
+                         "configuration) or the optional FP8 E4M3 layout")
     ap.add_argument("--workload", choices=["decode", *E2E, *OPS], default="decode",
                     help="decode (the metric) or an end-to-end SURVEY config")
     ap.add_argument("--eager", action="store_true",
@@ -849,13 +882,20 @@ def main() -> None:
     pages = math.ceil(max_len / bs)
     num_blocks = args.batch * pages
     # Every step carries exactly `batch` rows: capture that one graph.
+    fp8 = args.kv_cache_dtype == "fp8_e4m3"
     executor = Executor(model, block_size=bs, num_blocks=num_blocks,
                         max_model_len=max_model_len, max_num_seqs=args.batch,
-                        graph_sizes=(args.batch,))
+                        graph_sizes=(args.batch,),
+                        kv_cache_dtype=torch.float8_e4m3fn if fp8 else None)
     cache = executor.runner.kv_cache
     gen = torch.Generator(device=device).manual_seed(1)
-    cache.key.normal_(generator=gen)
-    cache.value.normal_(generator=gen)
+    if fp8:  # N(0, 1) values quantised layer by layer
+        for layer in range(cache.num_layers):
+            for t in (cache.key[layer], cache.value[layer]):
+                t.copy_(torch.randn(t.shape, generator=gen, device=device).to(t.dtype))
+    else:
+        cache.key.normal_(generator=gen)
+        cache.value.normal_(generator=gen)
     workload = DecodeWorkload(args.batch, args.context, bs, num_blocks, cfg.vocab_size)
 
     for _ in range(args.warmup):
@@ -869,7 +909,8 @@ def main() -> None:
     tok_s = args.batch * args.steps / elapsed
 
     roof = attention_roofline(executor, workload, cfg, headline=(
-        args.model == "qwen3-8b" and args.batch == 64 and args.context == 2048))
+        args.model == "qwen3-8b" and args.batch == 64 and args.context == 2048
+        and not fp8))
     cpu = None if args.no_cpu_baseline else cpu_baseline(cfg, args.batch, args.context)
     line = {
         "metric": "decode tok/s Qwen3-8B bs64 ctx2k; paged-attn HBM GB/s and % of peak",
@@ -882,7 +923,8 @@ def main() -> None:
         "config": {"workload": f"{args.model} decode bs{args.batch} ctx{args.context}",
                    "model": args.model, "global_batch": args.batch,
                    "seq_len": args.context, "parallelism": "single-gpu",
-                   "attention_backend": "hip", "graphs": True},
+                   "attention_backend": "hip", "graphs": True,
+                   "kv_cache_dtype": "fp8_e4m3" if fp8 else "bf16"},
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -13,6 +13,7 @@ from dataclasses import dataclass
 
 import torch
 
+from oracle import paged_kv as KV
 from oracle import pointwise as P
 
 
@@ -65,8 +66,12 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return (x.float() @ w.float().t()).to(x.dtype)
 
 
-def forward(cfg: TinyQwen3, w: dict[str, torch.Tensor], token_ids: list[int]) -> torch.Tensor:
-    """Full causal forward of one sequence; logits [L, vocab] (storage-dtype values)."""
+def forward(cfg: TinyQwen3, w: dict[str, torch.Tensor], token_ids: list[int],
+            kv_fp8: tuple[float, float] | None = None) -> torch.Tensor:
+    """Full causal forward of one sequence; logits [L, vocab] (storage-dtype values).
+    ``kv_fp8=(k_scale, v_scale)`` attends over K/V passed through the FP8 E4M3
+    cache layout (quantised, then read back), as an engine with that layout
+    does."""
     ids = torch.tensor(token_ids, dtype=torch.long)
     length = ids.numel()
     dtype = w["model.embed_tokens.weight"].dtype
@@ -91,8 +96,12 @@ def forward(cfg: TinyQwen3, w: dict[str, torch.Tensor], token_ids: list[int]) ->
                               w[f"{p}.self_attn.k_norm.weight"], cos, sin,
                               cfg.rms_norm_eps, cfg.rms_norm_eps)
         group = hq // hkv
-        kf = k.float().repeat_interleave(group, 1)
-        vf = v.float().repeat_interleave(group, 1)
+        kf, vf = k.float(), v.float()
+        if kv_fp8 is not None:
+            kf = KV.fp8_dequantize(KV.fp8_quantize(k, kv_fp8[0]), kv_fp8[0])
+            vf = KV.fp8_dequantize(KV.fp8_quantize(v, kv_fp8[1]), kv_fp8[1])
+        kf = kf.repeat_interleave(group, 1)
+        vf = vf.repeat_interleave(group, 1)
         s = torch.einsum("qhd,khd->hqk", q.float(), kf) * d ** -0.5
         s = s.masked_fill(~causal[None], float("-inf"))
         attn = torch.einsum("hqk,khd->qhd", torch.softmax(s, -1), vf).to(dtype)

@@ -176,12 +176,19 @@ def test_engine_config_validation(tmp_path):
     cfg = EngineConfig(model=tmp_path)
     assert cfg.max_num_seqs == 64 and cfg.kv_block_size == 16 and cfg.prefill_chunk_size == 512
     assert EngineConfig(model=tmp_path, attention_backend="cuda").attention_backend == "cuda"
+    assert cfg.kv_cache_dtype == "auto" and (cfg.kv_k_scale, cfg.kv_v_scale) == (1.0, 1.0)
+    fp8 = EngineConfig(model=tmp_path, kv_cache_dtype="fp8_e4m3", kv_k_scale=0.5)
+    assert fp8.kv_cache_dtype == "fp8_e4m3" and fp8.kv_k_scale == 0.5
     bad = [dict(model=tmp_path / "missing"), dict(model=tmp_path, dtype="float32"),
            dict(model=tmp_path, attention_backend="triton"),
            dict(model=tmp_path, gpu_memory_utilization=1.0),
            dict(model=tmp_path, prefill_reserve_tokens=0),
            dict(model=tmp_path, prefill_chunk_size=8192),
-           dict(model=tmp_path, max_num_seqs=0)]
+           dict(model=tmp_path, max_num_seqs=0),
+           dict(model=tmp_path, kv_cache_dtype="int8"),
+           dict(model=tmp_path, kv_k_scale=2.0),  # scales need the FP8 layout
+           dict(model=tmp_path, kv_cache_dtype="fp8_e4m3", kv_v_scale=0.0),
+           dict(model=tmp_path, kv_cache_dtype="fp8_e4m3", kv_k_scale=float("inf"))]
     for kw in bad:
         with pytest.raises((ValueError, TypeError)):
             EngineConfig(**kw)

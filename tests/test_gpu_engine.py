@@ -9,13 +9,13 @@ from test_gpu_runner import CFG, _our_model
 pytestmark = pytest.mark.gpu
 
 
-def teacher_forced_agreement(weights, prompt, ours, tie=0.05):
+def teacher_forced_agreement(weights, prompt, ours, tie=0.05, kv_fp8=None):
     """Steps at which our sampled token is the oracle's greedy choice given
     the same context (one oracle forward over prompt + ours). A step whose
     oracle top-2 logits differ by less than ``tie`` (about one bf16 ulp at
     these magnitudes) accepts either token: GEMM accumulation order may
     legitimately flip such a near-tie, and the sequence then diverges."""
-    logits = OM.forward(CFG, weights, list(prompt) + list(ours))
+    logits = OM.forward(CFG, weights, list(prompt) + list(ours), kv_fp8=kv_fp8)
     agree = 0
     for i, token in enumerate(ours):
         row = logits[len(prompt) - 1 + i]
@@ -53,6 +53,31 @@ def test_engine_greedy_with_shared_prefixes_matches_oracle(device):
         total += new
     assert agree / total >= 0.99, (agree, total)
     assert engine.scheduler.block_manager.prefix_cache.hits >= 1
+    engine.close()
+
+
+def test_engine_fp8_kv_cache_greedy_matches_fp8_oracle(device):
+    """The optional FP8 E4M3 KV layout end to end (chunked prefill, prefix
+    cache, graph-replayed decode): greedy tokens agree with the oracle model
+    attending over the same FP8-quantised K/V."""
+    from tinyvllm import GenerateRequest, SamplingParams
+
+    weights = OM.random_weights(CFG, seed=8, dtype=torch.bfloat16, std=0.2)
+    scales = (0.5, 0.25)
+    engine = _engine(_our_model(weights, device), kv_cache_dtype=torch.float8_e4m3fn,
+                     kv_scales=scales)
+    assert engine.executor.runner.kv_cache.key.dtype == torch.float8_e4m3fn
+    g = torch.Generator().manual_seed(9)
+    shared = torch.randint(0, CFG.vocab_size, (70,), generator=g).tolist()
+    prompts = [shared + torch.randint(0, CFG.vocab_size, (n,), generator=g).tolist()
+               for n in (5, 33)] + [torch.randint(0, CFG.vocab_size, (120,),
+                                                  generator=g).tolist()]
+    new = 10
+    params = SamplingParams(max_new_tokens=new, ignore_eos=True)
+    outs = engine.generate([GenerateRequest(p, params) for p in prompts])
+    agree = sum(teacher_forced_agreement(weights, p, o.output_token_ids, kv_fp8=scales)
+                for p, o in zip(prompts, outs))
+    assert agree / (new * len(prompts)) >= 0.99, agree
     engine.close()
 
 
