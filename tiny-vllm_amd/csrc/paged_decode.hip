@@ -22,9 +22,16 @@
 //  * Q.K^T on the matrix cores: per 16-token tile, 4 MFMA 16x16x32 steps with
 //    A = K rows (natural cache layout, 64 contiguous bytes per lane quad),
 //    B = the G query rows zero-padded to 16 columns;
-//  * P.V on the VALU: lane l holds 8 head dims of the token that the MFMA
-//    result row (l / 16) describes, so each lane's weights are a DPP
-//    row-broadcast of the score lane of its own 16-lane row - no LDS at all;
+//  * P.V on the matrix cores too, with no data movement: per 16-token tile,
+//    D[head][dim] += P[head][token] V[token][dim] on 16x16x16 MFMAs whose k
+//    index is the token. The scores a lane holds (its head, tokens
+//    4*quad + i) are exactly its A operand, and the V row pieces it loaded
+//    (tokens 4*quad + i, dims 8*col .. +7) hold its B operand of MFMA e
+//    (column col = dim 8*col + e): element e of its four rows, gathered
+//    with two v_perm. P enters as a pair of storage-type terms (rounded P
+//    and the rounded remainder, two MFMAs), so the product keeps about 16
+//    bits of P - as accurate as fp32 P on the VALU; the denominator sums
+//    the unrounded P;
 //  * 64 tokens per iteration: 16 K and 16 V 16-byte loads per lane in flight
 //    (32 KiB per wave) before any arithmetic waits on them.
 #include "common.h"
@@ -45,6 +52,22 @@ __device__ __forceinline__ void static_for(F&& f) {
     if constexpr (I < N) {
         f(std::integral_constant<int, I>{});
         static_for<I + 1, N>(f);
+    }
+}
+
+// D[16x16] += A[16x16] B[16x16]: lane l supplies A row l%16 and B column
+// l%16 with k = 4*(l/16)..+3 (one 8-byte pair of words each); D as for
+// the 16x16x32 form.
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x16(uint2 a, uint2 b, f32x4 c) {
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+    if constexpr (std::is_same_v<T, __bf16>) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+            __builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(
+            __builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
     }
 }
 
@@ -295,11 +318,10 @@ paged_decode_d128(DecodeArgs<T> a) {
     const int64_t t_begin = p_begin * bs;
     const int64_t t_end = min(length, p_end * bs);
 
-    float acc[GP][8];
+    // acc[e][v]: output head 4*quad + v, dim 8*col + e (the P.V MFMA layout).
+    f32x4 acc[8];
 #pragma unroll
-    for (int g = 0; g < GP; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY;  // running max (base-2 units), per score lane
     float l_run = 0.f;        // this lane's share of the denominator
 
@@ -486,26 +508,43 @@ paged_decode_d128(DecodeArgs<T> a) {
                     }
                 l_run = l_run * alpha + psum;
 
-                static_for<0, GP>([&](auto gc) {
-                    constexpr int g = decltype(gc)::value;
-                    const float ag = read_lane<g>(alpha);
+                // Rescale: output row v of this lane is head 4*quad + v, whose
+                // alpha lives in score lane (col = that head).
+                if constexpr (GP > 1) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[g][e] *= ag;
-                });
+                    for (int v = 0; v < 4; ++v) {
+                        if (4 * v >= 4 * GP) break;
+                        const float av = __shfl(alpha, 4 * quad + v, 64);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[e][v] *= av;
+                    }
+                } else {
+                    const float av = read_lane<0>(alpha);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[e] *= av;
+                }
 
 #pragma unroll
                 for (int j = 0; j < NT; ++j) {
+                    uint2 pa, pl;  // A: this lane's head, tokens 4*quad + 0..3
+                    pa.x = pack2<T>(pw[j][0], pw[j][1]);
+                    pa.y = pack2<T>(pw[j][2], pw[j][3]);
+                    pl.x = pack2<T>(pw[j][0] - half_lo<T>(pa.x), pw[j][1] - half_hi<T>(pa.x));
+                    pl.y = pack2<T>(pw[j][2] - half_lo<T>(pa.y), pw[j][3] - half_hi<T>(pa.y));
+                    U16x8 vr[4];  // the tile's V pieces as T elements
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        float vv[8];
-                        if constexpr (F8) fp8x8_unpack(vreg[j][i], vv);
-                        else unpack8<T>(vreg[j][i], vv);
-                        static_for<0, GP>([&](auto gc) {
-                            constexpr int g = decltype(gc)::value;
-                            const float p = row_bcast<g>(pw[j][i]);
+                        if constexpr (F8) vr[i] = fp8x8_widen<T>(vreg[j][i]);
+                        else vr[i] = vreg[j][i];
+                    }
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vv[e], acc[g][e]);
-                        });
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+                        uint2 vb;  // B: element e of tokens 4*quad + 0..3
+                        vb.x = __builtin_amdgcn_perm(vr[1].w[e >> 1], vr[0].w[e >> 1], sel);
+                        vb.y = __builtin_amdgcn_perm(vr[3].w[e >> 1], vr[2].w[e >> 1], sel);
+                        acc[e] = mfma16x16x16<T>(pa, vb, acc[e]);
+                        acc[e] = mfma16x16x16<T>(pl, vb, acc[e]);
                     }
                 }
                 load_v(next);
@@ -521,16 +560,16 @@ paged_decode_d128(DecodeArgs<T> a) {
 
     }  // t_begin < t_end
 
-    // Combine the four 16-lane rows (disjoint token subsets).
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            acc[g][e] += __shfl_xor(acc[g][e], 16, 64);
-            acc[g][e] += __shfl_xor(acc[g][e], 32, 64);
-        }
+    // The denominator: sum the four 16-lane rows (disjoint token subsets).
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
+    // (m, l) of this lane's output heads 4*quad + v, from their score lanes.
+    float mh[4], lh[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        mh[v] = __shfl(m_run, min(4 * quad + v, 15), 64);
+        lh[v] = __shfl(l_run, min(4 * quad + v, 15), 64);
+    }
 
     // Split merge through LDS: waves with split > 0 publish (o, m, l); the
     // split-0 wave of each head rescales and sums them:
@@ -540,16 +579,16 @@ paged_decode_d128(DecodeArgs<T> a) {
     if (a.splits > 1) {
         if (split > 0) {
             const int slot = local_head * (a.splits - 1) + split - 1;
-            if (quad == 0) {
 #pragma unroll
-                for (int g = 0; g < GP; ++g) {
-                    float4* po = reinterpret_cast<float4*>(&red_o[slot][g][col * 8]);
-                    po[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-                    po[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-                }
-                if (col < GP) {
-                    red_ml[slot][col][0] = m_run;
-                    red_ml[slot][col][1] = l_run;
+            for (int v = 0; v < 4; ++v) {
+                const int h = 4 * quad + v;
+                if (h >= GP) break;
+                float4* po = reinterpret_cast<float4*>(&red_o[slot][h][col * 8]);
+                po[0] = make_float4(acc[0][v], acc[1][v], acc[2][v], acc[3][v]);
+                po[1] = make_float4(acc[4][v], acc[5][v], acc[6][v], acc[7][v]);
+                if (col == 0) {
+                    red_ml[slot][h][0] = mh[v];
+                    red_ml[slot][h][1] = lh[v];
                 }
             }
         }
@@ -557,30 +596,30 @@ paged_decode_d128(DecodeArgs<T> a) {
         if (split > 0) return;
     }
 
-    static_for<0, GP>([&](auto gc) {
-        constexpr int g = decltype(gc)::value;
-        float m_self = read_lane<g>(m_run);
-        float mx = m_self;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int h = 4 * quad + v;
+        if (h >= GP || h >= a.group) break;
+        float mx = mh[v];
         for (int s = 1; s < a.splits; ++s)
-            mx = fmaxf(mx, red_ml[local_head * (a.splits - 1) + s - 1][g][0]);
-        if (g >= a.group || quad != 0) return;
+            mx = fmaxf(mx, red_ml[local_head * (a.splits - 1) + s - 1][h][0]);
         float num[8];
         float den = 0.f;
         if (mx == -INFINITY) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) num[e] = 0.f;
         } else {
-            const float w0 = fast_exp2(m_self - mx);
-            den = w0 * read_lane<g>(l_run);
+            const float w0 = fast_exp2(mh[v] - mx);
+            den = w0 * lh[v];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) num[e] = w0 * acc[g][e];
+            for (int e = 0; e < 8; ++e) num[e] = w0 * acc[e][v];
             for (int s = 1; s < a.splits; ++s) {
                 const int slot = local_head * (a.splits - 1) + s - 1;
-                const float ms = red_ml[slot][g][0];
+                const float ms = red_ml[slot][h][0];
                 if (ms == -INFINITY) continue;
                 const float ws = fast_exp2(ms - mx);
-                den += ws * red_ml[slot][g][1];
-                const float4* po = reinterpret_cast<const float4*>(&red_o[slot][g][col * 8]);
+                den += ws * red_ml[slot][h][1];
+                const float4* po = reinterpret_cast<const float4*>(&red_o[slot][h][col * 8]);
                 const float4 p0 = po[0], p1 = po[1];
                 num[0] += ws * p0.x; num[1] += ws * p0.y; num[2] += ws * p0.z; num[3] += ws * p0.w;
                 num[4] += ws * p1.x; num[5] += ws * p1.y; num[6] += ws * p1.z; num[7] += ws * p1.w;
@@ -588,7 +627,7 @@ paged_decode_d128(DecodeArgs<T> a) {
         }
         if (a.grid_splits > 1) {
             // Unnormalised partial of this workgroup's page ranges.
-            const int64_t base = (int64_t(r) * a.heads + h0 + g) * a.grid_splits + gsplit;
+            const int64_t base = (int64_t(r) * a.heads + h0 + h) * a.grid_splits + gsplit;
             float4* po = reinterpret_cast<float4*>(a.part_o + base * D + col * 8);
             po[0] = make_float4(num[0], num[1], num[2], num[3]);
             po[1] = make_float4(num[4], num[5], num[6], num[7]);
@@ -596,15 +635,15 @@ paged_decode_d128(DecodeArgs<T> a) {
                 a.part_ml[base * 2] = mx;
                 a.part_ml[base * 2 + 1] = den;
             }
-            return;
+            continue;
         }
         if (mx == -INFINITY) den = 1.f;  // zero-length row: zeros
         U16x8 packed;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             packed.w[e] = pack2<T>(num[2 * e] * a.v_scale / den, num[2 * e + 1] * a.v_scale / den);
-        *reinterpret_cast<U16x8*>(a.out + row * a.ots + (h0 + g) * a.ohs + col * 8) = packed;
-    });
+        *reinterpret_cast<U16x8*>(a.out + row * a.ots + (h0 + h) * a.ohs + col * 8) = packed;
+    }
 }
 
 // Merge split partials: out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
