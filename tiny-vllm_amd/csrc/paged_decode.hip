@@ -743,14 +743,15 @@ paged_decode_generic(const T* __restrict__ q, int64_t qts, int64_t qhs,
 
 // Launch shape of the MFMA decode kernel. `target` is the number of
 // (row, KV head, split) waves the split heuristic aims for (0 = the default
-// rule in choose_splits); `tiles` 16-token MFMA tiles per iteration (4 is
-// used when a workgroup has at most 4 waves: one wave per SIMD with a
-// 512-register budget keeps 32 KiB of K/V loads in flight per wave; larger
-// workgroups use 2 tiles at 2 waves per SIMD); `waves` the preferred waves
-// per workgroup. Measured on MI355X at Qwen3-8B bs64 ctx2048.
+// rule in choose_splits); `tiles` 16-token MFMA tiles per iteration (4: one
+// wave per SIMD with a 512-register budget, 32 KiB of K/V loads in flight per
+// wave, workgroups of at most 4 waves; 2: two waves per SIMD, 16 KiB each);
+// `waves` the preferred waves per workgroup. Measured on MI355X at Qwen3-8B
+// bs64 ctx2048 with cold KV: 2 tiles 89 us, 4 tiles 94 us (since P.V moved
+// to the matrix cores and freed vector registers).
 struct Tuning {
     int64_t target = 0;
-    int tiles = 4;
+    int tiles = 2;
     int waves = 4;
 };
 
