@@ -753,22 +753,26 @@ struct Tuning {
     int64_t target = 0;
     int tiles = 2;
     int waves = 4;
+    int split_waves = kMaxWaves;  // most page ranges of one head per workgroup
 };
 
 // Defaults can be overridden for measurement with
-// TVLLM_DECODE_TUNING="target,tiles,waves" (read once per process).
+// TVLLM_DECODE_TUNING="target,tiles,waves[,split_waves]" (read once per
+// process).
 const Tuning& tuning() {
     static const Tuning t = [] {
         Tuning v;
         if (const char* env = std::getenv("TVLLM_DECODE_TUNING")) {
             long long target = 0;
-            int tiles = 0, waves = 0;
-            if (std::sscanf(env, "%lld,%d,%d", &target, &tiles, &waves) == 3 &&
-                target >= 0 && (tiles == 2 || tiles == 4) && waves >= 1 &&
-                waves <= kMaxWaves) {
+            int tiles = 0, waves = 0, split_waves = kMaxWaves;
+            const int n = std::sscanf(env, "%lld,%d,%d,%d", &target, &tiles, &waves,
+                                      &split_waves);
+            if (n >= 3 && target >= 0 && (tiles == 2 || tiles == 4) && waves >= 1 &&
+                waves <= kMaxWaves && split_waves >= 1 && split_waves <= kMaxWaves) {
                 v.target = target;
                 v.tiles = tiles;
                 v.waves = waves;
+                v.split_waves = split_waves;
             }
         }
         return v;
@@ -806,7 +810,7 @@ SplitPlan plan_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
                       int64_t block_size) {
     const int64_t total = choose_splits(rows, kv_heads, max_context, block_size);
     SplitPlan p;
-    p.waves = std::min<int64_t>(total, kMaxWaves);
+    p.waves = std::min<int64_t>(total, tuning().split_waves);
     p.grid = (total + p.waves - 1) / p.waves;
     p.heads = heads_per_group(kv_heads, p.waves);
     return p;
