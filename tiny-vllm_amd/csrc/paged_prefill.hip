@@ -373,6 +373,20 @@ paged_prefill_d128(PrefillArgs<T> a) {
         if (matrix_first) softmax(0);
     }
 
+    // With eight waves, waves 0-3 own the K staging jobs and waves 4-7 the V
+    // jobs; each group stages in the half where it issues MFMAs, so staging
+    // runs alongside the other group's exponentials instead of in a phase of
+    // its own. K(i+2) goes to the buffer of K(i), V(i+1) to that of V(i-1):
+    // both were last read before the previous barrier, and neither buffer is
+    // read in the half that writes it.
+    constexpr bool split_staging = W == 8;
+    auto stage_next = [&](int i) {
+        store_tile(i, stage);
+        load_tile(i + 1, ids, stage);
+        load_ids(i + 2, ids);
+    };
+    // K(2) overwrites K(0), which every wave read above in scores(0).
+    if constexpr (split_staging) __syncthreads();
     for (int i = 0; i < ntiles; ++i) {
         // First half: tile i's P.V and tile i+1's S (matrix first), or
         // tile i's softmax (vector first).
@@ -381,6 +395,7 @@ paged_prefill_d128(PrefillArgs<T> a) {
                 pv(i);
                 if (i + 1 < wt) scores(i + 1);
             }
+            if constexpr (split_staging) stage_next(i);
         } else if (i < wt) {
             softmax(i);
         }
@@ -388,15 +403,14 @@ paged_prefill_d128(PrefillArgs<T> a) {
         // Second half: the roles swap.
         if (matrix_first) {
             if (i + 1 < wt) softmax(i + 1);
-        } else if (i < wt) {
-            pv(i);
-            if (i + 1 < wt) scores(i + 1);
+        } else {
+            if (i < wt) {
+                pv(i);
+                if (i + 1 < wt) scores(i + 1);
+            }
+            if constexpr (split_staging) stage_next(i);
         }
-        // Staging: K(i+2) -> the buffer of K(i) and V(i+1) -> the buffer of
-        // V(i-1); both were last read before the previous barrier.
-        store_tile(i, stage);
-        load_tile(i + 1, ids, stage);
-        load_ids(i + 2, ids);
+        if constexpr (!split_staging) stage_next(i);
         __syncthreads();
     }
     if (!wave_active) return;
