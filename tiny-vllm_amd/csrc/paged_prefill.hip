@@ -387,28 +387,32 @@ paged_prefill_d128(PrefillArgs<T> a) {
     };
     // K(2) overwrites K(0), which every wave read above in scores(0).
     if constexpr (split_staging) __syncthreads();
+    // A wave's MFMA half with its staging in one basic block (the common
+    // case i + 1 < wt), so the scheduler can slot the staging instructions
+    // between the matrix instructions.
+    auto matrix_half = [&](int i) {
+        if (i + 1 < wt) {
+            pv(i);
+            scores(i + 1);
+            if constexpr (split_staging) stage_next(i);
+        } else if (i < wt) {
+            pv(i);
+            if constexpr (split_staging) stage_next(i);
+        } else if constexpr (split_staging) {
+            stage_next(i);
+        }
+    };
     for (int i = 0; i < ntiles; ++i) {
         // First half: tile i's P.V and tile i+1's S (matrix first), or
         // tile i's softmax (vector first).
-        if (matrix_first) {
-            if (i < wt) {
-                pv(i);
-                if (i + 1 < wt) scores(i + 1);
-            }
-            if constexpr (split_staging) stage_next(i);
-        } else if (i < wt) {
-            softmax(i);
-        }
+        if (matrix_first) matrix_half(i);
+        else if (i < wt) softmax(i);
         __syncthreads();
         // Second half: the roles swap.
         if (matrix_first) {
             if (i + 1 < wt) softmax(i + 1);
         } else {
-            if (i < wt) {
-                pv(i);
-                if (i + 1 < wt) scores(i + 1);
-            }
-            if constexpr (split_staging) stage_next(i);
+            matrix_half(i);
         }
         if constexpr (!split_staging) stage_next(i);
         __syncthreads();
