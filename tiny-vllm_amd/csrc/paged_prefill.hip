@@ -290,11 +290,14 @@ paged_prefill_d128(PrefillArgs<T> a) {
                 for (int v = 0; v < 16; ++v)
                     if (32 * tb + 8 * (v >> 2) + (v & 3) > lim) sc[tb][v] = -INFINITY;
         }
-        float cmax = -INFINITY;
+        // Maxima and sums in four independent chains (a single chain of 32
+        // dependent instructions stalls the wave).
+        float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) cmax = fmaxf(cmax, sc[tb][v]);
+            for (int v = 0; v < 16; ++v) mx[v & 3] = fmaxf(mx[v & 3], sc[tb][v]);
+        const float cmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
         const float cm = pair_max(cmax) * a.scale_log2;  // scale > 0
         const bool grow = cm > m_run + kSlack;  // also: first finite max
         float alpha = 1.f;
@@ -308,14 +311,14 @@ paged_prefill_d128(PrefillArgs<T> a) {
             for (int n = 0; n < 4; ++n) o[n] *= alpha;
         }
         const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float psum = 0.f;
+        float ps[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             float p[16];
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tb][v], a.scale_log2, -m_use));
-                psum += p[v];
+                ps[v & 3] += p[v];
             }
 #pragma unroll
             for (int sh = 0; sh < 2; ++sh) {
@@ -326,7 +329,7 @@ paged_prefill_d128(PrefillArgs<T> a) {
                 w.w[3] = pack2<T>(p[8 * sh + 6], p[8 * sh + 7]);
             }
         }
-        l_run += psum;
+        l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
     };
     auto pv = [&](int j) {  // O^T += V^T P^T over four 16-token steps
         const uint16_t* vtt = vt[j & 1];
