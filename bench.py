@@ -74,9 +74,11 @@ class DecodeWorkload:
 
         self.greedy = SamplingParams(max_new_tokens=1 << 20)
 
-    def batch_for_step(self):
+    def batch_for_step(self, from_previous: bool = False):
         """The next decode step's PreparedBatch (block tables and slots as
-        int64 arrays, like BatchBuilder emits)."""
+        int64 arrays, like BatchBuilder emits). ``from_previous``: the input
+        ids are the previous launched step's sampled rows, taken on the
+        device (pipelined steps)."""
         import numpy as np
 
         from tinyvllm.batch import PreparedBatch, StepMode
@@ -91,7 +93,8 @@ class DecodeWorkload:
         slots = self.np_tables_2d[np.arange(n), pos // bs] * bs + pos % bs
         self.plan_id += 1
         return PreparedBatch(
-            plan_id=self.plan_id, mode=StepMode.DECODE_ONLY, input_ids=tuple(self.tokens),
+            plan_id=self.plan_id, mode=StepMode.DECODE_ONLY,
+            input_ids=(0,) * n if from_previous else tuple(self.tokens),
             positions=tuple(self.lengths), q_offsets=tuple(range(n + 1)),
             context_lens_before=tuple(self.lengths), query_lens=(1,) * n,
             context_lens_after=tuple(l + 1 for l in self.lengths),
@@ -100,11 +103,25 @@ class DecodeWorkload:
             kv_num_blocks=self.max_pages * n, kv_block_table_ids=table_ids,
             kv_block_table_offsets=tuple(offsets.tolist()), kv_slot_mapping=slots,
             request_ids=tuple(range(n)),
+            input_token_sources=tuple(range(n)) if from_previous else None,
         )
 
     def advance(self, tokens):
         self.tokens = list(tokens)
         self.lengths = [length + 1 for length in self.lengths]
+
+    def run(self, executor, steps: int, pending=None):
+        """``steps`` pipelined decode steps: step i+1 is built and launched
+        (its input ids taken from step i's sampled rows on the device)
+        before the host waits for step i's tokens. Returns the last step's
+        PendingStep; pass it back in to continue the chain."""
+        for _ in range(steps):
+            launched = executor.launch(self.batch_for_step(from_previous=pending is not None))
+            self.lengths = [length + 1 for length in self.lengths]
+            if pending is not None:
+                self.tokens = list(pending.result().sampled_token_ids)
+            pending = launched
+        return pending
 
 
 COUNTERS_FILE = ROOT / "profiles" / "paged_decode_qwen3-8b_bs64_ctx2k_counters.txt"
@@ -898,12 +915,13 @@ def main() -> None:
         cache.value.normal_(generator=gen)
     workload = DecodeWorkload(args.batch, args.context, bs, num_blocks, cfg.vocab_size)
 
-    for _ in range(args.warmup):
-        workload.advance(executor.execute(workload.batch_for_step()).sampled_token_ids)
+    # Pipelined like the engine: the host builds and launches step i+1
+    # while the GPU runs step i.
+    pending = workload.run(executor, args.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        workload.advance(executor.execute(workload.batch_for_step()).sampled_token_ids)
+    pending = workload.run(executor, args.steps, pending)
+    workload.tokens = list(pending.result().sampled_token_ids)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     tok_s = args.batch * args.steps / elapsed

@@ -239,6 +239,16 @@ int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
                  int64_t* out, void* workspace, int64_t workspace_bytes,
                  int dtype, tvllm_stream_t stream);
 
+/* Pipelined decode inputs: tokens[i] = prev[src[i]] for 0 <= src[i] <
+ * prev_count, other entries unchanged (src[i] = -1 keeps the host token).
+ * prev holds the previous step's sampled token ids on the device, so the
+ * host can upload step N+1's inputs before step N's tokens reach it.
+ * Replaces: the host-side input-id packing of the next decode step
+ * (reference tinyvllm/runtime/inputs.py:88-111), which needs the previous
+ * step's tokens on the host first (tinyvllm/executor.py:135). */
+int tvllm_resolve_tokens(int64_t* tokens, const int64_t* src, const int64_t* prev,
+                         int64_t n, int64_t prev_count, tvllm_stream_t stream);
+
 /* Causal paged attention for multi-token query rows (chunked prefill).
  * Item i owns query tokens q[q_offsets[i] : q_offsets[i+1]], the last
  * `query_len` of its `context_lens[i]` tokens (lower-right causal mask:

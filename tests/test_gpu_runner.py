@@ -89,3 +89,78 @@ def test_logits_match_oracle_at_every_position(device):
     expect = OM.forward(CFG, weights, prompt)[-1]
     diff = (logits[0].float().cpu() - expect).abs()
     assert diff.max() < 0.15 and diff.mean() / expect.abs().mean() < 2e-2, diff.max()
+
+
+def _decode_run(model, prompts, *, enforce_eager, pipelined):
+    """Prefill seqs 0-2, then 10 decode steps over them; seq 3 joins with a
+    whole-prompt prefill in a mixed step. Pipelined: step k+1 is launched
+    before step k's tokens reach the host, its decode inputs naming step k's
+    sampled rows (input_token_sources)."""
+    import dataclasses
+
+    from tinyvllm.executor import Executor
+
+    executor = Executor(model, block_size=16, num_blocks=64, max_model_len=512,
+                        max_num_seqs=4, enforce_eager=enforce_eager)
+    mb = ManualBatches(prompts, block_size=16, num_blocks=64)
+    for items in ([(0, 37, True), (1, 5, True)], [(2, 80, True)]):
+        mb.commit(items, executor.execute(mb.step(items)).sampled_token_ids)
+    pending = None  # (PendingStep, {seq: (sample row, placeholder index)})
+    for step in range(10):
+        items = [(s, 1, True) for s in range(3 if step < 4 else 4)]
+        if step == 4:
+            items[3] = (3, len(prompts[3]), True)
+        batch = mb.step(items)
+        if pipelined and pending is not None:
+            rows = pending[1]
+            src = []
+            for seq, n, _ in items:
+                src += [rows[seq][0] if seq in rows else -1] + [-1] * (n - 1)
+            batch = dataclasses.replace(batch, input_token_sources=tuple(src))
+        launched = executor.launch(batch)
+        if not pipelined:
+            mb.commit(items, launched.result().sampled_token_ids)
+            continue
+        # Placeholders now; the real ids once the step's result arrives.
+        mb.commit(items, [0] * len(items))
+        rows = {seq: (r, len(mb.tokens[seq]) - 1) for r, (seq, _, _) in enumerate(items)}
+        if pending is not None:
+            for seq, tok in zip(pending[0].sample_request_ids,
+                                pending[0].result().sampled_token_ids):
+                mb.tokens[seq][pending[1][seq][1]] = tok
+        pending = (launched, rows)
+    if pending is not None:
+        for seq, tok in zip(pending[0].sample_request_ids, pending[0].result().sampled_token_ids):
+            mb.tokens[seq][pending[1][seq][1]] = tok
+    return mb.tokens
+
+
+@pytest.mark.parametrize("enforce_eager", [False, True])
+def test_pipelined_launches_match_sequential_steps(device, enforce_eager):
+    """Device-side input ids (the previous step's sampled rows) give exactly
+    the tokens of steps whose ids went through the host."""
+    weights = OM.random_weights(CFG, seed=5, dtype=torch.bfloat16, std=0.2)
+    model = _our_model(weights, device)
+    g = torch.Generator().manual_seed(6)
+    prompts = [torch.randint(0, CFG.vocab_size, (n,), generator=g).tolist()
+               for n in (37, 5, 80, 23)]
+    seq = _decode_run(model, prompts, enforce_eager=enforce_eager, pipelined=False)
+    pipe = _decode_run(model, prompts, enforce_eager=enforce_eager, pipelined=True)
+    assert pipe == seq
+    assert all(len(t) > len(p) for t, p in zip(seq, prompts))
+
+
+def test_token_sources_are_validated(device):
+    import dataclasses
+
+    from tinyvllm.executor import Executor
+
+    weights = OM.random_weights(CFG, seed=5, dtype=torch.bfloat16, std=0.2)
+    executor = Executor(_our_model(weights, device), block_size=16, num_blocks=16,
+                        max_model_len=256, max_num_seqs=2, enforce_eager=True)
+    mb = ManualBatches([[1, 2, 3]], block_size=16, num_blocks=16)
+    batch = mb.step([(0, 3, True)])
+    with pytest.raises(ValueError, match="previous step"):  # nothing launched yet
+        executor.execute(dataclasses.replace(batch, input_token_sources=(-1, -1, 0)))
+    with pytest.raises(ValueError, match="one entry per token"):
+        executor.execute(dataclasses.replace(batch, input_token_sources=(-1,)))

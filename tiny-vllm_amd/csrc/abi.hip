@@ -20,4 +20,4 @@ void clear_error() { g_error[0] = '\0'; }
 
 extern "C" const char* tvllm_last_error(void) { return tvllm::g_error; }
 
-extern "C" int tvllm_abi_version(void) { return 2; }
+extern "C" int tvllm_abi_version(void) { return 3; }

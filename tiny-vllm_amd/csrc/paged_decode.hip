@@ -109,7 +109,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 // whole rows (16 lanes x 16 bytes): non-temporal loads measure ~13% more read
 // bandwidth on MI355X for such streams (7.1 vs 6.3 TB/s). K loads touch each
 // 128-byte line from two instructions (the MFMA operand layout), so they stay
-// ordinary loads: a non-temporal first touch would refetch the line.
+// ordinary loads: made non-temporal, the fused 8B bs64 ctx2048 launch measured
+// 93.9 us against 89.4 us.
 __device__ __forceinline__ U16x8 load_stream(const U16x8* p) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

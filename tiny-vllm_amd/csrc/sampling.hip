@@ -412,3 +412,34 @@ extern "C" int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
         return launch_status("sample");
     });
 }
+
+// ------------------------------------------------ pipelined input tokens ----
+
+namespace tvllm {
+namespace {
+
+// tokens[i] = prev[src[i]] where 0 <= src[i] < prev_count, else unchanged.
+__global__ void __launch_bounds__(256)
+resolve_tokens_kernel(int64_t* __restrict__ tokens, const int64_t* __restrict__ src,
+                      const int64_t* __restrict__ prev, int64_t n, int64_t prev_count) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int64_t s = src[i];
+    if (s >= 0 && s < prev_count) tokens[i] = prev[s];
+}
+
+}  // namespace
+}  // namespace tvllm
+
+extern "C" int tvllm_resolve_tokens(int64_t* tokens, const int64_t* src,
+                                    const int64_t* prev, int64_t n, int64_t prev_count,
+                                    tvllm_stream_t stream) {
+    using namespace tvllm;
+    TVLLM_CHECK(n >= 0 && prev_count >= 0, "resolve_tokens: negative size");
+    TVLLM_CHECK(n <= (int64_t(INT32_MAX) - 255), "resolve_tokens: too many tokens");
+    if (n == 0) return TVLLM_OK;
+    TVLLM_CHECK(tokens && src && (prev || prev_count == 0), "resolve_tokens: null pointer");
+    resolve_tokens_kernel<<<int((n + 255) / 256), 256, 0, as_hip(stream)>>>(
+        tokens, src, prev, n, prev_count);
+    return launch_status("resolve_tokens");
+}

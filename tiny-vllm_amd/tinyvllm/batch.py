@@ -102,6 +102,10 @@ class PreparedBatch:
     kv_block_table_offsets: tuple[int, ...]
     kv_slot_mapping: tuple[int, ...] | np.ndarray
     request_ids: tuple[int, ...]
+    # Pipelined steps (beyond the reference): per input token, -1 = the id in
+    # input_ids, j >= 0 = row j of the previous launched step's sampled tokens,
+    # still on the device when this batch is built. None = all from input_ids.
+    input_token_sources: tuple[int, ...] | np.ndarray | None = None
 
     @property
     def num_items(self) -> int:

@@ -46,6 +46,33 @@ class ExecutorCapabilities:
             raise ValueError("token ID is out of vocabulary range")
 
 
+class PendingStep:
+    """A launched step whose sampled token ids are on their way to the host."""
+
+    __slots__ = ("plan_id", "sample_request_ids", "_host", "_rows", "_event", "_result")
+
+    def __init__(self, plan_id: int, sample_request_ids: tuple[int, ...],
+                 host: torch.Tensor | None, rows: int, event) -> None:
+        self.plan_id = plan_id
+        self.sample_request_ids = sample_request_ids
+        self._host, self._rows, self._event = host, rows, event
+        self._result: StepResult | None = None
+
+    def ready(self) -> bool:
+        return self._result is not None or self._event is None or self._event.query()
+
+    def result(self) -> StepResult:
+        """Wait for the step's sampled ids (the step's one device->host sync)."""
+        if self._result is None:
+            tokens = ()
+            if self._event is not None:
+                self._event.synchronize()
+                tokens = tuple(self._host[:self._rows].tolist())
+            self._result = StepResult(self.plan_id, self.sample_request_ids, tokens)
+            self._host = self._event = None
+        return self._result
+
+
 class Executor:
     """Runs one PreparedBatch: forward, sample, and hand tokens back to the CPU."""
 
@@ -70,15 +97,43 @@ class Executor:
                             if self.runner.decode_inputs is not None else None),
         )
         self.sampler = Sampler() if sampler is None else sampler
+        self._host: list[torch.Tensor | None] = [None, None]
+        self._in_flight: list[PendingStep | None] = [None, None]
+        self._turn = 0
 
     @torch.inference_mode()
     def execute(self, batch: PreparedBatch) -> StepResult:
+        return self.launch(batch).result()
+
+    @torch.inference_mode()
+    def launch(self, batch: PreparedBatch) -> PendingStep:
+        """Enqueue the step and return at once; its sampled ids travel to a
+        pinned host buffer behind it on the stream. Until ``result()`` the
+        host is free to build the next batch, whose ``input_token_sources``
+        may name this step's sampled rows (they never leave the device)."""
         counters = self.sampler.counters(batch.sampling_params, batch.sample_request_ids)
         out = self.runner.run_and_sample(batch, counters)
-        tokens = ()
-        if out is not None:
-            tokens = tuple(out[1].tolist())  # the step's one device->host sync
-        return StepResult(batch.plan_id, batch.sample_request_ids, tokens)
+        if out is None:
+            return PendingStep(batch.plan_id, batch.sample_request_ids, None, 0, None)
+        tokens = out[1]
+        rows = tokens.numel()
+        # Two host buffers alternate; a step two launches back must be read
+        # before its buffer is reused.
+        index = self._turn
+        self._turn ^= 1
+        previous = self._in_flight[index]
+        if previous is not None:
+            previous.result()
+        host = self._host[index]
+        if host is None or host.numel() < rows:
+            host = torch.empty(max(rows, 64), dtype=torch.long, pin_memory=True)
+            self._host[index] = host
+        host[:rows].copy_(tokens, non_blocking=True)
+        event = torch.cuda.Event()
+        event.record()
+        pending = PendingStep(batch.plan_id, batch.sample_request_ids, host, rows, event)
+        self._in_flight[index] = pending
+        return pending
 
     def release(self, request_id: int) -> None:
         self.sampler.release(request_id)

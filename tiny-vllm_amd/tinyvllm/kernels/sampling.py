@@ -68,3 +68,21 @@ def sample(
             out.data_ptr(), None, 0, dtype_code(logits.dtype), stream_of(device),
         ))
     return out
+
+
+def resolve_tokens(tokens: torch.Tensor, src: torch.Tensor, prev: torch.Tensor) -> torch.Tensor:
+    """In place: ``tokens[i] = prev[src[i]]`` wherever ``0 <= src[i] < len(prev)``.
+
+    ``src[i] = -1`` keeps the uploaded token. Lets a step's input ids name the
+    previous step's sampled tokens while those are still on the device (the
+    reference uploads host token ids only: tinyvllm/runtime/inputs.py:88-111)."""
+    lib = load_kernels()
+    device = require_gpu(tokens, src, prev)
+    for tensor in (tokens, src, prev):
+        if tensor.dtype != torch.long or tensor.dim() != 1 or not tensor.is_contiguous():
+            raise RuntimeError("resolve_tokens takes contiguous 1-D int64 tensors")
+    if src.shape != tokens.shape:
+        raise RuntimeError("src must have one entry per token")
+    check(lib.tvllm_resolve_tokens(tokens.data_ptr(), src.data_ptr(), prev.data_ptr(),
+                                   tokens.numel(), prev.numel(), stream_of(device)))
+    return tokens

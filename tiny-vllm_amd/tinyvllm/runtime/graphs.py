@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from tinyvllm.kernels.paged_decode import decode_split_plan
-from tinyvllm.kernels.sampling import sample
+from tinyvllm.kernels.sampling import resolve_tokens, sample
 from tinyvllm.paged_kv import PagedKVCache
 from tinyvllm.runtime.attention import HipAttention
 from tinyvllm.runtime.inputs import DecodeInputs
@@ -54,9 +54,13 @@ class DecodeGraphs:
     @torch.inference_mode()
     def capture(self, model: torch.nn.Module, inputs: DecodeInputs, cache: PagedKVCache,
                 workspace: torch.Tensor | None, *,
-                sizes: tuple[int, ...] | None = None) -> None:
+                sizes: tuple[int, ...] | None = None,
+                tokens: torch.Tensor | None = None) -> None:
         """Capture one graph per bucket size (default: ``bucket_sizes`` up to
-        the input capacity)."""
+        the input capacity). ``tokens`` (int64, >= capacity rows) receives
+        every replay's sampled ids; a replay first takes its input ids from
+        the previous step's rows there wherever the uploaded token sources
+        say so."""
         limit = min(inputs.capacity, cache.num_blocks)
         sizes = bucket_sizes(limit) if sizes is None else tuple(
             sorted({min(int(x), limit) for x in sizes}))
@@ -69,7 +73,11 @@ class DecodeGraphs:
         d["offsets"][:n + 1].copy_(torch.arange(n + 1, device=inputs.device))
         d["lengths"][:n].fill_(1)
         d["blocks"][:n].copy_(inputs.rows[:n])
-        self.tokens = torch.zeros(inputs.capacity, dtype=torch.long, device=inputs.device)
+        if tokens is None:
+            tokens = torch.zeros(inputs.capacity, dtype=torch.long, device=inputs.device)
+        if tokens.dtype != torch.long or tokens.numel() < inputs.capacity:
+            raise ValueError("graph token buffer must hold capacity int64 rows")
+        self.tokens = tokens
         # Build dtype-cast RoPE tables before capture.
         model.model.rotary_emb(inputs.d["positions"][:1], next(model.parameters()).dtype)
 
@@ -108,8 +116,10 @@ class DecodeGraphs:
         model_input = inputs.view(size, max_context_len=bound)
         params = inputs.sampling_views(size)
         out = self.tokens[:size]
+        sources = inputs.d["sources"][:size]
 
         def step():
+            resolve_tokens(model_input.input_ids, sources, self.tokens)
             attention = HipAttention(model_input, cache, decode_workspace=workspace)
             hidden = model(model_input.input_ids, model_input.positions, attention=attention)
             logits = model.compute_logits(hidden)

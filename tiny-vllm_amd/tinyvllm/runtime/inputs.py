@@ -10,7 +10,9 @@ Layout (bytes, N = capacity rows, P = N * pages_per_row):
   float32 [N] temperature | float32 [N] top_p |
   int64 [N] tokens | [N] positions | [N] slots | [N + 1] table offsets |
   [N] context lengths | [N] top_k | [N] seeds | [N] sample counters |
-  [P] block ids
+  [N] token sources | [P] block ids
+A token source j >= 0 replaces the row's token, on the device, by row j of
+the previous step's sampled tokens (-1: keep the uploaded id).
 Rows past the live count are padding: slot -1 (no KV write), length 0 (zero
 attention output), greedy sampling.
 """
@@ -23,7 +25,7 @@ from tinyvllm.batch import PreparedBatch
 from tinyvllm.runtime.contracts import ModelInput, PagedKVMetadata, SingleQueryMetadata
 
 _INT_FIELDS = ("tokens", "positions", "slots", "offsets", "lengths", "top_k", "seeds",
-               "counters", "blocks")
+               "counters", "sources", "blocks")
 
 
 class DecodeInputs:
@@ -33,7 +35,7 @@ class DecodeInputs:
     @staticmethod
     def device_bytes(*, max_num_seqs: int, max_model_len: int, block_size: int) -> int:
         pages = -(-max_model_len // block_size)
-        return 4 * 2 * max_num_seqs + 8 * (8 * max_num_seqs + 1 + max_num_seqs * pages)
+        return 4 * 2 * max_num_seqs + 8 * (9 * max_num_seqs + 1 + max_num_seqs * pages)
 
     def __init__(self, *, max_num_seqs: int, max_model_len: int, block_size: int,
                  device: torch.device | str) -> None:
@@ -49,7 +51,8 @@ class DecodeInputs:
         self.block_size = block_size
         self.table_capacity = n * -(-max_model_len // block_size)
         sizes = {"tokens": n, "positions": n, "slots": n, "offsets": n + 1, "lengths": n,
-                 "top_k": n, "seeds": n, "counters": n, "blocks": self.table_capacity}
+                 "top_k": n, "seeds": n, "counters": n, "sources": n,
+                 "blocks": self.table_capacity}
         self.float_bytes = 8 * n
         total = self.float_bytes + 8 * sum(sizes.values())
         self.host = torch.zeros(total, dtype=torch.uint8, pin_memory=True)
@@ -70,7 +73,7 @@ class DecodeInputs:
 
         self.h = {k: v.numpy() for k, v in carve(self.host).items()}
         self.d = carve(self.device_data)
-        self._blocks_offset = self.float_bytes + 8 * (8 * n + 1)
+        self._blocks_offset = self.float_bytes + 8 * (9 * n + 1)
         self.rows = torch.arange(n, dtype=torch.long, device=self.device)
         # Graph capture and padding defaults: every row is padding.
         self._reset_padding(0, 0)
@@ -88,6 +91,7 @@ class DecodeInputs:
         h["top_k"][count:] = 0
         h["seeds"][count:] = 0
         h["counters"][count:] = 0
+        h["sources"][count:] = -1
 
     def prepare(self, batch: PreparedBatch, counters) -> ModelInput | None:
         """Upload a validated all-decode batch; None if it is not one."""
@@ -124,6 +128,8 @@ class DecodeInputs:
         h["seeds"][:count] = [p.seed - (1 << 64) if p.seed >= (1 << 63) else p.seed
                               for p in rows]
         h["counters"][:count] = counters
+        sources = batch.input_token_sources
+        h["sources"][:count] = -1 if sources is None else sources
         size = self._blocks_offset + 8 * table_size
         self.device_data[:size].copy_(self.host[:size], non_blocking=True)
         self.upload_done.record(self.stream)

@@ -14,7 +14,7 @@ from torch import nn
 from tinyvllm._validation import _check_positive_int
 from tinyvllm.batch import PreparedBatch
 from tinyvllm.kernels.paged_decode import decode_workspace_bytes
-from tinyvllm.kernels.sampling import sample
+from tinyvllm.kernels.sampling import resolve_tokens, sample
 from tinyvllm.paged_kv import PagedKVCache
 from tinyvllm.runtime.attention import HipAttention, SDPAAttention, check_backend
 from tinyvllm.runtime.contracts import (
@@ -63,6 +63,10 @@ class ModelRunner:
         self.decode_graphs: DecodeGraphs | None = None
         self.kv_cache: PagedKVCache | None = None
         self.decode_workspace: torch.Tensor | None = None
+        # Sampled ids of the last launched step stay here on the device; the
+        # next batch's input_token_sources index them (pipelined decode).
+        self.sampled = torch.zeros(max_num_seqs, dtype=torch.long, device=self.device)
+        self._prev_count = 0
         try:
             kv_dtype = self.dtype if kv_cache_dtype is None else kv_cache_dtype
             if kv_dtype not in (self.dtype, torch.float8_e4m3fn):
@@ -93,7 +97,7 @@ class ModelRunner:
                     self.decode_graphs = DecodeGraphs(self.decode_inputs.stream)
                     self.decode_graphs.capture(model, self.decode_inputs, self.kv_cache,
                                                self.decode_workspace,
-                                               sizes=graph_sizes)
+                                               sizes=graph_sizes, tokens=self.sampled)
         except Exception:
             self.clear()
             raise
@@ -162,6 +166,13 @@ class ModelRunner:
         expect = ids[toff[item] + pos // bs] * bs + pos % bs
         if (expect != np.asarray(batch.kv_slot_mapping, dtype=np.int64)).any():
             raise ValueError("write slots do not match block tables and positions")
+        sources = batch.input_token_sources
+        if sources is not None:
+            src = np.asarray(sources, dtype=np.int64)
+            if src.shape != (tokens,):
+                raise ValueError("input_token_sources must have one entry per token")
+            if src.size and (src.min() < -1 or src.max() >= getattr(self, "_prev_count", 0)):
+                raise ValueError("input token source is not a row of the previous step")
         samples = batch.sample_token_indices
         if (len(batch.sample_request_ids) != batch.num_samples
                 or len(batch.sampling_params) != batch.num_samples
@@ -248,6 +259,21 @@ class ModelRunner:
         self._validate(batch, cache)
         if counters is None:
             counters = [0] * batch.num_samples
+        self._prev_count = 0  # until this step's ids are in place
+        out = self._forward(batch, counters, want_tokens)
+        if out is None or out[1] is None:
+            return out
+        logits, tokens = out
+        rows = tokens.numel()
+        if rows <= self.sampled.numel():
+            if tokens.data_ptr() != self.sampled.data_ptr():
+                self.sampled[:rows].copy_(tokens)
+                tokens = self.sampled[:rows]
+            self._prev_count = rows
+        return logits, tokens
+
+    def _forward(self, batch, counters, want_tokens):
+        cache = self.kv_cache
         if self.decode_inputs is not None:
             model_input = self.decode_inputs.prepare(batch, counters)
             if model_input is not None:
@@ -256,6 +282,10 @@ class ModelRunner:
                         batch.num_items, max(batch.context_lens_after))
                     if replayed is not None:
                         return replayed
+                if batch.input_token_sources is not None:
+                    resolve_tokens(model_input.input_ids,
+                                   self.decode_inputs.d["sources"][:batch.num_items],
+                                   self.sampled)
                 attention = HipAttention(model_input, cache,
                                          decode_workspace=self.decode_workspace)
                 hidden = self.model(model_input.input_ids, model_input.positions,
@@ -266,6 +296,15 @@ class ModelRunner:
                     tokens = sample(logits, *self.decode_inputs.sampling_views(batch.num_items))
                 return logits, tokens
         model_input = self._lower(batch)
+        if batch.input_token_sources is not None:
+            src = torch.tensor(np.asarray(batch.input_token_sources, dtype=np.int64)).to(
+                self.device, non_blocking=True)
+            if self.backend == "hip":
+                resolve_tokens(model_input.input_ids, src, self.sampled)
+            else:  # the torch path: same substitution with torch ops
+                taken = self.sampled[src.clamp(min=0)]
+                model_input.input_ids.copy_(torch.where(src >= 0, taken,
+                                                        model_input.input_ids))
         hidden = self.model(model_input.input_ids, model_input.positions,
                             attention=self._attention(batch, model_input))
         if batch.num_samples == 0:
