@@ -674,6 +674,7 @@ def end_to_end(name: str, args) -> None:
     from tinyvllm import SamplingParams
     from tinyvllm.bootstrap import build_engine
     from tinyvllm.models.qwen3 import Qwen3ForCausalLM
+    from tinyvllm.scheduler import ScheduleDecision
 
     spec = E2E[name]
     rng = np.random.default_rng(0)
@@ -714,7 +715,7 @@ def end_to_end(name: str, args) -> None:
         generated += len(events.token_events)
         for ev in events.token_events:
             first_token.setdefault(ev.request_id, now - t0)
-        if not events.token_events and not events.completion_events:
+        if engine.scheduler.last_decision is ScheduleDecision.IDLE:
             arrival = engine.scheduler.next_arrival_ns
             if arrival is not None:
                 time.sleep(max(0.0, (arrival - time.monotonic_ns()) / 1e9))
@@ -763,6 +764,7 @@ def run_requests(engine, prompts, new: int, gap_ns: int):
     import torch
 
     from tinyvllm import SamplingParams
+    from tinyvllm.scheduler import ScheduleDecision
 
     params = SamplingParams(max_new_tokens=new, ignore_eos=True)
     torch.cuda.synchronize()
@@ -773,7 +775,7 @@ def run_requests(engine, prompts, new: int, gap_ns: int):
     while engine.has_unfinished():
         events = engine.step()
         done += events.completion_events
-        if not events.token_events and not events.completion_events:
+        if engine.scheduler.last_decision is ScheduleDecision.IDLE:
             arrival = engine.scheduler.next_arrival_ns
             if arrival is not None:
                 time.sleep(max(0.0, (arrival - time.monotonic_ns()) / 1e9))

@@ -17,7 +17,7 @@ from tinyvllm.engine import Engine, GenerateRequest
 from tinyvllm.executor import ExecutorCapabilities
 from tinyvllm.request import RequestStatus, SamplingParams
 from tinyvllm.runtime.runner import ModelRunner
-from tinyvllm.scheduler import Scheduler
+from tinyvllm.scheduler import PENDING_TOKEN, Scheduler
 
 VOCAB = 97
 EOS = 5
@@ -46,21 +46,33 @@ class SimExecutor:
         self.batches = 0
         self.fail_at = None
         self.released = []
+        self.truth = {}       # request -> every token the simulated model saw or made
+        self.last = []        # the previous step's sampled tokens ("on the device")
 
     def execute(self, batch):
         self.batches += 1
         if self.fail_at == self.batches:
             raise RuntimeError("injected executor failure")
+        self.validator._prev_count = len(self.last)
         self.validator._validate(batch, self.cache)
+        ids = list(batch.input_ids)
+        if batch.input_token_sources is not None:  # resolved "on the device"
+            ids = [self.last[s] if s >= 0 else t
+                   for t, s in zip(ids, batch.input_token_sources)]
         out = []
         for i, rid in enumerate(batch.request_ids):
             start, end = batch.q_offsets[i], batch.q_offsets[i + 1]
             before, after = batch.context_lens_before[i], batch.context_lens_after[i]
-            # Ground truth: the request's own tokens (prompt + sampled so far).
-            hist = self.scheduler.get_request(rid).token_slice(0, after)
-            assert list(batch.input_ids[start:end]) == hist[before:after]
+            # Ground truth: the request's own tokens (prompt + sampled so far);
+            # the scheduler's copy may still hold placeholders for tokens in flight.
+            truth = self.truth.setdefault(
+                rid, list(self.scheduler.get_request(rid).prompt_token_ids))
+            hist = truth[:after]
+            assert ids[start:end] == hist[before:after]
+            known = self.scheduler.get_request(rid).token_slice(0, after)
+            assert all(k == h for k, h in zip(known, hist) if k >= 0)
             for t, slot in zip(range(start, end), batch.kv_slot_mapping[start:end]):
-                self.slots[slot] = batch.input_ids[t]
+                self.slots[slot] = ids[t]
             # Read back the whole context through the block table.
             toff = batch.kv_block_table_offsets
             table = batch.kv_block_table_ids[toff[i]:toff[i + 1]]
@@ -68,7 +80,11 @@ class SimExecutor:
                 slot = table[p // self.bs] * self.bs + p % self.bs
                 assert self.slots.get(slot) == hist[p], (rid, p)
             if end - 1 in batch.sample_token_indices:
-                out.append(next_token(hist[:after]))
+                token = next_token(hist)
+                if len(truth) == after:
+                    truth.append(token)
+                out.append(token)
+        self.last = out
         return StepResult(batch.plan_id, batch.sample_request_ids, tuple(out))
 
     def release(self, request_id):
@@ -76,6 +92,27 @@ class SimExecutor:
 
     def clear(self):
         pass
+
+
+class _Launched:
+    def __init__(self, result):
+        self.sample_request_ids = result.sample_request_ids
+        self._result = result
+
+    def result(self):
+        return self._result
+
+
+class PipelinedSimExecutor(SimExecutor):
+    """Adds launch(): the engine plans step k+1 before reading step k's
+    tokens, whose ids reach the next batch only as input_token_sources."""
+
+    def launch(self, batch):
+        if batch.input_token_sources is not None:
+            self.pipelined_batches += 1
+        return _Launched(self.execute(batch))
+
+    pipelined_batches = 0
 
 
 def expected(prompt, params, max_model_len):
@@ -89,9 +126,15 @@ def expected(prompt, params, max_model_len):
     return out
 
 
+@pytest.fixture(params=[False, True], ids=["serial", "pipelined"])
+def pipelined(request):
+    return request.param
+
+
 def make_engine(*, bs=4, blocks=96, max_len=96, seqs=4, tokens=24, chunk=10,
-                prefix=True, clock=None):
-    ex = SimExecutor(block_size=bs, num_blocks=blocks, max_model_len=max_len, max_batch=seqs)
+                prefix=True, clock=None, pipelined=False):
+    cls = PipelinedSimExecutor if pipelined else SimExecutor
+    ex = cls(block_size=bs, num_blocks=blocks, max_model_len=max_len, max_batch=seqs)
     sched = Scheduler(max_active_requests=seqs, max_step_requests=seqs,
                       max_scheduled_tokens=tokens, prefill_chunk_size=chunk,
                       max_model_len=max_len, prefill_reserve_tokens=4,
@@ -103,9 +146,9 @@ def make_engine(*, bs=4, blocks=96, max_len=96, seqs=4, tokens=24, chunk=10,
 
 
 @pytest.mark.parametrize("prefix", [True, False])
-def test_many_requests_chunked_prefill_matches_model(prefix):
+def test_many_requests_chunked_prefill_matches_model(prefix, pipelined):
     rng = random.Random(0)
-    engine, ex = make_engine(prefix=prefix)
+    engine, ex = make_engine(prefix=prefix, pipelined=pipelined)
     reqs = []
     for _ in range(12):
         prompt = [rng.randrange(6, VOCAB) for _ in range(rng.randrange(1, 40))]
@@ -118,9 +161,9 @@ def test_many_requests_chunked_prefill_matches_model(prefix):
     assert engine.scheduler.block_manager.free_block_count == 96  # everything released
 
 
-def test_shared_prefixes_hit_the_cache_and_stay_exact():
+def test_shared_prefixes_hit_the_cache_and_stay_exact(pipelined):
     rng = random.Random(1)
-    engine, ex = make_engine(blocks=80, max_len=80, chunk=8, tokens=20)
+    engine, ex = make_engine(blocks=80, max_len=80, chunk=8, tokens=20, pipelined=pipelined)
     shared = [rng.randrange(6, VOCAB) for _ in range(30)]
     reqs = [GenerateRequest(shared + [rng.randrange(6, VOCAB) for _ in range(rng.randrange(1, 6))],
                             SamplingParams(max_new_tokens=6, ignore_eos=True)) for _ in range(6)]
@@ -131,9 +174,9 @@ def test_shared_prefixes_hit_the_cache_and_stay_exact():
     assert cache.hits >= 1 and cache.hit_tokens >= 7 * 4
 
 
-def test_poisson_arrivals_with_injected_clock():
+def test_poisson_arrivals_with_injected_clock(pipelined):
     now = [0]
-    engine, ex = make_engine(clock=lambda: now[0])
+    engine, ex = make_engine(clock=lambda: now[0], pipelined=pipelined)
     rng = np.random.default_rng(2)
     arrivals = np.cumsum(rng.exponential(5_000_000, size=5)).astype(int)
     for i, at in enumerate(arrivals):
@@ -150,8 +193,8 @@ def test_poisson_arrivals_with_injected_clock():
     assert len(finished) == 5
 
 
-def test_cancel_and_eos():
-    engine, ex = make_engine()
+def test_cancel_and_eos(pipelined):
+    engine, ex = make_engine(pipelined=pipelined)
     a = engine.submit([7] * 12, SamplingParams(max_new_tokens=50, ignore_eos=True))
     b = engine.submit([8] * 5, SamplingParams(max_new_tokens=50))
     engine.step()
@@ -167,8 +210,8 @@ def test_cancel_and_eos():
     assert set(ex.released) == {a, b}
 
 
-def test_executor_failure_is_fail_stop():
-    engine, ex = make_engine()
+def test_executor_failure_is_fail_stop(pipelined):
+    engine, ex = make_engine(pipelined=pipelined)
     ex.fail_at = 3
     engine.submit([9] * 30, SamplingParams(max_new_tokens=10))
     with pytest.raises(RuntimeError):
@@ -184,3 +227,67 @@ def test_requests_that_cannot_fit_are_rejected():
         engine.submit([6] * 40, SamplingParams(max_new_tokens=10))
     with pytest.raises(ValueError):
         engine.submit([6] * 97, SamplingParams(max_new_tokens=1))
+
+
+def _eos_prompts(rng, count, max_new):
+    """Prompts whose simulated continuation hits EOS before max_new tokens."""
+    found = []
+    while len(found) < count:
+        prompt = [rng.randrange(6, VOCAB) for _ in range(rng.randrange(1, 30))]
+        out = expected(prompt, SamplingParams(max_new_tokens=max_new), 96)
+        if out[-1] == EOS and len(out) < max_new:
+            found.append(prompt)
+    return found
+
+
+def test_pipelined_eos_drops_rows_launched_past_the_stop():
+    """EOS is seen one step late: the request's next row is already launched.
+    Its outputs must end at EOS, its extra row be discarded, and every block
+    come back to the pool."""
+    rng = random.Random(7)
+    engine, ex = make_engine(pipelined=True, seqs=4, tokens=24)
+    prompts = _eos_prompts(rng, 6, 40)
+    reqs = [GenerateRequest(p, SamplingParams(max_new_tokens=40)) for p in prompts]
+    reqs += [GenerateRequest([rng.randrange(6, VOCAB) for _ in range(9)],
+                             SamplingParams(max_new_tokens=12, ignore_eos=True))
+             for _ in range(3)]
+    outs = engine.generate(reqs)
+    for req, out in zip(reqs, outs):
+        assert out.status is RequestStatus.FINISHED
+        assert list(out.output_token_ids) == expected(req.prompt_token_ids, req.sampling, 96)
+    assert ex.pipelined_batches > 0
+    assert engine.scheduler.block_manager.free_block_count == 96
+    assert not engine.scheduler.has_unresolved_steps
+    # The engine is reusable and still exact afterwards.
+    again = engine.generate(reqs[:2])
+    assert [list(o.output_token_ids) for o in again] == [list(o.output_token_ids)
+                                                          for o in outs[:2]]
+
+
+def test_pipelined_cancel_drops_the_token_in_flight():
+    engine, ex = make_engine(pipelined=True)
+    a = engine.submit([7] * 12, SamplingParams(max_new_tokens=50, ignore_eos=True))
+    seen = []
+    for _ in range(6):
+        seen += [e.token_id for e in engine.step().token_events]
+    assert engine.cancel(a)
+    events = []
+    while engine.has_unfinished():
+        events += engine.step().completion_events
+    (done,) = events
+    assert done.status is RequestStatus.ABORTED
+    # Only tokens that reached the host count; all of them are the model's.
+    assert list(done.output_token_ids) == seen
+    assert seen == expected([7] * 12, SamplingParams(max_new_tokens=50, ignore_eos=True),
+                            96)[:len(seen)]
+    assert PENDING_TOKEN not in done.output_token_ids
+    assert engine.scheduler.block_manager.free_block_count == 96
+
+
+def test_pipelined_token_events_lag_one_step():
+    engine, ex = make_engine(pipelined=True)
+    engine.submit([9] * 3, SamplingParams(max_new_tokens=3, ignore_eos=True))
+    first = engine.step()   # prefill launched, nothing resolved yet
+    assert not first.token_events
+    second = engine.step()  # decode launched; the prefill's token resolves
+    assert len(second.token_events) == 1

@@ -160,7 +160,10 @@ class BatchBuilder:
         self.max_model_len = max_model_len
 
     def prepare(self, plan: StepPlan, requests: tuple[RequestState, ...], *,
-                kv: KVPlan) -> PreparedBatch:
+                kv: KVPlan, pending_rows: dict[int, int] | None = None) -> PreparedBatch:
+        """``pending_rows``: request -> row among the previous launched step's
+        samples, for requests whose newest token (a negative placeholder) is
+        still on the device; such inputs become ``input_token_sources``."""
         if len(requests) != len(plan.items):
             raise ValueError("requests must align with plan items")
         if kv.plan_id != plan.plan_id:
@@ -180,6 +183,7 @@ class BatchBuilder:
         table_off = [0]
         slots: list[np.ndarray] = []
         rids: list[int] = []
+        sources: list[int] | None = None
         for item, request in zip(plan.items, requests):
             if request.request_id != item.request_id:
                 raise ValueError("request order does not match plan")
@@ -191,6 +195,16 @@ class BatchBuilder:
             tokens = request.token_slice(item.token_start, item.token_end)
             if len(tokens) != item.query_len:
                 raise RuntimeError("token slice length does not match query_len")
+            if tokens and tokens[-1] < 0:  # the previous step's sample, unresolved
+                row = (pending_rows or {}).get(request.request_id)
+                if row is None or min(tokens[:-1], default=0) < 0:
+                    raise ValueError("unresolved input token without a pending sample row")
+                if sources is None:
+                    sources = [-1] * len(input_ids)
+                sources.extend([-1] * (len(tokens) - 1) + [row])
+                tokens = tokens[:-1] + [0]
+            elif sources is not None:
+                sources.extend([-1] * len(tokens))
             table, slot_map = kv.append_metadata(item.request_id, item.token_start,
                                                  item.query_len)
             rids.append(request.request_id)
@@ -219,4 +233,5 @@ class BatchBuilder:
             kv_block_table_offsets=tuple(table_off),
             kv_slot_mapping=np.concatenate(slots) if slots else np.zeros(0, np.int64),
             request_ids=tuple(rids),
+            input_token_sources=None if sources is None else tuple(sources),
         )

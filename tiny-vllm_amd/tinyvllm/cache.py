@@ -306,14 +306,19 @@ class BlockManager:
         return self.prefix_cache.match(request_id, token_ids)
 
     def cache_full_blocks(self, request_id: int,
-                          token_slice: Callable[[int, int], Sequence[int]]) -> None:
+                          token_slice: Callable[[int, int], Sequence[int]],
+                          known_tokens: int | None = None) -> None:
         """Publish the request's completed blocks; a block whose contents are
-        already cached elsewhere is swapped for the canonical copy."""
+        already cached elsewhere is swapped for the canonical copy.
+        ``known_tokens`` caps the publishable prefix (token ids past it are
+        still on the device)."""
         if self._open is not None:
             raise RuntimeError("publish prefix blocks only after successful writes")
         table = self._tables[request_id]
-        swaps = self.prefix_cache.publish(request_id, table, self.valid_token_count(request_id),
-                                          token_slice)
+        valid = self.valid_token_count(request_id)
+        if known_tokens is not None:
+            valid = min(valid, known_tokens)
+        swaps = self.prefix_cache.publish(request_id, table, valid, token_slice)
         if not swaps:
             return
         updated = list(table)

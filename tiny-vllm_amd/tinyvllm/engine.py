@@ -2,7 +2,11 @@
 
 ``step()`` applies queued commands, asks the scheduler for one plan,
 flattens it (BatchBuilder), runs it on the executor and commits the sampled
-tokens. Any failure after dispatch is fail-stop: the engine releases all
+tokens. With an executor that can ``launch`` (the GPU executor), steps are
+pipelined: ``step()`` launches plan k, commits its KV side, then waits for
+plan k-1's tokens and resolves them, so the host plans and uploads each step
+while the GPU runs the previous one; token and completion events arrive one
+step later than the launch that produced them. Any failure after dispatch is fail-stop: the engine releases all
 KV ownership and refuses further work. Time is injectable (``clock``,
 ``sleep``, ``step(now_ns)``) for deterministic arrival schedules.
 """
@@ -30,6 +34,9 @@ class EngineExecutor(Protocol):
     def capabilities(self) -> ExecutorCapabilities: ...
 
     def execute(self, batch: PreparedBatch) -> StepResult: ...
+
+    # Optional: ``launch(batch)`` returning an object with ``result() ->
+    # StepResult`` enables pipelined steps.
 
     def release(self, request_id: int) -> None: ...
 
@@ -83,7 +90,10 @@ class Engine:
 
     def __init__(self, scheduler: Scheduler, executor: EngineExecutor, *,
                  clock: Callable[[], int] = time.monotonic_ns,
-                 sleep: Callable[[float], None] = time.sleep) -> None:
+                 sleep: Callable[[float], None] = time.sleep,
+                 pipelined: bool | None = None) -> None:
+        """``pipelined``: None uses pipelined steps when the executor has
+        ``launch``; False forces one step at a time."""
         executor.capabilities.validate_configuration(
             max_model_len=scheduler.max_model_len,
             block_size=scheduler.kv_block_size,
@@ -104,6 +114,11 @@ class Engine:
         self._closed = False
         self._failed: str | None = None
         self._generating = False
+        can_launch = callable(getattr(executor, "launch", None))
+        if pipelined and not can_launch:
+            raise ValueError("pipelined steps need an executor with launch()")
+        self._pipelined = can_launch if pipelined is None else bool(pipelined)
+        self._in_flight = None  # the launched step whose tokens are unresolved
 
     @classmethod
     def from_config(cls, config: "EngineConfig") -> "Engine":
@@ -176,33 +191,64 @@ class Engine:
             if isinstance(command, CancelCommand):
                 self._cancelling.discard(command.request_id)
         txn = self.scheduler.begin_step(start)
-        if txn is None:
+        launched = None
+        accepted: tuple[tuple[int, int], ...] | None = None
+        if txn is not None:
             try:
-                return self._events(None)
+                requests = tuple(self.scheduler.get_request(i.request_id)
+                                 for i in txn.plan.items)
+                batch = self.builder.prepare(
+                    txn.plan, requests, kv=txn.kv,
+                    pending_rows=self.scheduler.pending_sample_rows())
+                dispatch = start if explicit else max(start, self._clock())
+            except BaseException:
+                self.scheduler.rollback(txn)
+                raise
+            try:
+                self.scheduler.mark_dispatched(txn, dispatch)
             except BaseException as exc:
                 self._fail_stop(exc)
                 raise
+            try:
+                if self._pipelined:
+                    launched = self.executor.launch(batch)
+                else:
+                    result = self.executor.execute(batch)
+            except BaseException as exc:
+                self._fail_stop(exc)
+                raise RuntimeError("executor failed; engine is failed") from exc
+            try:
+                done = dispatch if explicit else max(dispatch, self._clock())
+                if self._pipelined:
+                    self.scheduler.commit_launch(txn, done)
+                else:
+                    accepted = self.scheduler.commit_step(txn, result, done)
+            except BaseException as exc:
+                self._fail_stop(exc)
+                raise
+        previous, self._in_flight = self._in_flight, launched
+        if previous is not None:
+            accepted = self._resolve(previous, start if explicit else None)
         try:
-            requests = tuple(self.scheduler.get_request(i.request_id) for i in txn.plan.items)
-            batch = self.builder.prepare(txn.plan, requests, kv=txn.kv)
-            dispatch = start if explicit else max(start, self._clock())
-        except BaseException:
-            self.scheduler.rollback(txn)
-            raise
-        try:
-            self.scheduler.mark_dispatched(txn, dispatch)
+            events = self._events(accepted)
         except BaseException as exc:
             self._fail_stop(exc)
             raise
+        if not self._active and self._in_flight is not None:
+            # Only rows of finished requests are in flight: drain them.
+            previous, self._in_flight = self._in_flight, None
+            self._resolve(previous, start if explicit else None)
+        return events
+
+    def _resolve(self, pending, now_ns: int | None) -> tuple[tuple[int, int], ...]:
         try:
-            result = self.executor.execute(batch)
+            result = pending.result()
         except BaseException as exc:
             self._fail_stop(exc)
             raise RuntimeError("executor failed; engine is failed") from exc
         try:
-            done = dispatch if explicit else max(dispatch, self._clock())
-            self.scheduler.commit_step(txn, result, done)
-            return self._events(result)
+            return self.scheduler.resolve(result, self._clock() if now_ns is None
+                                          else now_ns)
         except BaseException as exc:
             self._fail_stop(exc)
             raise
@@ -239,7 +285,7 @@ class Engine:
             raise RuntimeError("engine stopped before all requests completed")
         return [outputs[i] for i in ids]
 
-    def _events(self, result: StepResult | None) -> EngineStepEvents:
+    def _events(self, accepted: tuple[tuple[int, int], ...] | None) -> EngineStepEvents:
         completions = self.scheduler.consume_finished()
         done = {e.request_id for e in completions}
         # A cancel queued during execute may target a request that just
@@ -254,10 +300,9 @@ class Engine:
         self._cancelling -= done
         for event in completions:
             self.executor.release(event.request_id)
-        if result is None:
+        if not accepted:
             return EngineStepEvents(completion_events=completions)
-        tokens = tuple(TokenEvent(r, t) for r, t in zip(result.sample_request_ids,
-                                                        result.sampled_token_ids))
+        tokens = tuple(TokenEvent(r, t) for r, t in accepted)
         return EngineStepEvents(token_events=tokens, completion_events=completions)
 
     def reset_prefix_cache(self) -> None:
@@ -290,6 +335,7 @@ class Engine:
         self._dispose(cause)
 
     def _dispose(self, cause: BaseException) -> None:
+        self._in_flight = None
         self._commands.clear()
         self._active.clear()
         self._cancelling.clear()

@@ -14,6 +14,16 @@ the same prefix block in one step are serialised so the second reuses it.
 Every step is a transaction: ``begin_step`` stages blocks, ``mark_dispatched``
 publishes ownership right before execution, ``commit_step`` applies the
 sampled tokens (EOS / length stop) or ``rollback`` / ``fail_step`` undo it.
+
+Pipelined engines split ``commit_step`` in two (beyond the reference, whose
+engine waits for every step's tokens before planning the next):
+``commit_launch`` commits the step's KV writes and appends a ``PENDING_TOKEN``
+placeholder for each sampled token, so the next step can be planned while the
+GPU still runs this one; ``resolve`` later fills the placeholders in launch
+order and applies EOS. A request that hit EOS may already sit in the next,
+launched step: its extra row is discarded when that step resolves. Length
+stops are known at launch; such a request leaves the decode queue at once and
+finishes when its last token resolves.
 """
 from __future__ import annotations
 
@@ -61,6 +71,9 @@ class CancelCommand:
 
 
 EngineCommand = AddCommand | CancelCommand
+
+# An output slot whose token id is still on the device (pipelined steps).
+PENDING_TOKEN = -1
 
 
 class TxnState(Enum):
@@ -156,6 +169,13 @@ class Scheduler:
         self._txn: ScheduleTxn | None = None
         self._decision = ScheduleDecision.IDLE
         self._failed = False
+        # Pipelined steps: launched plans awaiting their tokens (plan id,
+        # sampled request ids), each request's unresolved output slots
+        # (plan id, output index), and length-stopped requests whose last
+        # token is unresolved.
+        self._launched: deque[tuple[int, tuple[int, ...]]] = deque()
+        self._unresolved: dict[int, deque[tuple[int, int]]] = {}
+        self._finishing: set[int] = set()
 
     # ------------------------------------------------------------ queries --
 
@@ -166,6 +186,20 @@ class Scheduler:
     @property
     def has_open_transaction(self) -> bool:
         return self._txn is not None
+
+    @property
+    def has_unresolved_steps(self) -> bool:
+        """Launched steps whose sampled tokens have not been resolved yet."""
+        return bool(self._launched)
+
+    def pending_sample_rows(self) -> dict[int, int]:
+        """Request -> row of its token among the last launched step's samples,
+        for requests whose newest output is still unresolved."""
+        if not self._launched:
+            return {}
+        plan_id, rids = self._launched[-1]
+        return {rid: row for row, rid in enumerate(rids)
+                if self._unresolved.get(rid) and self._unresolved[rid][-1][0] == plan_id}
 
     @property
     def last_decision(self) -> ScheduleDecision:
@@ -362,39 +396,55 @@ class Scheduler:
         object.__setattr__(txn, "state", TxnState.ROLLED_BACK)
         self._txn = None
 
-    def commit_step(self, txn: ScheduleTxn, result: StepResult, now_ns: int) -> None:
-        """Apply a step's sampled tokens; finish requests on EOS or length."""
+    def commit_step(self, txn: ScheduleTxn, result: StepResult,
+                    now_ns: int) -> tuple[tuple[int, int], ...]:
+        """Apply a step's sampled tokens; finish requests on EOS or length.
+        Returns the (request id, token id) pairs applied."""
+        self._require(txn, TxnState.DISPATCHED)
+        try:
+            self._check_result(txn.plan, result)
+        except Exception:
+            self.fail_step(txn)
+            raise
+        self.commit_launch(txn, now_ns)
+        return self.resolve(result, now_ns)
+
+    def _check_result(self, plan: StepPlan, result: StepResult) -> None:
+        if result.plan_id != plan.plan_id:
+            raise RuntimeError("result plan_id does not match plan")
+        sampled = [i.request_id for i in plan.items if i.should_sample]
+        if tuple(sampled) != tuple(result.sample_request_ids):
+            raise RuntimeError("result sampling order does not match plan")
+        for token_id in result.sampled_token_ids:
+            _check_token_id(token_id)
+
+    def commit_launch(self, txn: ScheduleTxn, now_ns: int) -> None:
+        """Commit a launched step's KV writes before its tokens are known:
+        each sampled row gets a PENDING_TOKEN output that ``resolve`` fills."""
         self._require(txn, TxnState.DISPATCHED)
         try:
             self._check_now(now_ns)
             plan = txn.plan
-            if result.plan_id != plan.plan_id:
-                raise RuntimeError("result plan_id does not match plan")
-            sampled = [i.request_id for i in plan.items if i.should_sample]
-            if tuple(sampled) != tuple(result.sample_request_ids):
-                raise RuntimeError("result sampling order does not match plan")
-            for token_id in result.sampled_token_ids:
-                _check_token_id(token_id)
             txn.kv.complete_writes()
-            tokens = iter(result.sampled_token_ids)
+            sampled = []
             for item in plan.items:
                 request = self._requests[item.request_id]
                 request.computed_tokens = item.token_end
-                self._blocks.cache_full_blocks(request.request_id, request.token_slice)
+                self._publish_known(request)
                 if not item.should_sample:
                     self._prefilling.append(request.request_id)
                     continue
-                token_id = next(tokens)
-                request.output_token_ids.append(token_id)
-                if request.first_token_ns is None:
-                    request.first_token_ns = now_ns
+                sampled.append(request.request_id)
+                request.output_token_ids.append(PENDING_TOKEN)
+                self._unresolved.setdefault(request.request_id, deque()).append(
+                    (plan.plan_id, len(request.output_token_ids) - 1))
                 request.work_class = WorkClass.DECODE
-                eos = token_id in self._eos and not request.sampling.ignore_eos
-                if (eos or request.remaining_new_tokens == 0
+                if (request.remaining_new_tokens == 0
                         or request.total_tokens >= self.max_model_len):
-                    self._terminate(request, RequestStatus.FINISHED, now_ns)
+                    self._finishing.add(request.request_id)
                 else:
                     self._decoding.append(request.request_id)
+            self._launched.append((plan.plan_id, tuple(sampled)))
             if txn.rotate_prefill and plan.num_prefill_items:
                 self._prefer_waiting = not self._prefer_waiting
         except Exception:
@@ -403,6 +453,68 @@ class Scheduler:
         self._now = now_ns
         object.__setattr__(txn, "state", TxnState.COMMITTED)
         self._txn = None
+
+    def resolve(self, result: StepResult, now_ns: int) -> tuple[tuple[int, int], ...]:
+        """Fill the oldest launched step's placeholders with its sampled
+        tokens; apply EOS and pending length stops. Returns the accepted
+        (request id, token id) pairs - rows of requests that finished or
+        were cancelled meanwhile are dropped."""
+        self._healthy()
+        try:
+            self._check_now(now_ns)
+            if not self._launched:
+                raise RuntimeError("no launched step awaits tokens")
+            plan_id, sampled = self._launched[0]
+            if result.plan_id != plan_id:
+                raise RuntimeError("result plan_id does not match the oldest launched plan")
+            if tuple(result.sample_request_ids) != sampled:
+                raise RuntimeError("result sampling order does not match plan")
+            for token_id in result.sampled_token_ids:
+                _check_token_id(token_id)
+            self._launched.popleft()
+            accepted = []
+            for request_id, token_id in zip(sampled, result.sampled_token_ids):
+                request = self._requests.get(request_id)
+                slots = self._unresolved.get(request_id)
+                if request is None or request.terminal or not slots or slots[0][0] != plan_id:
+                    continue
+                index = slots.popleft()[1]
+                if not slots:
+                    del self._unresolved[request_id]
+                request.output_token_ids[index] = token_id
+                accepted.append((request_id, token_id))
+                if request.first_token_ns is None:
+                    request.first_token_ns = now_ns
+                if token_id in self._eos and not request.sampling.ignore_eos:
+                    self._stop_speculation(request, index)
+                    self._terminate(request, RequestStatus.FINISHED, now_ns)
+                elif request_id in self._finishing and request_id not in self._unresolved:
+                    self._finishing.discard(request_id)
+                    self._terminate(request, RequestStatus.FINISHED, now_ns)
+                else:
+                    self._publish_known(request)
+        except Exception:
+            self.shutdown()
+            raise
+        self._now = now_ns
+        return tuple(accepted)
+
+    def _publish_known(self, request: RequestState) -> None:
+        """Publish full blocks whose token ids are all on the host."""
+        pending = len(self._unresolved.get(request.request_id, ()))
+        self._blocks.cache_full_blocks(request.request_id, request.token_slice,
+                                       request.total_tokens - pending)
+
+    def _stop_speculation(self, request: RequestState, last: int) -> None:
+        """Drop outputs after index ``last`` (rows launched past a stop) and
+        take the request out of the decode and finishing queues."""
+        request_id = request.request_id
+        del request.output_token_ids[last + 1:]
+        self._unresolved.pop(request_id, None)
+        if request_id in self._finishing:
+            self._finishing.discard(request_id)
+        elif request_id in self._decoding:
+            self._decoding.remove(request_id)
 
     def fail_step(self, txn: ScheduleTxn) -> None:
         self._require(txn, TxnState.DISPATCHED)
@@ -424,6 +536,9 @@ class Scheduler:
         self._waiting.clear()
         self._prefilling.clear()
         self._decoding.clear()
+        self._launched.clear()
+        self._unresolved.clear()
+        self._finishing.clear()
         self._slots = [None] * self.max_active_requests
         self._txn = None
         self._commands_applied = False
@@ -536,7 +651,9 @@ class Scheduler:
         elif request.status is RequestStatus.WAITING:
             self._waiting.remove(request.request_id)
         elif request.work_class is WorkClass.DECODE:
-            self._decoding.remove(request.request_id)
+            slots = self._unresolved.get(request.request_id)
+            self._stop_speculation(request, slots[0][1] - 1 if slots
+                                   else len(request.output_token_ids) - 1)
         else:
             self._prefilling.remove(request.request_id)
         self._terminate(request, RequestStatus.ABORTED, now_ns)
