@@ -332,43 +332,23 @@ paged_decode_d128(DecodeArgs<T> a) {
     if (t_begin < t_end) {
         const int64_t table = a.offsets[r];
 
+        // Prologue loads go out together: the query, the new token's slot,
+        // then (below) the first group of block ids, ahead of the new
+        // token's K/V write - each would otherwise cost a memory round trip
+        // of its own at short contexts.
+        const int64_t new_slot = FUSED ? a.slots[row] : -1;
         // B operand: query head g = col (zero beyond the group), dims c*32 + quad*8.
         U16x8 qb[4];
         {
             const bool has = col < a.group;
             const T* qrow = a.q + row * a.qts + (h0 + (has ? col : 0)) * a.qhs + quad * 8;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                if (has) {
-                    qb[c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
-                } else {
-                    qb[c].w[0] = qb[c].w[1] = qb[c].w[2] = qb[c].w[3] = 0u;
-                }
-            }
+            for (int c = 0; c < 4; ++c) qb[c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) qb[c].w[w] = has ? qb[c].w[w] : 0u;
         }
-        if constexpr (FUSED) {
-            // The row's new token (position length - 1) is written by the
-            // wave whose page range holds it, before that wave reads it.
-            if (t_begin <= length - 1 && length - 1 < t_end) {
-                const int64_t slot = a.slots[row];
-                if (slot >= 0) {
-                    constexpr int EB = F8 ? 1 : int(sizeof(T));  // bytes per element
-                    const int64_t off = (slot * a.kv_heads + kvh) * D * EB;
-                    write_new_kv<T, F8>(a.kraw + row * a.krts + kvh * a.krhs,
-                                        a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
-                                        a.cos_t + row * 64, a.sin_t + row * 64, a.k_eps,
-                                        static_cast<char*>(a.kcache) + off,
-                                        static_cast<char*>(a.vcache) + off, a.k_inv_scale,
-                                        a.v_inv_scale, lane);
-                    // Only this wave reads the row, and no CU has it cached
-                    // (caches start clean per dispatch): a workgroup-scope
-                    // release (store completion, no cache write-back) orders
-                    // the stores before this wave's loads.
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                }
-            }
-        }
-
         // The wave's range is walked in groups of 64 * IDR pages. Lane p
         // holds the block ids of pages p, p + 64, ... of the group in
         // registers (fetched once per group; only the low word: ids < 2^32,
@@ -439,6 +419,29 @@ paged_decode_d128(DecodeArgs<T> a) {
         // last chunk of a group loads clamped (cached) rows instead of
         // branching, so the loop's wait counts never cover a skipped path.
         load_group();
+        if constexpr (FUSED) {
+            // The row's new token (position length - 1) is written by the
+            // wave whose page range holds it, before that wave reads it.
+            if (t_begin <= length - 1 && length - 1 < t_end) {
+                const int64_t slot = new_slot;
+                if (slot >= 0) {
+                    constexpr int EB = F8 ? 1 : int(sizeof(T));  // bytes per element
+                    const int64_t off = (slot * a.kv_heads + kvh) * D * EB;
+                    write_new_kv<T, F8>(a.kraw + row * a.krts + kvh * a.krhs,
+                                        a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
+                                        a.cos_t + row * 64, a.sin_t + row * 64, a.k_eps,
+                                        static_cast<char*>(a.kcache) + off,
+                                        static_cast<char*>(a.vcache) + off, a.k_inv_scale,
+                                        a.v_inv_scale, lane);
+                    // Only this wave reads the row, and no CU has it cached
+                    // (caches start clean per dispatch): a workgroup-scope
+                    // release (store completion, no cache write-back) orders
+                    // the stores before this wave's loads.
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                }
+            }
+        }
+
         {
             const uint32_t first = resolve(g_begin);
             load_k(first);

@@ -36,6 +36,19 @@ __device__ __forceinline__ void load8(const T* p, int valid, float (&v)[8]) {
     for (int i = 0; i < 8; ++i) v[i] = i < valid ? to_f<T>(p[i]) : 0.f;
 }
 
+// 16-byte vector load of 8 elements at base[c] when ok, zeros otherwise.
+// The load is unconditional (from base[0] when !ok, which must be mapped),
+// so that a thread's loads are all in flight at once: loads under a branch
+// are each waited for before the branch closes.
+template <typename T>
+__device__ __forceinline__ void load8_masked(const T* base, int c, bool ok,
+                                             float (&v)[8]) {
+    const U16x8 raw = *reinterpret_cast<const U16x8*>(base + (ok ? c : 0));
+    unpack8<T>(raw, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = ok ? v[i] : 0.f;
+}
+
 template <typename T, bool VEC>
 __device__ __forceinline__ void store8(T* p, int valid, const float (&v)[8]) {
     if constexpr (VEC && sizeof(T) == 2) {
@@ -68,24 +81,41 @@ rms_norm_kernel(const T* __restrict__ x, int64_t rows, int64_t heads, int width,
     const bool active = row < rows;
 
     const int64_t r = active ? row : 0;
-    const int64_t tok = r / heads;
+    // rows <= INT32_MAX (checked on the host): 32-bit division.
+    const int64_t tok = uint32_t(r) / uint32_t(heads);
     const T* src = x + tok * token_stride + (r - tok * heads) * head_stride;
     const T* res = RESIDUAL ? residual + tok * residual_stride : nullptr;
 
     // Weights are loaded up front so their latency overlaps the reduction.
     float v[NV][8], wv[NV][8];
     float ss = 0.f;
+    float rv[NV][8];
 #pragma unroll
     for (int n = 0; n < NV; ++n) {
         const int c = (n * TPR + t) * 8;
-        const int valid = active ? min(8, width - c) : 0;
-        load8<T, VEC>(src + c, valid, v[n]);
-        load8<T, VEC>(weight + c, valid, wv[n]);
-        if constexpr (RESIDUAL) {
-            float rv[8];
-            load8<T, VEC>(res + c, valid, rv);
+        if constexpr (VEC && sizeof(T) == 2) {  // width % 8 == 0: whole chunks
+            const bool ok = c < width;  // inactive threads read row 0
+            load8_masked<T>(src, c, ok, v[n]);
+            load8_masked<T>(weight, c, ok, wv[n]);
+            if constexpr (RESIDUAL) load8_masked<T>(res, c, ok, rv[n]);
+        } else {
+            const int valid = active ? min(8, width - c) : 0;
+            load8<T, VEC>(src + c, valid, v[n]);
+            load8<T, VEC>(weight + c, valid, wv[n]);
+            if constexpr (RESIDUAL) load8<T, VEC>(res + c, valid, rv[n]);
+        }
+    }
+    // Keep the weight loads in flight with the row's: without this the
+    // compiler sinks them past the reduction, a second memory round trip.
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[n][i] = rnd<T>(v[n][i] + rv[i]);
+    for (int n = 0; n < NV; ++n)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(wv[n][i]));
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        if constexpr (RESIDUAL) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[n][i] = rnd<T>(v[n][i] + rv[n][i]);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) ss += v[n][i] * v[n][i];
@@ -198,31 +228,64 @@ add_rms_norm_partials_kernel(const float* __restrict__ parts, int nparts,
                              T* __restrict__ residual_out, float eps) {
     const int64_t row = blockIdx.x;
     const int t = threadIdx.x;
-    float v[NV][8], wv[NV][8];
+    float v[NV][8], wv[NV][8], rv[NV][8];
+    float acc[NV][8];
     float ss = 0.f;
+    // Every load of the thread is issued before any is used (out-of-range
+    // chunks read chunk 0 and are masked).
+    constexpr int NPP = NP > 0 ? NP : 1;
+    float4 pa[NV][NPP][2];
 #pragma unroll
     for (int n = 0; n < NV; ++n) {
         const int c = (n * 256 + t) * 8;
         const bool ok = c < width;  // width % 8 == 0 (checked on the host)
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (ok) {
-            const float* src = parts + row * int64_t(width) + c;
-            const int np = NP > 0 ? NP : nparts;
+        const float* src = parts + row * int64_t(width) + (ok ? c : 0);
 #pragma unroll
-            for (int p = 0; p < (NP > 0 ? NP : 64); ++p) {
-                if (NP == 0 && p >= np) break;
+        for (int i = 0; i < 8; ++i) acc[n][i] = 0.f;
+        if constexpr (NP > 0) {
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                pa[n][p][0] = *reinterpret_cast<const float4*>(src + p * part_stride);
+                pa[n][p][1] = *reinterpret_cast<const float4*>(src + p * part_stride + 4);
+            }
+        } else {
+            for (int p = 0; p < nparts; ++p) {
                 const float4 a = *reinterpret_cast<const float4*>(src + p * part_stride);
                 const float4 b = *reinterpret_cast<const float4*>(src + p * part_stride + 4);
-                acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-                acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+                acc[n][0] += a.x; acc[n][1] += a.y; acc[n][2] += a.z; acc[n][3] += a.w;
+                acc[n][4] += b.x; acc[n][5] += b.y; acc[n][6] += b.z; acc[n][7] += b.w;
             }
         }
-        float rv[8];
-        load8<T, true>(weight + c, ok ? 8 : 0, wv[n]);
-        load8<T, true>(residual + row * residual_stride + c, ok ? 8 : 0, rv);
+        load8_masked<T>(weight, c, ok, wv[n]);
+        load8_masked<T>(residual + row * residual_stride, c, ok, rv[n]);
+    }
+    if constexpr (NP > 0) {
+        // Materialise the partials here: the compiler would otherwise move
+        // part of their loads under the chunk's range check, after the rest.
+#pragma unroll
+        for (int n = 0; n < NV; ++n)
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    asm volatile("" : "+v"(pa[n][p][h].x), "+v"(pa[n][p][h].y),
+                                 "+v"(pa[n][p][h].z), "+v"(pa[n][p][h].w));
+#pragma unroll
+        for (int n = 0; n < NV; ++n)
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                acc[n][0] += pa[n][p][0].x; acc[n][1] += pa[n][p][0].y;
+                acc[n][2] += pa[n][p][0].z; acc[n][3] += pa[n][p][0].w;
+                acc[n][4] += pa[n][p][1].x; acc[n][5] += pa[n][p][1].y;
+                acc[n][6] += pa[n][p][1].z; acc[n][7] += pa[n][p][1].w;
+            }
+    }
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const bool ok = (n * 256 + t) * 8 < width;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            v[n][i] = ok ? rnd<T>(rnd<T>(acc[i]) + rv[i]) : 0.f;
+            v[n][i] = ok ? rnd<T>(rnd<T>(acc[n][i]) + rv[n][i]) : 0.f;
             ss += v[n][i] * v[n][i];
         }
     }
@@ -246,21 +309,28 @@ add_rms_norm_partials_kernel(const float* __restrict__ parts, int nparts,
 
 // --------------------------------------------------------- SiLU * up ----
 
-template <typename T, bool VEC>
+// NARROW: rows * chunks_per_row < 2^32, so the index splits in 32 bits.
+template <typename T, bool VEC, bool NARROW>
 __global__ void __launch_bounds__(256)
 silu_mul_kernel(const T* __restrict__ x, int64_t rows, int64_t heads, int half,
                 int64_t token_stride, int64_t head_stride, T* __restrict__ out,
                 int chunks_per_row) {
     const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t row = idx / chunks_per_row;
+    const int64_t row = NARROW ? int64_t(uint32_t(idx) / uint32_t(chunks_per_row))
+                               : idx / chunks_per_row;
     if (row >= rows) return;
     const int c = int(idx - row * chunks_per_row) * 8;
     const int valid = min(8, half - c);
-    const int64_t tok = row / heads;
+    const int64_t tok = NARROW ? int64_t(uint32_t(row) / uint32_t(heads)) : row / heads;
     const T* src = x + tok * token_stride + (row - tok * heads) * head_stride;
     float g[8], u[8], y[8];
-    load8<T, VEC>(src + c, valid, g);
-    load8<T, VEC>(src + half + c, valid, u);
+    if constexpr (VEC && sizeof(T) == 2) {  // half % 8 == 0: c + 8 <= half
+        load8_masked<T>(src, c, true, g);
+        load8_masked<T>(src + half, c, true, u);
+    } else {
+        load8<T, VEC>(src + c, valid, g);
+        load8<T, VEC>(src + half + c, valid, u);
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const float act = rnd<T>(g[i] / (1.0f + expf(-g[i])));
@@ -310,12 +380,21 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
     for (int p = 0; p < NP; ++p) {
         const int d = lane + 64 * p;
         const bool ok = d < half;
-        x1[p] = ok ? to_f<T>(src[d]) : 0.f;
-        x2[p] = ok ? to_f<T>(src[d + half]) : 0.f;
-        w1[p] = ok ? to_f<T>(w[d]) : 0.f;
-        w2[p] = ok ? to_f<T>(w[d + half]) : 0.f;
-        cs[p] = ok ? to_f<T>(cos_t[tok * half + d]) : 0.f;
-        sn[p] = ok ? to_f<T>(sin_t[tok * half + d]) : 0.f;
+        const int dd = ok ? d : 0;  // unconditional loads: all in flight at once
+        const float a1 = to_f<T>(src[dd]), a2 = to_f<T>(src[dd + half]);
+        const float b1 = to_f<T>(w[dd]), b2 = to_f<T>(w[dd + half]);
+        const float c1 = to_f<T>(cos_t[tok * half + dd]);
+        const float s1 = to_f<T>(sin_t[tok * half + dd]);
+        x1[p] = ok ? a1 : 0.f;
+        x2[p] = ok ? a2 : 0.f;
+        w1[p] = ok ? b1 : 0.f;
+        w2[p] = ok ? b2 : 0.f;
+        cs[p] = ok ? c1 : 0.f;
+        sn[p] = ok ? s1 : 0.f;
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        asm volatile("" : "+v"(w1[p]), "+v"(w2[p]), "+v"(cs[p]), "+v"(sn[p]));
         ss += x1[p] * x1[p];
         ss += x2[p] * x2[p];
     }
@@ -480,14 +559,16 @@ extern "C" int tvllm_silu_and_mul(const void* input, int64_t tokens,
         const bool vec = sizeof(T) == 2 && half % 8 == 0 && token_stride % 8 == 0 &&
                          head_stride % 8 == 0 && aligned16(input) && aligned16(out);
         const int blocks = int((total + 255) / 256);
-        if (vec)
-            silu_mul_kernel<T, true><<<blocks, 256, 0, s>>>(
+        const bool narrow = int64_t(blocks) * 256 <= int64_t(UINT32_MAX);
+        auto go = [&]<bool V, bool N>() {
+            silu_mul_kernel<T, V, N><<<blocks, 256, 0, s>>>(
                 static_cast<const T*>(input), rows, heads, half, token_stride,
                 head_stride, static_cast<T*>(out), chunks);
-        else
-            silu_mul_kernel<T, false><<<blocks, 256, 0, s>>>(
-                static_cast<const T*>(input), rows, heads, half, token_stride,
-                head_stride, static_cast<T*>(out), chunks);
+        };
+        if (vec && narrow) go.template operator()<true, true>();
+        else if (vec) go.template operator()<true, false>();
+        else if (narrow) go.template operator()<false, true>();
+        else go.template operator()<false, false>();
         return launch_status("silu_and_mul");
     });
 }
