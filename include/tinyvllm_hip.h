@@ -228,7 +228,11 @@ int tvllm_argmax(const void* logits, int64_t rows, int64_t vocab,
  *   mass exceeds top_p (ties broken by lower index);
  *   out[r] = argmax_{kept i} p_i / E_i,  E_i ~ Exp(1) from a counter-based
  *   Philox4x32-10 stream keyed by (seeds[r], counters[r], i).
- * temperature > 0. workspace: tvllm_sample_workspace_size(rows, vocab).
+ * temperature > 0 samples; temperature 0 rows take the argmax.
+ * workspace (optional, 16-byte aligned): tvllm_sample_workspace_size(rows,
+ * vocab) bytes of per-span argmax partials, so that each row's scan is
+ * spread over several workgroups (an extra launch); with workspace_bytes 0
+ * each row's workgroup scans the row alone. Same result either way.
  * Replaces: TorchSampler._sample_batch (reference tinyvllm/sampling.py:75-164);
  *           the noise stream differs from torch.Generator's. */
 int64_t tvllm_sample_workspace_size(int64_t rows, int64_t vocab);

@@ -363,6 +363,43 @@ def test_sample_greedy_rows_and_degenerate_filters(device):
         assert out[r] == best[r], r
 
 
+@pytest.mark.parametrize("dtype,vocab", [(torch.bfloat16, 151936), (torch.float32, 151939),
+                                         (torch.float16, 16387)])
+def test_sample_greedy_split_scan_matches_argmax(device, dtype, vocab):
+    """Greedy rows scanned in spans over many workgroups (the workspace
+    path) agree with torch's argmax and with the one-workgroup scan: ties
+    across spans keep the lower index, a NaN anywhere wins, the last element
+    and a vocabulary tail that is not a whole vector count."""
+    from tinyvllm.kernels._extension import check, dtype_code, load_kernels, stream_of
+    from tinyvllm.kernels.sampling import sample
+
+    g = torch.Generator().manual_seed(8)
+    rows = 9
+    logits = torch.randn(rows, vocab, generator=g).to(dtype)
+    logits[1, 100] = logits[1, vocab - 30] = 40.0   # tie in different spans
+    logits[2, vocab - 1] = 50.0                     # last element (the tail)
+    logits[3, 16383] = logits[3, 16384] = 45.0      # tie across a span boundary
+    logits[4, vocab // 2] = float("nan")            # NaN in a middle span
+    logits[5, 7] = float("nan")
+    logits[5, vocab - 2] = float("nan")             # first NaN wins
+    logits[6] = 0.0                                 # all equal -> index 0
+    expect = logits.float().argmax(-1)
+    expect[4], expect[5] = vocab // 2, 7
+    zeros_f = torch.zeros(rows, device=device)
+    zeros_l = torch.zeros(rows, dtype=torch.long, device=device)
+    ones_f = torch.ones(rows, device=device)
+    dl = logits.to(device)
+    out = sample(dl, zeros_f, zeros_l, ones_f, zeros_l, zeros_l).cpu()
+    assert out.tolist() == expect.tolist()
+    single = torch.empty(rows, dtype=torch.long, device=device)
+    lib = load_kernels()
+    check(lib.tvllm_sample(dl.data_ptr(), rows, vocab, dl.stride(0), zeros_f.data_ptr(),
+                           zeros_l.data_ptr(), ones_f.data_ptr(), zeros_l.data_ptr(),
+                           zeros_l.data_ptr(), single.data_ptr(), None, 0,
+                           dtype_code(dtype), stream_of(device)))
+    assert single.cpu().tolist() == expect.tolist()
+
+
 def test_sample_stays_in_kept_set_and_follows_softmax(device):
     from oracle.sampling import kept_set
     from tinyvllm.kernels.sampling import sample

@@ -45,6 +45,22 @@ __device__ __forceinline__ void wave_argmax(float& v, int64_t& idx) {
     }
 }
 
+// Block-wide argmax over W waves; every thread gets the result.
+template <int W>
+__device__ void block_argmax_w(float& v, int64_t& idx) {
+    __shared__ float sv[W];
+    __shared__ int64_t si[W];
+    wave_argmax(v, idx);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[w] = v; si[w] = idx; }
+    __syncthreads();
+    v = sv[0];
+    idx = si[0];
+    for (int i = 1; i < W; ++i)
+        if (better(sv[i], si[i], v, idx)) { v = sv[i]; idx = si[i]; }
+    __syncthreads();
+}
+
 // Block-wide argmax; every thread gets the result.
 __device__ void block_argmax(float& v, int64_t& idx) {
     __shared__ float sv[kWaves];
@@ -223,6 +239,66 @@ __device__ __forceinline__ void thread_argmax(const T* row, int64_t vocab, float
     if constexpr (VEC) {
         const int64_t nvec = vocab / 8;
         const U16x8* rv = reinterpret_cast<const U16x8*>(row);
+        // Rows of up to kOnePass * kThreads vectors (vocabularies up to
+        // 163840): every load of the thread is issued at once - out-of-range
+        // ones read vector 0 and are skipped - so the row costs one memory
+        // round trip instead of one per loop iteration.
+        constexpr int kOnePass = 20;
+        if (nvec <= int64_t(kOnePass) * kThreads) {
+            U16x8 raw[kOnePass];
+            const uint32_t n32 = uint32_t(nvec);
+#pragma unroll
+            for (int u = 0; u < kOnePass; ++u) {  // 32-bit offsets from the row base
+                const uint32_t c = threadIdx.x + uint32_t(u) * kThreads;
+                raw[u] = rv[c < n32 ? c : 0u];
+            }
+            // Two cheap passes over the registers instead of a NaN-aware
+            // compare per element (which left the row scan VALU-bound): the
+            // maximum, then the first index holding it. A thread that saw a
+            // NaN redoes its elements with the exact compare.
+            float m = -INFINITY;
+            bool nan = false;
+#pragma unroll
+            for (int u = 0; u < kOnePass; ++u) {
+                const uint32_t c = threadIdx.x + uint32_t(u) * kThreads;
+                if (c >= n32) break;
+                float x[8];
+                unpack8<T>(raw[u], x);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    m = fmaxf(m, x[e]);
+                    nan |= x[e] != x[e];
+                }
+            }
+            if (!nan) {
+                uint32_t first = UINT32_MAX;
+#pragma unroll
+                for (int u = 0; u < kOnePass; ++u) {
+                    const uint32_t c = threadIdx.x + uint32_t(u) * kThreads;
+                    if (c >= n32) break;
+                    float x[8];
+                    unpack8<T>(raw[u], x);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        first = x[e] == m ? min(first, c * 8u + uint32_t(e)) : first;
+                }
+                if (first != UINT32_MAX) {
+                    best = m;
+                    bi = first;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < kOnePass; ++u) {
+                    const int64_t c = threadIdx.x + int64_t(u) * kThreads;
+                    if (c >= nvec) break;
+                    float x[8];
+                    unpack8<T>(raw[u], x);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (better(x[e], c * 8 + e, best, bi)) { best = x[e]; bi = c * 8 + e; }
+                }
+            }
+        } else {
         // Four independent 16-byte loads in flight per thread, then compare
         // in index order (ties keep the lower index either way).
         constexpr int U = 4;
@@ -248,6 +324,7 @@ __device__ __forceinline__ void thread_argmax(const T* row, int64_t vocab, float
             for (int e = 0; e < 8; ++e)
                 if (better(x[e], c * 8 + e, best, bi)) { best = x[e]; bi = c * 8 + e; }
         }
+        }
         tail = nvec * 8;
     }
     for (int64_t i = tail + threadIdx.x; i < vocab; i += kThreads) {
@@ -256,19 +333,103 @@ __device__ __forceinline__ void thread_argmax(const T* row, int64_t vocab, float
     }
 }
 
+// Greedy scan split over workgroups: row r's span s (kPartSpan elements)
+// is scanned by one 256-thread workgroup, 8 vectors per thread in flight at
+// once; the sampling kernel combines the spans. One 1024-thread workgroup
+// per row left the scan VALU-bound on one CU (28 us per 151936-wide row).
+constexpr int kPartThreads = 256;
+constexpr int kPartVecs = 8;
+constexpr int64_t kPartSpan = int64_t(kPartThreads) * kPartVecs * 8;
+
+struct ArgPart {
+    float v;
+    int32_t i;  // -1: empty span
+};
+
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(kPartThreads)
+argmax_part_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride, int nparts,
+                   ArgPart* __restrict__ parts) {
+    const int r = blockIdx.x / nparts;
+    const int span = blockIdx.x - r * nparts;
+    const T* row = logits + int64_t(r) * stride;
+    const int64_t begin = int64_t(span) * kPartSpan;
+    const int64_t end = min(vocab, begin + kPartSpan);
+    float best = -INFINITY;
+    int64_t bi = INT64_MAX;
+    int64_t tail = begin;
+    if constexpr (VEC) {
+        const U16x8* rv = reinterpret_cast<const U16x8*>(row);
+        const uint32_t v0 = uint32_t(begin / 8), v1 = uint32_t(end / 8);  // whole vectors
+        U16x8 raw[kPartVecs];
+#pragma unroll
+        for (int u = 0; u < kPartVecs; ++u) {
+            const uint32_t c = v0 + threadIdx.x + uint32_t(u) * kPartThreads;
+            raw[u] = rv[c < v1 ? c : v0];
+        }
+        float m = -INFINITY;
+        bool nan = false;
+#pragma unroll
+        for (int u = 0; u < kPartVecs; ++u) {
+            const uint32_t c = v0 + threadIdx.x + uint32_t(u) * kPartThreads;
+            if (c >= v1) break;
+            float x[8];
+            unpack8<T>(raw[u], x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                m = fmaxf(m, x[e]);
+                nan |= x[e] != x[e];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kPartVecs; ++u) {
+            const uint32_t c = v0 + threadIdx.x + uint32_t(u) * kPartThreads;
+            if (c >= v1) break;
+            float x[8];
+            unpack8<T>(raw[u], x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t i = int64_t(c) * 8 + e;
+                if (nan ? better(x[e], i, best, bi) : (x[e] == m && i < bi)) {
+                    best = x[e];
+                    bi = i;
+                }
+            }
+        }
+        tail = int64_t(v1) * 8;
+    }
+    for (int64_t i = tail + threadIdx.x; i < end; i += kPartThreads) {
+        const float x = load_logit(row, i);
+        if (better(x, i, best, bi)) { best = x; bi = i; }
+    }
+    block_argmax_w<kPartThreads / 64>(best, bi);
+    if (threadIdx.x == 0)
+        parts[blockIdx.x] = ArgPart{best, bi == INT64_MAX ? -1 : int32_t(bi)};
+}
+
 template <typename T, bool VEC>
 __global__ void __launch_bounds__(kThreads)
 sample_kernel(const T* __restrict__ logits, int64_t vocab, int64_t stride,
               const float* __restrict__ temperature, const int64_t* __restrict__ top_k,
               const float* __restrict__ top_p, const int64_t* __restrict__ seeds,
-              const int64_t* __restrict__ counters, int64_t* __restrict__ out) {
+              const int64_t* __restrict__ counters, int64_t* __restrict__ out,
+              const ArgPart* __restrict__ parts, int nparts) {
     const int r = blockIdx.x;
     const T* row = logits + int64_t(r) * stride;
 
-    // Row max (also the greedy answer).
+    // Row max (also the greedy answer): from the per-span partials of
+    // argmax_part_kernel when given, else scanned here.
     float best = -INFINITY;
     int64_t bi = INT64_MAX;
-    thread_argmax<T, VEC>(row, vocab, best, bi);
+    if (parts != nullptr) {
+        for (int i = threadIdx.x; i < nparts; i += kThreads) {
+            const ArgPart p = parts[int64_t(r) * nparts + i];
+            const int64_t pi = p.i < 0 ? INT64_MAX : int64_t(p.i);
+            if (better(p.v, pi, best, bi)) { best = p.v; bi = pi; }
+        }
+    } else {
+        thread_argmax<T, VEC>(row, vocab, best, bi);
+    }
     block_argmax(best, bi);
     const float temp = temperature[r];
     if (!(temp > 0.f)) {
@@ -374,9 +535,9 @@ extern "C" int tvllm_argmax(const void* logits, int64_t rows, int64_t vocab,
 }
 
 extern "C" int64_t tvllm_sample_workspace_size(int64_t rows, int64_t vocab) {
-    (void)rows;
-    (void)vocab;
-    return 0;  // single-pass-per-row design: no cross-workgroup partials
+    // One (value, index) partial per kPartSpan-wide span of each row.
+    if (rows <= 0 || vocab <= 0) return 0;
+    return rows * ((vocab + kPartSpan - 1) / kPartSpan) * int64_t(sizeof(ArgPart));
 }
 
 extern "C" int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
@@ -385,8 +546,6 @@ extern "C" int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
                             const int64_t* seeds, const int64_t* counters,
                             int64_t* out, void* workspace, int64_t workspace_bytes,
                             int dtype, tvllm_stream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     TVLLM_CHECK(rows >= 0 && vocab > 0 && row_stride >= vocab,
                 "sample: invalid logits geometry");
     TVLLM_CHECK(vocab < (int64_t(1) << 24), "sample: vocab must be < 2^24");
@@ -394,22 +553,35 @@ extern "C" int tvllm_sample(const void* logits, int64_t rows, int64_t vocab,
     if (rows == 0) return TVLLM_OK;
     TVLLM_CHECK(logits && temperature && top_k && top_p && seeds && counters && out,
                 "sample: null pointer");
+    TVLLM_CHECK(workspace_bytes >= 0 && (workspace_bytes == 0 || workspace != nullptr),
+                "sample: null workspace");
     hipStream_t s = as_hip(stream);
+    // With a workspace of tvllm_sample_workspace_size bytes the row scan is
+    // split over spans (argmax_part_kernel); without one each row's
+    // workgroup scans it alone.
+    const int64_t nparts = (vocab + kPartSpan - 1) / kPartSpan;
+    const bool split = workspace_bytes >= tvllm_sample_workspace_size(rows, vocab) &&
+                       aligned16(workspace) && rows * nparts <= INT32_MAX;
+    ArgPart* parts = split ? static_cast<ArgPart*>(workspace) : nullptr;
     return dispatch_float(dtype, [&]<int DT>() {
         using T = typename Elem<DT>::T;
         const bool vec = sizeof(T) == 2 && row_stride % 8 == 0 && aligned16(logits);
-        if constexpr (sizeof(T) == 2) {
-            if (vec) {
-                sample_kernel<T, true><<<int(rows), kThreads, 0, s>>>(
-                    static_cast<const T*>(logits), vocab, row_stride, temperature, top_k,
-                    top_p, seeds, counters, out);
-                return launch_status("sample");
+        auto go = [&]<bool V>() {
+            if (split) {
+                argmax_part_kernel<T, V><<<int(rows * nparts), kPartThreads, 0, s>>>(
+                    static_cast<const T*>(logits), vocab, row_stride, int(nparts), parts);
+                const int status = launch_status("sample");
+                if (status != TVLLM_OK) return status;
             }
+            sample_kernel<T, V><<<int(rows), kThreads, 0, s>>>(
+                static_cast<const T*>(logits), vocab, row_stride, temperature, top_k,
+                top_p, seeds, counters, out, parts, int(nparts));
+            return launch_status("sample");
+        };
+        if constexpr (sizeof(T) == 2) {
+            if (vec) return go.template operator()<true>();
         }
-        sample_kernel<T, false><<<int(rows), kThreads, 0, s>>>(
-            static_cast<const T*>(logits), vocab, row_stride, temperature, top_k,
-            top_p, seeds, counters, out);
-        return launch_status("sample");
+        return go.template operator()<false>();
     });
 }
 

@@ -62,10 +62,15 @@ def sample(
     if out is None:
         out = torch.empty(rows, dtype=torch.long, device=device)
     if rows:
+        # Per-span argmax partials: the row scan is spread over many
+        # workgroups (an allocation from torch's pool, graph-capturable).
+        size = lib.tvllm_sample_workspace_size(rows, vocab)
+        workspace = torch.empty(size, dtype=torch.uint8, device=device) if size else None
         check(lib.tvllm_sample(
             logits.data_ptr(), rows, vocab, logits.stride(0), temperature.data_ptr(),
             top_k.data_ptr(), top_p.data_ptr(), seeds.data_ptr(), counters.data_ptr(),
-            out.data_ptr(), None, 0, dtype_code(logits.dtype), stream_of(device),
+            out.data_ptr(), None if workspace is None else workspace.data_ptr(), size,
+            dtype_code(logits.dtype), stream_of(device),
         ))
     return out
 
