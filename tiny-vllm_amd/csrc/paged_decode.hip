@@ -105,12 +105,11 @@ __device__ __forceinline__ uint32_t shfl_u32(uint32_t v, int src) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// V rows are streamed exactly once per step and each load instruction covers
-// whole rows (16 lanes x 16 bytes): non-temporal loads measure ~13% more read
-// bandwidth on MI355X for such streams (7.1 vs 6.3 TB/s). K loads touch each
-// 128-byte line from two instructions (the MFMA operand layout), so they stay
-// ordinary loads: made non-temporal, the fused 8B bs64 ctx2048 launch measured
-// 93.9 us against 89.4 us.
+// K and V rows are streamed exactly once per step and each load instruction
+// covers whole 128-byte lines: non-temporal loads measure ~13% more read
+// bandwidth on MI355X for such streams (7.1 vs 6.3 TB/s). (FP8 K rows are
+// loaded in the MFMA operand layout, each line by four instructions, and
+// stay ordinary loads: a non-temporal first touch would refetch the line.)
 __device__ __forceinline__ U16x8 load_stream(const U16x8* p) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -393,15 +392,55 @@ paged_decode_d128(DecodeArgs<T> a) {
         auto load_k = [&](uint32_t my_row) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
-                const uint32_t kr = shfl_u32(my_row, 16 * j + col);
-                const Unit* kp = kc + kr + quad;
+                if constexpr (F8) {
+                    const uint32_t kr = shfl_u32(my_row, 16 * j + col);
+                    const Unit* kp = kc + kr + quad;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) kreg[j][c] = kp[c * 4];
+                    for (int c = 0; c < 4; ++c) kreg[j][c] = kp[c * 4];
+                } else {
+                    // Whole 128-byte lines per instruction: kreg[j][2l]
+                    // holds line l of tokens 16j + (col & 7), kreg[j][2l+1]
+                    // line l of tokens 16j + 8 + (col & 7); lane (col, quad)
+                    // loads 16-byte unit (col >> 3) * 4 + quad of the line.
+                    const uint32_t lo = shfl_u32(my_row, 16 * j + (col & 7));
+                    const uint32_t hi = shfl_u32(my_row, 16 * j + 8 + (col & 7));
+                    const uint32_t u = uint32_t((col >> 3) * 4 + quad);
+#pragma unroll
+                    for (int l = 0; l < 2; ++l) {
+                        kreg[j][2 * l] = load_stream(kc + lo + 8 * l + u);
+                        kreg[j][2 * l + 1] = load_stream(kc + hi + 8 * l + u);
+                    }
+                }
             }
         };
+        // MFMA A operand of k-step c: lane (col, quad) = token 16j + col,
+        // 16-byte unit 4c + quad. From the line loads: k-step 2l takes
+        // kreg[j][2l] in lanes col < 8 and kreg[j][2l+1] rotated by 8 lanes
+        // in lanes col >= 8; k-step 2l+1 the other way round (one DPP row
+        // rotation and one select per word).
         auto k_operand = [&](int j, int c) -> U16x8 {
-            if constexpr (F8) return fp8x8_widen<T>(kreg[j][c]);
-            else return kreg[j][c];
+            if constexpr (F8) {
+                return fp8x8_widen<T>(kreg[j][c]);
+            } else {
+                const int l = c >> 1;
+                const bool low = col < 8;
+                const U16x8& x = kreg[j][2 * l];
+                const U16x8& y = kreg[j][2 * l + 1];
+                U16x8 o;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    if ((c & 1) == 0) {
+                        const uint32_t yr = uint32_t(__builtin_amdgcn_update_dpp(
+                            0, int(y.w[w]), 0x128, 0xf, 0xf, false));  // row_ror:8
+                        o.w[w] = low ? x.w[w] : yr;
+                    } else {
+                        const uint32_t xr = uint32_t(__builtin_amdgcn_update_dpp(
+                            0, int(x.w[w]), 0x128, 0xf, 0xf, false));
+                        o.w[w] = low ? xr : y.w[w];
+                    }
+                }
+                return o;
+            }
         };
         auto load_v = [&](uint32_t my_row) {
 #pragma unroll
