@@ -226,27 +226,45 @@ __device__ __forceinline__ void rope_query(U16x8 (&qb)[4], const T* __restrict__
 // with the V row into the cache slot.
 // FP8 cache (F8): the rounded K element and the V element are quantised
 // with the cache's inverse scales, as the standalone kernels do.
-template <typename T, bool F8>
-__device__ __forceinline__ void write_new_kv(const T* __restrict__ k, const T* __restrict__ v,
+// The new K/V row's inputs for lane l: the raw K pair (l, l + 64), its
+// norm weights and RoPE angle, and the raw V pair. Loaded by every wave in
+// the kernel prologue (a few cached words), so that the wave that writes the
+// row does not add a memory round trip of its own.
+template <typename T>
+struct NewKV {
+    float x1, x2, w1, w2, c, s;
+    T v1, v2;  // copied bit for bit (16-bit caches)
+};
+
+template <typename T>
+__device__ __forceinline__ NewKV<T> load_new_kv(const T* __restrict__ k, const T* __restrict__ v,
                                              const T* __restrict__ w, const T* __restrict__ cs,
-                                             const T* __restrict__ sn, float eps,
+                                             const T* __restrict__ sn, int lane) {
+    return NewKV<T>{to_f<T>(k[lane]), to_f<T>(k[lane + 64]), to_f<T>(w[lane]),
+                    to_f<T>(w[lane + 64]), to_f<T>(cs[lane]),  to_f<T>(sn[lane]),
+                    v[lane], v[lane + 64]};
+}
+
+// New K row: normalised and rotated exactly as the standalone kernel does
+// (lane l owns the pair (l, l + 64), one wave-wide sum of squares), written
+// with the V row into the cache slot.
+// FP8 cache (F8): the rounded K element and the V element are quantised
+// with the cache's inverse scales, as the standalone kernels do.
+template <typename T, bool F8>
+__device__ __forceinline__ void write_new_kv(const NewKV<T>& in, float eps,
                                              void* __restrict__ kdst, void* __restrict__ vdst,
                                              float k_inv, float v_inv, int lane) {
-    const float x1 = to_f<T>(k[lane]), x2 = to_f<T>(k[lane + 64]);
-    const float w1 = to_f<T>(w[lane]), w2 = to_f<T>(w[lane + 64]);
-    const float c = to_f<T>(cs[lane]), s = to_f<T>(sn[lane]);
-    const float ss = wave_sum(x1 * x1 + x2 * x2);
+    const float ss = wave_sum(in.x1 * in.x1 + in.x2 * in.x2);
     const float inv = rsqrtf(ss * (1.0f / 128.f) + eps);
-    const float n1 = rnd<T>(rnd<T>(x1 * inv) * w1);
-    const float n2 = rnd<T>(rnd<T>(x2 * inv) * w2);
-    const float o1 = rnd<T>(rnd<T>(n1 * c) - rnd<T>(n2 * s));
-    const float o2 = rnd<T>(rnd<T>(n2 * c) + rnd<T>(n1 * s));
+    const float n1 = rnd<T>(rnd<T>(in.x1 * inv) * in.w1);
+    const float n2 = rnd<T>(rnd<T>(in.x2 * inv) * in.w2);
+    const float o1 = rnd<T>(rnd<T>(n1 * in.c) - rnd<T>(n2 * in.s));
+    const float o2 = rnd<T>(rnd<T>(n2 * in.c) + rnd<T>(n1 * in.s));
     if constexpr (F8) {
         uint8_t* kd = static_cast<uint8_t*>(kdst);
         uint8_t* vd = static_cast<uint8_t*>(vdst);
         const uint32_t kq = fp8x4_pack(o1 * k_inv, o2 * k_inv, 0.f, 0.f);
-        const uint32_t vq = fp8x4_pack(to_f<T>(v[lane]) * v_inv, to_f<T>(v[lane + 64]) * v_inv,
-                                       0.f, 0.f);
+        const uint32_t vq = fp8x4_pack(to_f<T>(in.v1) * v_inv, to_f<T>(in.v2) * v_inv, 0.f, 0.f);
         kd[lane] = uint8_t(kq);
         kd[lane + 64] = uint8_t(kq >> 8);
         vd[lane] = uint8_t(vq);
@@ -256,8 +274,8 @@ __device__ __forceinline__ void write_new_kv(const T* __restrict__ k, const T* _
         T* vd = static_cast<T*>(vdst);
         kd[lane] = static_cast<T>(o1);
         kd[lane + 64] = static_cast<T>(o2);
-        vd[lane] = v[lane];
-        vd[lane + 64] = v[lane + 64];
+        vd[lane] = in.v1;
+        vd[lane + 64] = in.v2;
     }
 }
 
@@ -336,6 +354,11 @@ paged_decode_d128(DecodeArgs<T> a) {
         // token's K/V write - each would otherwise cost a memory round trip
         // of its own at short contexts.
         const int64_t new_slot = FUSED ? a.slots[row] : -1;
+        NewKV<T> new_kv{};
+        if constexpr (FUSED)
+            new_kv = load_new_kv<T>(a.kraw + row * a.krts + kvh * a.krhs,
+                                    a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
+                                    a.cos_t + row * 64, a.sin_t + row * 64, lane);
         // B operand: query head g = col (zero beyond the group), dims c*32 + quad*8.
         U16x8 qb[4];
         {
@@ -459,6 +482,11 @@ paged_decode_d128(DecodeArgs<T> a) {
         // branching, so the loop's wait counts never cover a skipped path.
         load_group();
         if constexpr (FUSED) {
+            // Keep the new row's loads here, in flight with the query and the
+            // block ids (the compiler would sink them into the writer's branch).
+            asm volatile("" : "+v"(new_kv.x1), "+v"(new_kv.x2), "+v"(new_kv.w1), "+v"(new_kv.w2),
+                         "+v"(new_kv.c), "+v"(new_kv.s));
+            asm volatile("" : "+v"(new_kv.v1), "+v"(new_kv.v2));
             // The row's new token (position length - 1) is written by the
             // wave whose page range holds it, before that wave reads it.
             if (t_begin <= length - 1 && length - 1 < t_end) {
@@ -466,9 +494,7 @@ paged_decode_d128(DecodeArgs<T> a) {
                 if (slot >= 0) {
                     constexpr int EB = F8 ? 1 : int(sizeof(T));  // bytes per element
                     const int64_t off = (slot * a.kv_heads + kvh) * D * EB;
-                    write_new_kv<T, F8>(a.kraw + row * a.krts + kvh * a.krhs,
-                                        a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
-                                        a.cos_t + row * 64, a.sin_t + row * 64, a.k_eps,
+                    write_new_kv<T, F8>(new_kv, a.k_eps,
                                         static_cast<char*>(a.kcache) + off,
                                         static_cast<char*>(a.vcache) + off, a.k_inv_scale,
                                         a.v_inv_scale, lane);
