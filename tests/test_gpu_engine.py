@@ -148,10 +148,17 @@ def test_engine_pipelined_eos_stops_early_and_frees_blocks(device):
                          for p in prompts])
     free.close()
     eos = ref[0].output_token_ids[3]
+    serial = _engine(model, eos_token_ids=[eos], pipelined=False)
+    expect = serial.generate([GenerateRequest(p, SamplingParams(max_new_tokens=12))
+                              for p in prompts])
+    serial.close()
     engine = _engine(model, eos_token_ids=[eos])
     assert engine._pipelined
     outs = engine.generate([GenerateRequest(p, SamplingParams(max_new_tokens=12))
                             for p in prompts])
+    # Same kernels, same tokens: pipelining changes when ids reach the host,
+    # not which ids are sampled (one extra row per stopped request aside).
+    assert [o.output_token_ids for o in outs] == [o.output_token_ids for o in expect]
     agree = total = 0
     for prompt, out in zip(prompts, outs):
         toks = list(out.output_token_ids)

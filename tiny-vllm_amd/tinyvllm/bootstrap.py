@@ -45,8 +45,10 @@ def build_engine(model, *, max_model_len: int, max_num_seqs: int = 64,
                  attention_backend: str = "hip", enforce_eager: bool = False,
                  enable_prefix_caching: bool = True, eos_token_ids=None,
                  graph_sizes=None, clock=None, kv_cache_dtype: torch.dtype | None = None,
-                 kv_scales: tuple[float, float] = (1.0, 1.0)) -> "Engine":
-    """Engine around an already built model (random-init benchmarks, tests)."""
+                 kv_scales: tuple[float, float] = (1.0, 1.0),
+                 pipelined: bool | None = None) -> "Engine":
+    """Engine around an already built model (random-init benchmarks, tests).
+    ``pipelined=False`` runs one step at a time (the reference's loop)."""
     from tinyvllm.engine import Engine
     from tinyvllm.executor import Executor
     from tinyvllm.scheduler import Scheduler
@@ -64,7 +66,7 @@ def build_engine(model, *, max_model_len: int, max_num_seqs: int = 64,
         kv_num_blocks=num_blocks, eos_token_ids=eos_token_ids,
         enable_prefix_caching=enable_prefix_caching)
     kwargs = {} if clock is None else {"clock": clock}
-    return Engine(scheduler, executor, **kwargs)
+    return Engine(scheduler, executor, pipelined=pipelined, **kwargs)
 
 
 def create_engine(config: EngineConfig) -> "Engine":
