@@ -107,9 +107,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // K and V rows are streamed exactly once per step and each load instruction
 // covers whole 128-byte lines: non-temporal loads measure ~13% more read
-// bandwidth on MI355X for such streams (7.1 vs 6.3 TB/s). (FP8 K rows are
-// loaded in the MFMA operand layout, each line by four instructions, and
-// stay ordinary loads: a non-temporal first touch would refetch the line.)
+// bandwidth on MI355X for such streams (7.1 vs 6.3 TB/s).
 __device__ __forceinline__ U16x8 load_stream(const U16x8* p) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -416,10 +414,21 @@ paged_decode_d128(DecodeArgs<T> a) {
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
                 if constexpr (F8) {
-                    const uint32_t kr = shfl_u32(my_row, 16 * j + col);
-                    const Unit* kp = kc + kr + quad;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) kreg[j][c] = kp[c * 4];
+                    // Whole 128-byte rows per instruction (8 tokens each):
+                    // lane (col, quad) loads 16-byte chunk 2c + (quad >> 1),
+                    // c = 2 (col >> 3) + (quad & 1), of token 16j + (col & 7)
+                    // (kreg[j][0..1]) and of token 16j + 8 + (col & 7)
+                    // (kreg[j][2..3]). A chunk is k-step c of quads
+                    // 2 (quad >> 1) (low half) and 2 (quad >> 1) + 1 (high).
+                    const uint32_t lo = shfl_u32(my_row, 16 * j + (col & 7));
+                    const uint32_t hi = shfl_u32(my_row, 16 * j + 8 + (col & 7));
+                    const uint32_t m = uint32_t(2 * (2 * (col >> 3) + (quad & 1)) + (quad >> 1));
+                    const U16x8 x = load_stream(reinterpret_cast<const U16x8*>(kc + lo + 2 * m));
+                    const U16x8 y = load_stream(reinterpret_cast<const U16x8*>(kc + hi + 2 * m));
+                    kreg[j][0] = make_uint2(x.w[0], x.w[1]);
+                    kreg[j][1] = make_uint2(x.w[2], x.w[3]);
+                    kreg[j][2] = make_uint2(y.w[0], y.w[1]);
+                    kreg[j][3] = make_uint2(y.w[2], y.w[3]);
                 } else {
                     // Whole 128-byte lines per instruction: kreg[j][2l]
                     // holds line l of tokens 16j + (col & 7), kreg[j][2l+1]
@@ -441,9 +450,37 @@ paged_decode_d128(DecodeArgs<T> a) {
         // kreg[j][2l] in lanes col < 8 and kreg[j][2l+1] rotated by 8 lanes
         // in lanes col >= 8; k-step 2l+1 the other way round (one DPP row
         // rotation and one select per word).
+        // FP8: after the loads of tile j arrive, swap the high halves of even
+        // quads with the low halves of odd quads (permlane16 swap), so that
+        // kreg[j][0] / [1] hold k-steps 2 (col >> 3) and 2 (col >> 3) + 1 of
+        // token 16j + (col & 7) for the lane's own quad ([2] / [3]: token
+        // 16j + 8 + (col & 7)).
+        auto swap_f8 = [&](int j) {
+            if constexpr (F8) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    auto a0 = __builtin_amdgcn_permlane16_swap(kreg[j][2 * h].x,
+                                                               kreg[j][2 * h + 1].x, false, false);
+                    auto a1 = __builtin_amdgcn_permlane16_swap(kreg[j][2 * h].y,
+                                                               kreg[j][2 * h + 1].y, false, false);
+                    kreg[j][2 * h] = make_uint2(a0[0], a1[0]);
+                    kreg[j][2 * h + 1] = make_uint2(a0[1], a1[1]);
+                }
+            }
+        };
         auto k_operand = [&](int j, int c) -> U16x8 {
             if constexpr (F8) {
-                return fp8x8_widen<T>(kreg[j][c]);
+                // k-steps 0, 1: lanes col < 8 hold them for tokens 0-7, lanes
+                // col >= 8 take tokens 8-15 from 8 lanes away; k-steps 2, 3
+                // the other way round.
+                const bool low = col < 8;
+                const uint2 own = kreg[j][c];
+                const uint2 other = c < 2 ? kreg[j][c + 2] : kreg[j][c - 2];
+                const uint2 rot = make_uint2(
+                    uint32_t(__builtin_amdgcn_update_dpp(0, int(other.x), 0x128, 0xf, 0xf, false)),
+                    uint32_t(__builtin_amdgcn_update_dpp(0, int(other.y), 0x128, 0xf, 0xf, false)));
+                const uint2 v = (c < 2) == low ? own : rot;
+                return fp8x8_widen<T>(v);
             } else {
                 const int l = c >> 1;
                 const bool low = col < 8;
@@ -543,6 +580,7 @@ paged_decode_d128(DecodeArgs<T> a) {
                 float s[NT][4];
 #pragma unroll
                 for (int j = 0; j < NT; ++j) {
+                    swap_f8(j);
                     f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int c = 0; c < 4; ++c) d = mfma16x16x32<T>(k_operand(j, c), qb[c], d);
