@@ -665,7 +665,7 @@ E2E = {
 
 
 def end_to_end(name: str, args) -> None:
-    """A SURVEY end-to-end configuration through the full engine (scheduler,
+    """One of the benchmark end-to-end configurations through the full engine (scheduler,
     chunked prefill, prefix cache, graph-replayed decode): random-init
     weights, random token-id prompts, greedy, output tokens per second."""
     import numpy as np
@@ -852,7 +852,7 @@ def main() -> None:
                     help="decode workload: KV cache in the model dtype (the metric's "
                          "configuration) or the optional FP8 E4M3 layout")
     ap.add_argument("--workload", choices=["decode", *E2E, *OPS], default="decode",
-                    help="decode (the metric) or an end-to-end SURVEY config")
+                    help="decode (the metric), an op benchmark (c1, c2, prefill) or an end-to-end configuration (c3, c4, c5, published)")
     ap.add_argument("--eager", action="store_true",
                     help="op workloads: launch kernels directly instead of graph replay")
     ap.add_argument("--kernel-only", action="store_true",
