@@ -62,6 +62,26 @@ def test_argument_errors_surface_without_touching_a_gpu():
         check(status)
 
 
+def test_resolve_tokens_and_sample_workspace_contracts():
+    """Host-side contracts of the pipelined-input and sampling entry points
+    (no launch: errors and zero-sized calls only)."""
+    from tinyvllm.kernels._extension import check, load_kernels
+
+    lib = load_kernels()
+    status = lib.tvllm_resolve_tokens(None, None, None, -1, 0, None)
+    with pytest.raises(RuntimeError, match="negative size"):
+        check(status)
+    assert lib.tvllm_resolve_tokens(None, None, None, 0, 0, None) == 0
+    # One 8-byte (value, index) partial per 16384-wide span of each row.
+    assert lib.tvllm_sample_workspace_size(64, 151936) == 64 * 10 * 8
+    assert lib.tvllm_sample_workspace_size(3, 16384) == 3 * 1 * 8
+    assert lib.tvllm_sample_workspace_size(0, 151936) == 0
+    status = lib.tvllm_sample(None, 1, 100, 100, None, None, None, None, None, None,
+                              None, 64, 0, None)
+    with pytest.raises(RuntimeError):
+        check(status)
+
+
 def test_decode_workspace_sizes():
     """Splits inside one workgroup merge in LDS (no workspace); only long
     contexts over few rows also split across workgroups and need HBM
