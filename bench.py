@@ -197,11 +197,11 @@ def attention_roofline(executor, workload, cfg, iters: int = 30,
             "avg_launch_us": round(seconds * 1e6, 2), "bytes_per_launch": algorithmic}
 
 
-def cpu_baseline(cfg, batch: int, context: int, reps: int = 2) -> dict:
+def cpu_baseline(cfg, batch: int, context: int, reps: int = 15) -> dict:
     """The oracle's decode step on the host cores: one decoder layer at full
     batch and context (GEMMs + paged gather + fp32 softmax attention + the
-    pointwise chain), timed `reps` times, extrapolated to all layers plus
-    the LM head."""
+    pointwise chain), timed `reps` times (median; ~10 s of host work at the
+    8B shape), extrapolated to all layers plus the LM head (median of 3)."""
     import torch
 
     from oracle import attention as OA
@@ -257,9 +257,12 @@ def cpu_baseline(cfg, batch: int, context: int, reps: int = 2) -> dict:
         times.append(time.perf_counter() - t0)
     per_layer = sorted(times)[len(times) // 2]
     w_head = mat(cfg.vocab_size, h)
-    t0 = time.perf_counter()
-    OM.linear(x, w_head).float().argmax(-1)
-    head = time.perf_counter() - t0
+    heads = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        OM.linear(x, w_head).float().argmax(-1)
+        heads.append(time.perf_counter() - t0)
+    head = sorted(heads)[1]
     step = per_layer * cfg.num_hidden_layers + head
     return {"value": round(batch / step, 3), "unit": "tok/s", "cores": threads,
             "kind": "port",
