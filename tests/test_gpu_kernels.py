@@ -574,3 +574,51 @@ def test_decode_shared_prefix_pages_long_context(device):
     out, expect = _run_decode(case, device, max_context_len=32768)
     assert_bf16_close(out, expect)
     assert torch.equal(out[1].view(torch.int16), out[5].view(torch.int16))
+
+
+
+def test_decode_split_merge_reuses_its_workspace(device):
+    """Workgroup-level splits write partials to the workspace and a second
+    kernel merges them. Repeated calls on one workspace (eager and in a
+    replayed graph) give identical outputs, equal to the oracle's."""
+    from tinyvllm.kernels.paged_decode import decode_workspace_bytes, paged_decode_attention
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    lengths = [1000, 3, 0, 777]
+    pool = sum(-(-n // 16) for n in lengths) + 8
+    case = paged_decode_case(seed=91, batch=4, heads=16, kv_heads=8, pool_blocks=pool,
+                             lengths=lengths)
+    need = decode_workspace_bytes(4, 16, 8, 128, 1024, case["block_size"])
+    assert need > 0  # this shape splits over workgroups
+    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    cache = _Cache(case["k"].to(device), case["v"].to(device), case["block_size"])
+    meta = SingleQueryMetadata(case["rows"].to(device), case["blocks"].to(device),
+                               case["offsets"].to(device), case["lengths"].to(device), 1024)
+    q = case["q"].to(device)
+    outs = []
+    for _ in range(3):
+        out = torch.full_like(q, 7.0)
+        paged_decode_attention(q, cache, 0, meta, out, scale=case["scale"], workspace=ws)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    expect = torch.full_like(case["q"], 7.0)
+    OA.decode_attention(case["q"], case["k"], case["v"], case["rows"], case["blocks"],
+                        case["offsets"], case["lengths"], case["block_size"], case["scale"],
+                        expect)
+    assert_bf16_close(outs[0], expect)
+    assert all(torch.equal(o, outs[0]) for o in outs[1:])
+    graph_out = torch.full_like(q, 7.0)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        paged_decode_attention(q, cache, 0, meta, graph_out, scale=case["scale"], workspace=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_decode_attention(q, cache, 0, meta, graph_out, scale=case["scale"], workspace=ws)
+    for _ in range(3):
+        graph_out.fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(graph_out.cpu(), outs[0])
