@@ -70,3 +70,50 @@ def test_wrong_slots_and_positions_are_rejected():
     bad = dataclasses.replace(b, input_ids=(7, 100))
     with pytest.raises(ValueError, match="vocabulary"):
         _runner()._validate(bad, _Cache)
+
+
+def test_token_sources_must_name_rows_of_the_previous_step():
+    b = _batch([[3, 9], [4, 10]], befores=[6, 5], qlens=[1, 2])
+    r = _runner()
+    r._prev_count = 2
+    r._validate(dataclasses.replace(b, input_token_sources=(1, 0, -1)), _Cache)
+    for sources, message in (((2, -1, -1), "previous step"), ((0, -2, -1), "previous step"),
+                             ((0, 1), "one entry per token")):
+        with pytest.raises(ValueError, match=message):
+            r._validate(dataclasses.replace(b, input_token_sources=sources), _Cache)
+    r._prev_count = 0  # nothing launched before: no source is valid
+    with pytest.raises(ValueError, match="previous step"):
+        r._validate(dataclasses.replace(b, input_token_sources=(0, -1, -1)), _Cache)
+
+
+def test_batch_builder_turns_pending_tokens_into_sources():
+    """A decode row whose newest token is still a placeholder gets input id 0
+    and a source naming its row among the previous step's samples; prompt
+    tokens keep source -1; a placeholder without a known row is an error."""
+    from tinyvllm.batch import BatchBuilder, StepPlan, WorkItem
+    from tinyvllm.request import RequestState, WorkClass
+    from tinyvllm.scheduler import PENDING_TOKEN
+
+    class _KV:
+        plan_id, request_ids, block_size, num_blocks = 5, (1, 2), 4, 32
+
+        def append_metadata(self, rid, start, count):
+            table = np.array([3, 9] if rid == 1 else [4], dtype=np.int64)
+            pos = np.arange(start, start + count)
+            return table, table[pos // 4] * 4 + pos % 4
+
+    dec = RequestState(request_id=1, submit_seq=0, prompt_token_ids=[11, 12, 13, 14, 15],
+                       sampling=SamplingParams(), arrival_ns=0,
+                       output_token_ids=[21])
+    dec.output_token_ids.append(PENDING_TOKEN)  # sampled by the launched step, row 3
+    pre = RequestState(request_id=2, submit_seq=1, prompt_token_ids=[31, 32, 33],
+                       sampling=SamplingParams(), arrival_ns=0)
+    plan = StepPlan(plan_id=5, items=(
+        WorkItem(1, 0, WorkClass.DECODE, 6, 1, 6, True),
+        WorkItem(2, 1, WorkClass.PREFILL, 0, 3, 0, True)))
+    batch = BatchBuilder(max_model_len=64).prepare(plan, (dec, pre), kv=_KV(),
+                                                   pending_rows={1: 3})
+    assert batch.input_ids == (0, 31, 32, 33)
+    assert batch.input_token_sources == (3, -1, -1, -1)
+    with pytest.raises(ValueError, match="pending sample row"):
+        BatchBuilder(max_model_len=64).prepare(plan, (dec, pre), kv=_KV())
