@@ -31,12 +31,13 @@ async def collect(stream):
     return tokens, done
 
 
-def test_async_engine_concurrent_streams_match_the_model():
+@pytest.mark.parametrize("pipelined", [False, True], ids=["serial", "pipelined"])
+def test_async_engine_concurrent_streams_match_the_model(pipelined):
     prompts = [[11 + i] * (3 + 5 * i) for i in range(5)]
     params = SamplingParams(max_new_tokens=9, ignore_eos=True)
 
     async def main():
-        async with AsyncEngine(factory()) as bridge:
+        async with AsyncEngine(factory(pipelined=pipelined)) as bridge:
             streams = [await bridge.submit(p, params) for p in prompts]
             return await asyncio.gather(*(collect(s) for s in streams))
 
@@ -45,11 +46,12 @@ def test_async_engine_concurrent_streams_match_the_model():
         assert tokens == list(done.output_token_ids) == expected(prompt, params, 96)
 
 
-def test_async_engine_cancel_overload_and_rejection():
+@pytest.mark.parametrize("pipelined", [False, True], ids=["serial", "pipelined"])
+def test_async_engine_cancel_overload_and_rejection(pipelined):
     params = SamplingParams(max_new_tokens=60, ignore_eos=True)
 
     async def main():
-        async with AsyncEngine(factory(), max_requests=2) as bridge:
+        async with AsyncEngine(factory(pipelined=pipelined), max_requests=2) as bridge:
             a = await bridge.submit([7] * 5, params)
             b = await bridge.submit([8] * 5, params)
             with pytest.raises(OverloadedError):
@@ -111,14 +113,15 @@ def test_async_engine_factory_error_surfaces_on_enter():
     run(main())
 
 
-def test_async_llm_streams_deltas_then_output():
+@pytest.mark.parametrize("pipelined", [False, True], ids=["serial", "pipelined"])
+def test_async_llm_streams_deltas_then_output(pipelined):
     from tinyvllm.serving.async_llm import AsyncLLM, TextDelta
     from tinyvllm.serving.llm import TextOutput
 
     params = SamplingParams(max_new_tokens=5, ignore_eos=True)
 
     async def main():
-        async with AsyncLLM(engine_factory=factory()) as llm:
+        async with AsyncLLM(engine_factory=factory(pipelined=pipelined)) as llm:
             items = [x async for x in llm.stream_token_ids([20, 21, 22], params)]
             out = await llm.generate_token_ids([23, 24], params)
             return items, out
