@@ -72,9 +72,9 @@ def test_resolve_tokens_and_sample_workspace_contracts():
     with pytest.raises(RuntimeError, match="negative size"):
         check(status)
     assert lib.tvllm_resolve_tokens(None, None, None, 0, 0, None) == 0
-    # One 8-byte (value, index) partial per 16384-wide span of each row.
-    assert lib.tvllm_sample_workspace_size(64, 151936) == 64 * 10 * 8
-    assert lib.tvllm_sample_workspace_size(3, 16384) == 3 * 1 * 8
+    # One 8-byte (value, index) partial per 8192-wide span of each row.
+    assert lib.tvllm_sample_workspace_size(64, 151936) == 64 * 19 * 8
+    assert lib.tvllm_sample_workspace_size(3, 16384) == 3 * 2 * 8
     assert lib.tvllm_sample_workspace_size(0, 151936) == 0
     status = lib.tvllm_sample(None, 1, 100, 100, None, None, None, None, None, None,
                               None, 64, 0, None)
