@@ -291,3 +291,34 @@ def test_pipelined_token_events_lag_one_step():
     assert not first.token_events
     second = engine.step()  # decode launched; the prefill's token resolves
     assert len(second.token_events) == 1
+
+
+def test_pipelined_eos_on_the_last_allowed_token_and_cancel_while_finishing():
+    """Length stop known at launch (the request leaves the decode queue) and
+    an EOS resolved for that same last token; a request cancelled while its
+    last token is still in flight."""
+    rng = random.Random(9)
+    eos_first = next(p for p in ([rng.randrange(6, VOCAB) for _ in range(rng.randrange(1, 20))]
+                                 for _ in range(10000))
+                     if next_token(p) == EOS)
+    engine, ex = make_engine(pipelined=True)
+    a = engine.submit(eos_first, SamplingParams(max_new_tokens=1))  # EOS is also the last
+    b = engine.submit([31] * 9, SamplingParams(max_new_tokens=2, ignore_eos=True))
+    events = []
+    while engine.has_unfinished():
+        events += engine.step().completion_events
+    by_id = {e.request_id: e for e in events}
+    assert list(by_id[a].output_token_ids) == [EOS]
+    assert list(by_id[b].output_token_ids) == expected([31] * 9, SamplingParams(
+        max_new_tokens=2, ignore_eos=True), 96)
+    # Cancel right after the step that launched the last token's row.
+    c = engine.submit([32] * 5, SamplingParams(max_new_tokens=1, ignore_eos=True))
+    engine.step()  # prefill launched; its (only, last) token is in flight
+    assert engine.cancel(c)
+    done = []
+    while engine.has_unfinished():
+        done += engine.step().completion_events
+    (ev,) = done
+    assert ev.status is RequestStatus.ABORTED and PENDING_TOKEN not in ev.output_token_ids
+    assert engine.scheduler.block_manager.free_block_count == 96
+    assert not engine.scheduler.has_unresolved_steps
