@@ -104,20 +104,30 @@ class SplitKPartials:
 
 
 class SplitKLinear(nn.Linear):
-    """Bias-free nn.Linear for a projection with a long reduction axis (the
-    MLP down projection). For skinny inputs - the decode batch - hipBLASLt's
-    single GEMM leaves most of the GPU idle, so the product runs as a batched
-    torch.bmm over ``splits`` slices of the reduction axis with fp32 outputs,
-    returned as SplitKPartials for RMSNorm.add to sum inside its kernel.
-    Other inputs take F.linear. (Measured on MI355X, 4096x12288 bf16: 37 us
-    -> 24 us at 64 rows, 67 us -> 28 us at 128 rows.)"""
+    """Bias-free nn.Linear whose output feeds an RMSNorm.add (the attention
+    output and MLP down projections). For skinny inputs - the decode batch -
+    hipBLASLt's single GEMM leaves most of the GPU idle, so the product runs
+    as a batched torch.bmm over ``splits`` slices of the reduction axis with
+    fp32 outputs, returned as SplitKPartials for RMSNorm.add to sum inside
+    its kernel. Other inputs take F.linear. Measured on MI355X in graph
+    replay (bf16, us, F.linear -> split-K):
+      4096x12288 (8B down): 64 rows 37 -> 24 (4), 128 rows 67 -> 28 (4);
+        1-16 rows 22 -> 22 (4)
+      4096x4096 (8B o): 1-16 rows 15.5 -> 9.7 (4), 64 rows 15.0 -> 14.9 (4)
+      1024x2048 (0.6B o): 1-16 rows 8.1 -> 4.5-4.8 (8)
+      1024x3072 (0.6B down): 1-16 rows 9.4-11.4 -> 4.8-7.0 (8)"""
 
     def __init__(self, in_features: int, out_features: int, *, device=None,
                  dtype=None) -> None:
         super().__init__(in_features, out_features, bias=False, device=device, dtype=dtype)
 
     def splits_for(self, rows: int) -> int:
-        s = 4 if 32 <= rows <= 128 else 8 if 128 < rows <= 512 else 1
+        if rows > 512:
+            s = 1
+        elif rows > 128:
+            s = 8
+        else:  # narrow outputs need more slices to fill the GPU
+            s = 8 if self.out_features <= 2048 else 4
         return s if self.in_features % (8 * s) == 0 else 1
 
     def forward(self, x: torch.Tensor) -> torch.Tensor | SplitKPartials:

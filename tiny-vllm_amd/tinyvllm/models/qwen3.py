@@ -133,7 +133,9 @@ class Qwen3Attention(nn.Module):
             (config.q_proj_size, config.kv_proj_size, config.kv_proj_size),
             shard_names=("q", "k", "v"), device=device, dtype=dtype,
         )
-        self.o_proj = nn.Linear(config.q_proj_size, config.hidden_size, bias=False,
+        # Split-K at decode batch sizes: its partials go to the next
+        # RMSNorm.add, like the MLP down projection's.
+        self.o_proj = SplitKLinear(config.q_proj_size, config.hidden_size,
                                 device=device, dtype=dtype)
         self.q_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps, device=device, dtype=dtype)
         self.k_norm = RMSNorm(self.head_dim, eps=config.rms_norm_eps, device=device, dtype=dtype)
