@@ -115,19 +115,22 @@ class SplitKLinear(nn.Linear):
         1-16 rows 22 -> 22 (4)
       4096x4096 (8B o): 1-16 rows 15.5 -> 9.7 (4), 64 rows 15.0 -> 14.9 (4)
       1024x2048 (0.6B o): 1-16 rows 8.1 -> 4.5-4.8 (8)
-      1024x3072 (0.6B down): 1-16 rows 9.4-11.4 -> 4.8-7.0 (8)"""
+      1024x3072 (0.6B down): 1-16 rows 9.4-11.4 -> 4.8-7.0 (8)
+      129-512 rows: 8B down 8 slices (256 rows 57 -> 41), 8B o 4 (512 rows
+        34 -> 26), 0.6B 2 (512-row down 13.8 -> 10.5)"""
 
     def __init__(self, in_features: int, out_features: int, *, device=None,
                  dtype=None) -> None:
         super().__init__(in_features, out_features, bias=False, device=device, dtype=dtype)
 
     def splits_for(self, rows: int) -> int:
+        narrow = self.out_features <= 2048
         if rows > 512:
             s = 1
-        elif rows > 128:
-            s = 8
+        elif rows > 128:  # prefill chunks and mixed steps
+            s = 2 if narrow else 8 if self.in_features >= 8192 else 4
         else:  # narrow outputs need more slices to fill the GPU
-            s = 8 if self.out_features <= 2048 else 4
+            s = 8 if narrow else 4
         return s if self.in_features % (8 * s) == 0 else 1
 
     def forward(self, x: torch.Tensor) -> torch.Tensor | SplitKPartials:
