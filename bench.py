@@ -197,10 +197,10 @@ def attention_roofline(executor, workload, cfg, iters: int = 30,
             "avg_launch_us": round(seconds * 1e6, 2), "bytes_per_launch": algorithmic}
 
 
-def cpu_baseline(cfg, batch: int, context: int, reps: int = 15) -> dict:
+def cpu_baseline(cfg, batch: int, context: int, reps: int = 21) -> dict:
     """The oracle's decode step on the host cores: one decoder layer at full
     batch and context (GEMMs + paged gather + fp32 softmax attention + the
-    pointwise chain), timed `reps` times (median; ~10 s of host work at the
+    pointwise chain), timed `reps` times (median; ~14 s of host work at the
     8B shape), extrapolated to all layers plus the LM head (median of 3)."""
     import torch
 

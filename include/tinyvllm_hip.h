@@ -49,6 +49,12 @@ const char* tvllm_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int tvllm_abi_version(void);
 
+/* Hex SHA-256 prefix of the sources (csrc/*.hip, csrc/*.h, include/*.h) the
+ * library was built from; the Python loader refuses a library whose digest
+ * differs from the sources beside it. No counterpart in the reference (its
+ * JIT build recompiles on source change, _extension.py:11-42). */
+const char* tvllm_source_hash(void);
+
 /* Scatter K/V rows into the paged cache: cache[slot[t]] = key[t] (bit copy;
  * cache_dtype == dtype, k_scale = v_scale = 1), or for cache_dtype
  * TVLLM_FP8_E4M3 the E4M3 byte of clamp(x * (1 / scale), -448, 448) per
@@ -96,7 +102,9 @@ int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
  * k_cache, v_cache: contiguous [num_slots, num_kv_heads, head_dim].
  * rows, offsets (num_rows + 1), lengths, blocks: int64 device vectors.
  * workspace: >= tvllm_paged_decode_workspace_size(...) bytes (may be NULL
- * when that size is 0). head_dim must be 64 or 128.
+ * when that size is 0). head_dim 128 with group <= 16 runs the MFMA kernel
+ * (GQA heads share each K/V load); any other head_dim <= 256 or group runs a
+ * slower generic kernel (one wave per query head, no MFMA).
  * cache_dtype: dtype (caches hold q's element type; k_scale = v_scale = 1)
  * or TVLLM_FP8_E4M3 (caches hold E4M3 bytes, [num_slots, kv_heads, head_dim];
  * K = stored * k_scale, V = stored * v_scale; head_dim 128, group <= 16).

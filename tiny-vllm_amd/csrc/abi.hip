@@ -21,3 +21,11 @@ void clear_error() { g_error[0] = '\0'; }
 extern "C" const char* tvllm_last_error(void) { return tvllm::g_error; }
 
 extern "C" int tvllm_abi_version(void) { return 3; }
+
+#ifndef TVLLM_SOURCE_HASH
+#define TVLLM_SOURCE_HASH "unknown"
+#endif
+
+// Digest of the kernel sources this library was compiled from (set by the
+// build script), so a loader can refuse a library older than its sources.
+extern "C" const char* tvllm_source_hash(void) { return TVLLM_SOURCE_HASH; }

@@ -22,7 +22,10 @@
 //    never moves between lanes.
 //  * O^T += V^T P^T (A = V^T from an LDS copy that staging stores transposed,
 //    with the tokens of each 16-token step ordered the way the MFMA k index
-//    visits them; B = the lane's probabilities rounded to the storage type).
+//    visits them; B = the lane's probabilities as two storage-type terms, P
+//    rounded and the rounded remainder, one MFMA each, so the product keeps
+//    about 16 bits of P - a single rounded P leaves ~1e-3 relative error in
+//    the output, the size of the whole bf16 tolerance).
 //    The O^T accumulator of a lane belongs to its own query: the softmax
 //    rescale and the final 1/l are lane-local.
 //  * online softmax in base 2 (v_exp_f32) with one running (max, sum) per
@@ -266,6 +269,7 @@ paged_prefill_d128(PrefillArgs<T> a) {
     // ---- per-wave math on one tile j ----------------------------------
     f32x16 sc[2];  // raw S^T of the tile: sc[tb][v] = token 32tb + 8(v/4) + 4*half + v%4
     U16x8 pb[4];   // P of the tile, k-step st: token 16st + 8jj + 4*half + i at k = 4jj + i
+    U16x8 pr[4];   // P - pb (the rounding remainder), rounded, same layout
     auto scores = [&](int j) {
         const uint16_t* kt = ks[j & 1];
         sc[0] = f32x16{};
@@ -321,13 +325,14 @@ paged_prefill_d128(PrefillArgs<T> a) {
                 ps[v & 3] += p[v];
             }
 #pragma unroll
-            for (int sh = 0; sh < 2; ++sh) {
-                U16x8& w = pb[2 * tb + sh];
-                w.w[0] = pack2<T>(p[8 * sh + 0], p[8 * sh + 1]);
-                w.w[1] = pack2<T>(p[8 * sh + 2], p[8 * sh + 3]);
-                w.w[2] = pack2<T>(p[8 * sh + 4], p[8 * sh + 5]);
-                w.w[3] = pack2<T>(p[8 * sh + 6], p[8 * sh + 7]);
-            }
+            for (int sh = 0; sh < 2; ++sh)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float p0 = p[8 * sh + 2 * e], p1 = p[8 * sh + 2 * e + 1];
+                    const uint32_t hw = pack2<T>(p0, p1);
+                    pb[2 * tb + sh].w[e] = hw;
+                    pr[2 * tb + sh].w[e] = pack2<T>(p0 - half_lo<T>(hw), p1 - half_hi<T>(hw));
+                }
         }
         l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
     };
@@ -339,6 +344,7 @@ paged_prefill_d128(PrefillArgs<T> a) {
             for (int n = 0; n < 4; ++n) {
                 const U16x8 va = *reinterpret_cast<const U16x8*>(
                     &vtt[(32 * n + col) * V_LD + 16 * st + 8 * half]);
+                o[n] = mfma32<T>(va, pr[st], o[n]);
                 o[n] = mfma32<T>(va, pb[st], o[n]);
             }
     };

@@ -29,6 +29,7 @@ _INT = ctypes.c_int
 _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_last_error": (ctypes.c_char_p, []),
     "tvllm_abi_version": (_INT, []),
+    "tvllm_source_hash": (ctypes.c_char_p, []),
     "tvllm_store_kv": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, _P,
                               _I64, _I64, _I64, _I64, _INT, _INT, _F32, _F32, _P]),
     "tvllm_paged_decode_workspace_size": (_I64, [_I64] * 6),
@@ -89,6 +90,16 @@ def load_kernels() -> ctypes.CDLL:
         raise RuntimeError(
             f"tinyvllm HIP library ABI {version} does not match {ABI_VERSION}; rebuild it"
         )
+    from .build import CSRC_DIR, source_hash
+
+    if CSRC_DIR.is_dir():  # sources travel with the tree; refuse a stale build
+        built = lib.tvllm_source_hash().decode()
+        expected = source_hash()
+        if built != expected:
+            raise RuntimeError(
+                f"{LIBRARY_PATH.name} was built from other sources (digest {built}, "
+                f"sources {expected}); rebuild it (python -m tinyvllm.kernels.build)"
+            )
     return lib
 
 

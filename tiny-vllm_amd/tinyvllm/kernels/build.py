@@ -9,6 +9,7 @@ Usage: ``python -m tinyvllm.kernels.build`` or ``build_library()``.
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -52,6 +53,19 @@ def sources() -> list[Path]:
     return sorted(CSRC_DIR.glob("*.hip"))
 
 
+def source_hash() -> str:
+    """Digest of every input of the library (kernels, headers, flags); the
+    loader compares it with the one compiled into the library."""
+    h = hashlib.sha256()
+    files = sorted(CSRC_DIR.glob("*.hip")) + sorted(CSRC_DIR.glob("*.h")) + \
+        sorted(INCLUDE_DIR.glob("*.h"))
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    h.update(" ".join(HIPCC_FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
 def build_library(*, jobs: int | None = None, verbose: bool = False) -> Path:
     """Compile every ``csrc/*.hip`` and link the shared library; returns its path."""
     hipcc = _hipcc()
@@ -61,9 +75,12 @@ def build_library(*, jobs: int | None = None, verbose: bool = False) -> Path:
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
 
+    digest = source_hash()
+
     def compile_one(src: Path) -> Path:
         obj = build_dir / (src.stem + ".o")
-        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}",
+               f'-DTVLLM_SOURCE_HASH="{digest}"', "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         proc = subprocess.run(cmd, capture_output=True, text=True)

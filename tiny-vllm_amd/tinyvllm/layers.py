@@ -134,7 +134,10 @@ class SplitKLinear(nn.Linear):
         return s if self.in_features % (8 * s) == 0 else 1
 
     def forward(self, x: torch.Tensor) -> torch.Tensor | SplitKPartials:
-        s = self.splits_for(x.shape[0]) if x.dim() == 2 else 1
+        # Split-K views the rows in place: only for contiguous 2-D GPU inputs
+        # (torch.bmm with an fp32 out_dtype is a GPU-only overload).
+        split_ok = x.dim() == 2 and x.is_cuda and x.is_contiguous()
+        s = self.splits_for(x.shape[0]) if split_ok else 1
         if s == 1:
             return F.linear(x, self.weight)
         rows, k = x.shape
