@@ -125,6 +125,29 @@ int tvllm_paged_decode(const void* q, int64_t q_token_stride,
                        int dtype, int cache_dtype, float k_scale, float v_scale,
                        tvllm_stream_t stream);
 
+/* tvllm_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * split-K partials go to a static 8 MiB device array per GPU (held until
+ * the process ends); a geometry whose tvllm_paged_decode_workspace_size
+ * exceeds 8 MiB is rejected with TVLLM_EINVAL (the default split plan needs
+ * at most ~4.3 MB). Allocates nothing. Calls that
+ * overlap on one GPU (different streams) share that array and race; calls
+ * ordered on one stream are safe. The first call on a device looks up the
+ * array's address (hipGetSymbolAddress): make it outside graph capture. */
+int tvllm_paged_decode_noalloc(const void* q, int64_t q_token_stride,
+                               int64_t q_head_stride, const void* k_cache,
+                               const void* v_cache, void* out,
+                               int64_t out_token_stride, int64_t out_head_stride,
+                               const int64_t* rows, const int64_t* blocks,
+                               const int64_t* offsets, const int64_t* lengths,
+                               int64_t num_rows, int64_t num_heads,
+                               int64_t num_kv_heads, int64_t head_dim,
+                               int64_t num_slots, int64_t block_size,
+                               int64_t max_context_len, float scale,
+                               int dtype, int cache_dtype, float k_scale,
+                               float v_scale, tvllm_stream_t stream);
+
 /* tvllm_qk_norm_rope's fused KV write followed by tvllm_paged_decode, in
  * one kernel, for a step whose rows are all decode rows: q, k, v are the raw
  * projections (element strides, last 1); each workgroup normalises and

@@ -38,6 +38,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 namespace tvllm {
@@ -1159,6 +1160,77 @@ extern "C" int tvllm_paged_decode(
                              num_slots, block_size, max_context_len, scale, workspace,
                              workspace_bytes, dtype, cache_dtype, k_scale, v_scale, stream,
                              nullptr);
+}
+
+// ---------------------------------------------------------- no-alloc --
+// tvllm_paged_decode_noalloc: the split-K partials live in this file-scope
+// device array instead of a caller workspace. Each GPU holds its own copy;
+// host code reaches it only through the address hipGetSymbolAddress returns
+// for the current device, taken once per device on first use.
+namespace tvllm {
+namespace {
+
+// The split planner asks for at most ~4.3 MB (fewer than 512 split (row, KV
+// head) units x group 16 x 520 bytes); 8 MiB leaves room for other plans.
+constexpr int64_t kScratchBytes = int64_t(8) << 20;
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of this device's scratch array (nullptr with the error set).
+void* scratch_for_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("paged_decode_noalloc: no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || ptr == nullptr) {
+            set_error("paged_decode_noalloc: hipGetSymbolAddress failed: %s",
+                      hipGetErrorString(err));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace tvllm
+
+extern "C" int tvllm_paged_decode_noalloc(
+    const void* q, int64_t q_token_stride, int64_t q_head_stride,
+    const void* k_cache, const void* v_cache, void* out, int64_t out_token_stride,
+    int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
+    const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
+    int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
+    int64_t block_size, int64_t max_context_len, float scale, int dtype,
+    int cache_dtype, float k_scale, float v_scale, tvllm_stream_t stream) {
+    const int64_t need = tvllm_paged_decode_workspace_size(
+        num_rows, num_heads, num_kv_heads, head_dim, max_context_len, block_size);
+    TVLLM_CHECK(need <= kScratchBytes,
+                "paged_decode_noalloc: this geometry needs %lld bytes of split-K "
+                "workspace, above the %lld-byte static scratch; use tvllm_paged_decode",
+                (long long)need, (long long)kScratchBytes);
+    void* ws = nullptr;
+    if (need > 0) {
+        ws = scratch_for_current_device();
+        if (ws == nullptr) return int(TVLLM_ELAUNCH);
+    }
+    // Every split workgroup writes its partials before the merge reads them,
+    // so the scratch needs no clearing between calls.
+    return paged_decode_impl(q, q_token_stride, q_head_stride, k_cache, v_cache, out,
+                             out_token_stride, out_head_stride, rows, blocks, offsets,
+                             lengths, num_rows, num_heads, num_kv_heads, head_dim,
+                             num_slots, block_size, max_context_len, scale, ws,
+                             need > 0 ? kScratchBytes : 0, dtype, cache_dtype, k_scale,
+                             v_scale, stream, nullptr);
 }
 
 extern "C" int tvllm_paged_decode_qk_norm_rope(

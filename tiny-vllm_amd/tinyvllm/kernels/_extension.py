@@ -38,6 +38,10 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
                                   _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                   _I64, _I64, _I64, _F32, _P, _I64, _INT, _INT, _F32,
                                   _F32, _P]),
+    "tvllm_paged_decode_noalloc": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64,
+                                          _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                          _I64, _I64, _I64, _F32, _INT, _INT, _F32,
+                                          _F32, _P]),
     "tvllm_paged_decode_qk_norm_rope": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64,
                                                _I64, _P, _P, _P, _P, _F32, _F32, _P, _P,
                                                _P, _P, _I64, _I64, _P, _P, _P, _P, _I64,
