@@ -67,11 +67,13 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
 
 
 def forward(cfg: TinyQwen3, w: dict[str, torch.Tensor], token_ids: list[int],
-            kv_fp8: tuple[float, float] | None = None) -> torch.Tensor:
+            kv_fp8: tuple[float, float] | None = None,
+            logit_rows: list[int] | None = None) -> torch.Tensor:
     """Full causal forward of one sequence; logits [L, vocab] (storage-dtype values).
     ``kv_fp8=(k_scale, v_scale)`` attends over K/V passed through the FP8 E4M3
     cache layout (quantised, then read back), as an engine with that layout
-    does."""
+    does. ``logit_rows`` limits the LM head to those positions (logits
+    [len(logit_rows), vocab])."""
     ids = torch.tensor(token_ids, dtype=torch.long)
     length = ids.numel()
     dtype = w["model.embed_tokens.weight"].dtype
@@ -110,6 +112,9 @@ def forward(cfg: TinyQwen3, w: dict[str, torch.Tensor], token_ids: list[int],
                                      w[f"{p}.post_attention_layernorm.weight"], cfg.rms_norm_eps)
         gu = linear(x, w[f"{p}.mlp.gate_up_proj.weight"])
         hidden = linear(P.silu_and_mul(gu), w[f"{p}.mlp.down_proj.weight"])
+    if logit_rows is not None:
+        rows = torch.tensor(logit_rows, dtype=torch.long)
+        hidden, residual = hidden[rows], residual[rows]
     hidden, _ = P.add_rms_norm(hidden, residual, w["model.norm.weight"], cfg.rms_norm_eps)
     head = w.get("lm_head.weight", w["model.embed_tokens.weight"])
     return linear(hidden, head).float()  # bf16 logits, as F.linear produces

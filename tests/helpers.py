@@ -120,3 +120,63 @@ class ManualBatches:
 
     def step(self, items):
         return self._batch(items)
+
+
+def assert_within_ulp(actual: torch.Tensor, expected: torch.Tensor,
+                      scale: torch.Tensor | None = None, ulps: float = 1.0,
+                      max_abs: float = MAX_ABS, mean_rel: float = MEAN_REL) -> None:
+    """The bf16 bar widened where one bf16 ulp exceeds it: each element within
+    max(max_abs, ulps x ulp(max(|expected|, |scale|))) - rounding flips of
+    values above 4, where max abs 2e-2 is sub-ulp (``scale``: the operands'
+    magnitude, for rounded sums) - and the mean relative (L1) error within
+    ``mean_rel``."""
+    a = actual.detach().float().cpu()
+    e = expected.detach().float().cpu()
+    assert a.shape == e.shape, (a.shape, e.shape)
+    assert torch.isfinite(a).all(), "non-finite values in output"
+    mag = e.abs() if scale is None else torch.maximum(e.abs(), scale.detach().float().abs())
+    ulp = torch.exp2(torch.floor(torch.log2(mag.clamp_min(2.0 ** -126))) - 7)
+    allowed = torch.clamp(ulps * ulp, min=max_abs)
+    excess = ((a - e).abs() / allowed).max().item() if a.numel() else 0.0
+    assert excess <= 1.0, f"error {excess:.2f}x max({max_abs}, {ulps} bf16 ulp)"
+    rel = ((a - e).abs().sum() / e.abs().sum().clamp_min(1e-30)).item()
+    assert rel <= mean_rel, f"mean rel err {rel:.3e} > {mean_rel}"
+
+
+def bf16_ulp(x: float) -> float:
+    """One bf16 unit in the last place at |x| (7 fraction bits)."""
+    x = abs(float(x))
+    if x == 0.0:
+        return 2.0 ** -133
+    return 2.0 ** (math.floor(math.log2(x)) - 7)
+
+
+def build_model(cfg, weights, device):
+    """Our Qwen3ForCausalLM for an oracle TinyQwen3 config, loaded with the
+    oracle's packed weight dict through the checkpoint weight routes."""
+    from tinyvllm.models.qwen3 import Qwen3Config, Qwen3ForCausalLM
+
+    qcfg = Qwen3Config.from_dict(dict(
+        model_type="qwen3", vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size,
+        intermediate_size=cfg.intermediate_size, num_hidden_layers=cfg.num_hidden_layers,
+        num_attention_heads=cfg.num_attention_heads,
+        num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+        max_position_embeddings=cfg.max_position_embeddings, rope_theta=cfg.rope_theta,
+        tie_word_embeddings=cfg.tie_word_embeddings))
+    model = Qwen3ForCausalLM(qcfg, device=device, dtype=torch.bfloat16)
+    q = cfg.num_attention_heads * cfg.head_dim
+    kv = cfg.num_key_value_heads * cfg.head_dim
+    for name, tensor in weights.items():
+        t = tensor.to(device)
+        if name.endswith("qkv_proj.weight"):
+            base = name[:-len("qkv_proj.weight")]
+            model.load_weight(base + "q_proj.weight", t[:q])
+            model.load_weight(base + "k_proj.weight", t[q:q + kv])
+            model.load_weight(base + "v_proj.weight", t[q + kv:])
+        elif name.endswith("gate_up_proj.weight"):
+            base = name[:-len("gate_up_proj.weight")]
+            model.load_weight(base + "gate_proj.weight", t[:cfg.intermediate_size])
+            model.load_weight(base + "up_proj.weight", t[cfg.intermediate_size:])
+        else:
+            model.load_weight(name, t)
+    return model.eval()

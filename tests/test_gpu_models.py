@@ -1,0 +1,456 @@
+"""Model-level parity at the benchmark architectures (configs C3, C4, C5).
+
+* C3: the whole Qwen3-0.6B (28 layers, vocab 151936, tied embeddings) with
+  N(0, 0.02) weights, 32 requests of 512 random ids, greedy, through the
+  engine (chunked prefill, graph-replayed decode at batch 32). The sampled
+  tokens of 4 rows are checked teacher-forced against the CPU oracle model.
+* C4: Qwen3-8B geometry (hidden 4096, 32Q/8KV, FFN 12288, vocab 151936),
+  64 requests of 2048 ids, chunked prefill 512, Poisson arrivals (mean gap
+  20 ms on a simulated clock), greedy. A 2-layer model is checked token by
+  token against the oracle (and pipelined == serial, all blocks freed); the
+  full 36-layer model is checked one layer at a time in a live decode step
+  (attention output, post-attention norm, residual and KV write against the
+  oracle layer on the engine's own cache).
+* C5: Qwen3-32B geometry (hidden 5120, 64Q/8KV, FFN 25600), 16 requests of
+  16k-32k ids sharing a 4096-token prefix through the prefix cache: the
+  live-layer check at the second layer of a 2-layer model, the first layer's
+  K/V of the shared prefix against the oracle, and shared prefix pages.
+
+Greedy agreement (north star: >= 99% of steps) is teacher-forced: a step
+agrees when our token is the oracle's argmax for the same context, or when
+the oracle scores it within one bf16 ulp of its best logit (a tie at bf16
+resolution that another summation order may legitimately break).
+Reference path: models/qwen3.py:458-494 and :703-717, executor.py:126-141.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_close, assert_within_ulp, bf16_ulp
+from oracle import attention as OA
+from oracle import model as OM
+from oracle import pointwise as OP
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 151936
+GEOMETRY = {  # hidden, intermediate, layers, q heads, kv heads, tied embeddings
+    "qwen3-0.6b": (1024, 3072, 28, 16, 8, True),
+    "qwen3-8b": (4096, 12288, 36, 32, 8, False),
+    "qwen3-32b": (5120, 25600, 64, 64, 8, False),
+}
+
+
+def oracle_config(name, layers=None, max_position=4096):
+    h, inter, n, hq, hkv, tied = GEOMETRY[name]
+    return OM.TinyQwen3(vocab_size=VOCAB, hidden_size=h, intermediate_size=inter,
+                        num_hidden_layers=layers or n, num_attention_heads=hq,
+                        num_key_value_heads=hkv, head_dim=128, tie_word_embeddings=tied,
+                        max_position_embeddings=max_position)
+
+
+def teacher_forced(cfg, weights, prompt, ours):
+    """(agreeing steps, worst oracle logit deficit in ulps) of our greedy
+    tokens against one oracle forward over prompt + ours."""
+    rows = [len(prompt) - 1 + i for i in range(len(ours))]
+    logits = OM.forward(cfg, weights, list(prompt) + list(ours), logit_rows=rows)
+    agree, worst = 0, 0.0
+    for i, token in enumerate(ours):
+        row = logits[i]
+        best = float(row.max())
+        deficit = (best - float(row[token])) / bf16_ulp(best)
+        worst = max(worst, deficit)
+        agree += int(deficit <= 1.0)
+    return agree, worst
+
+
+def run_engine(engine, prompts, params, arrivals_ns=None, step_ns=2_000_000,
+               on_step=None):
+    """Step the engine on a simulated clock until every request finishes;
+    returns each prompt's output ids (submission order)."""
+    from tinyvllm.scheduler import ScheduleDecision
+
+    arrivals_ns = arrivals_ns if arrivals_ns is not None else [0] * len(prompts)
+    ids = [engine.submit(p, params, arrival_ns=int(a)) for p, a in zip(prompts, arrivals_ns)]
+    out = {rid: [] for rid in ids}
+    now = 0
+    while engine.has_unfinished():
+        events = engine.step(now_ns=now)
+        for ev in events.token_events:
+            out[ev.request_id].append(ev.token_id)
+        if on_step is not None:
+            on_step(out)
+        now += step_ns
+        if engine.scheduler.last_decision is ScheduleDecision.IDLE:
+            nxt = engine.scheduler.next_arrival_ns
+            if nxt is not None:
+                now = max(now, nxt)
+    return [out[rid] for rid in ids]
+
+
+def blocks_for(lengths, new):
+    return sum(-(-(n + new) // 16) for n in lengths) + 64
+
+
+# ------------------------------------------------------- live layer probe --
+
+class LayerProbe:
+    """Records one decode-only step's inputs and outputs of decoder layer
+    ``idx`` (eager forward hooks; the runner's graphs are bypassed for the
+    armed step)."""
+
+    def __init__(self, model, idx, rows):
+        self.layer = model.model.layers[idx]
+        self.idx, self.rows = idx, rows
+        self.armed, self.cap, self.request_ids = False, None, ()
+        self._buf = {}
+        self.handles = [
+            self.layer.register_forward_pre_hook(self._pre, with_kwargs=True),
+            self.layer.register_forward_hook(self._post, with_kwargs=True),
+            self.layer.self_attn.o_proj.register_forward_pre_hook(self._attn_out),
+            self.layer.mlp.register_forward_pre_hook(self._mlp_in),
+        ]
+
+    def _pre(self, module, args, kwargs):
+        kv = kwargs["attention"].kv
+        if not self.armed or kv.prefill is not None or kv.decode is None \
+                or kv.decode.query_rows.numel() != self.rows:
+            self._buf = {}
+            return
+        hidden = args[0]
+        parts = getattr(hidden, "partials", None)
+        d = kv.decode
+        self._buf = dict(
+            hidden=(parts if parts is not None else hidden).detach().clone(),
+            split=parts is not None,
+            residual=None if kwargs["residual"] is None else kwargs["residual"].clone(),
+            slots=kv.slot_mapping.clone(), blocks=d.block_table_ids.clone(),
+            offsets=d.block_table_offsets.clone(), lengths=d.context_lens.clone())
+
+    def _attn_out(self, module, args):
+        if self._buf:
+            self._buf["attn"] = args[0].detach().clone()
+
+    def _mlp_in(self, module, args):
+        if self._buf:
+            self._buf["normed"] = args[0].detach().clone()
+
+    def _post(self, module, args, kwargs, output):
+        if self._buf and self.cap is None:
+            self._buf["residual_out"] = output[1].detach().clone()
+            self.cap = {k: (v.cpu() if torch.is_tensor(v) else v)
+                        for k, v in self._buf.items()}
+        self._buf = {}
+
+    def step_eager(self, engine, now_ns):
+        """One engine step with this probe armed and decode graphs bypassed."""
+        runner = engine.executor.runner
+        graphs, runner.decode_graphs = runner.decode_graphs, None
+        forward = runner._forward
+
+        def recording(batch, *args, **kwargs):  # batch row -> request id
+            if self.cap is None:
+                self.request_ids = tuple(batch.request_ids)
+            return forward(batch, *args, **kwargs)
+
+        runner._forward = recording
+        self.armed = True
+        try:
+            return engine.step(now_ns=now_ns)
+        finally:
+            self.armed = False
+            runner.decode_graphs = graphs
+            del runner._forward
+
+    def close(self):
+        for h in self.handles:
+            h.remove()
+
+
+def model_and_weights(cfg, device, seed):
+    """Our model with random-init weights N(0, 0.02) (norm weights 1),
+    generated on the GPU, and the same weights on the CPU in the oracle's
+    naming (packed q|k|v and gate|up, as the model stores them)."""
+    from tinyvllm.models.qwen3 import Qwen3ForCausalLM
+
+    model = Qwen3ForCausalLM.random_init(_our_config(cfg), device=device, seed=seed)
+    weights = {name: p.detach().cpu() for name, p in model.named_parameters()}
+    if cfg.tie_word_embeddings:
+        weights.pop("lm_head.weight", None)
+    return model, weights
+
+
+def layer_weights(model, idx):
+    """Layer ``idx``'s weights on the CPU, oracle names."""
+    layer = model.model.layers[idx]
+    return {
+        "in": layer.input_layernorm.weight.detach().cpu(),
+        "post": layer.post_attention_layernorm.weight.detach().cpu(),
+        "qkv": layer.self_attn.qkv_proj.weight.detach().cpu(),
+        "o": layer.self_attn.o_proj.weight.detach().cpu(),
+        "qn": layer.self_attn.q_norm.weight.detach().cpu(),
+        "kn": layer.self_attn.k_norm.weight.detach().cpu(),
+    }
+
+
+def check_kv(our_k, our_v, k, v):
+    """K/V rows the engine wrote vs the oracle's projections. The write itself
+    is a bit copy (checked bit-exact by the kernel tests); the values come
+    from our GEMM, whose summation order may flip one rounding of the
+    projection: V within one bf16 ulp, K (then normalised and rotated)
+    within two; mean relative error within 1e-3 for both."""
+    assert_within_ulp(our_v, v, ulps=1.0)
+    assert_within_ulp(our_k, k, ulps=2.0)
+
+
+def check_layer_against_oracle(cap, w, key_cache, value_cache, cfg, block_size=16):
+    """The attention half of one decoder layer restated on the CPU from the
+    captured input, over the engine's own KV cache (layer copy, CPU):
+    our KV write and attention output must be within the bf16 bar of the
+    oracle's, the residual sum within two rounding flips, the post-attention
+    norm within the bf16 bar of the oracle norm of our residual."""
+    hq, hkv, d, eps = cfg.num_attention_heads, cfg.num_key_value_heads, 128, 1e-6
+    hidden = cap["hidden"]
+    if cap["split"]:  # split-K partials: summed in order, rounded once
+        acc = hidden[0].clone()
+        for p in range(1, hidden.shape[0]):
+            acc = acc + hidden[p]
+        hidden = acc.to(torch.bfloat16)
+    if cap["residual"] is None:
+        x, res = OP.rms_norm(hidden, w["in"], eps), hidden
+    else:
+        x, res = OP.add_rms_norm(hidden, cap["residual"], w["in"], eps)
+    t = x.shape[0]
+    qkv = OM.linear(x, w["qkv"])
+    q = qkv[:, :hq * d].view(t, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    positions = cap["lengths"] - 1
+    cos, sin = OP.rope_tables(positions, d, cfg.rope_theta, torch.bfloat16)
+    q, k = OP.qk_norm_rope(q, k, w["qn"], w["kn"], cos, sin, eps, eps)
+    slots = cap["slots"]
+    check_kv(key_cache[slots], value_cache[slots], k, v)  # the fused KV write
+    attn = torch.empty_like(q)
+    OA.decode_attention(q, key_cache, value_cache, torch.arange(t), cap["blocks"],
+                        cap["offsets"], cap["lengths"], block_size, d ** -0.5, attn)
+    assert_bf16_close(cap["attn"].view(t, hq, d), attn)
+    o = OM.linear(attn.view(t, hq * d), w["o"])
+    normed, res2 = OP.add_rms_norm(o, res, w["post"], eps)
+    # The residual stream grows with depth (|x| ~ 20 at layer 20 of the 8B),
+    # where max abs 2e-2 is below one ulp: allow one rounding flip of the
+    # projection and one of the sum (2 ulps of the operands' magnitude).
+    assert_within_ulp(cap["residual_out"], res2,
+                      scale=torch.maximum(o.float().abs(), res.float().abs()), ulps=2.0)
+    # The norm given our residual: the strict bar. Against the independent
+    # oracle chain only the mean error is bounded: where o and the residual
+    # cancel, one rounding flip of o is many ulps of the sum, and the norm
+    # scales that up.
+    assert_bf16_close(cap["normed"], OP.rms_norm(cap["residual_out"], w["post"], eps))
+    assert_within_ulp(cap["normed"], normed, max_abs=float("inf"))
+
+
+def probe_run(engine, model, idx, prompts, params, arrivals_ns, step_ns=50_000_000):
+    """Run to completion; once every request has two tokens, one decode step
+    runs eagerly with the layer probe armed, and the probed layer's cache is
+    copied to the CPU right after it. A simulated step of 50 ms lets all
+    Poisson arrivals (mean gap 20 ms) land within the prefill phase, so some
+    step decodes every request at once."""
+    probe = LayerProbe(model, idx, rows=len(prompts))
+    state = {"done": False, "cache": None}
+    from tinyvllm.scheduler import ScheduleDecision
+
+    ids = [engine.submit(p, params, arrival_ns=int(a)) for p, a in zip(prompts, arrivals_ns)]
+    out = {rid: [] for rid in ids}
+    now = 0
+    try:
+        while engine.has_unfinished():
+            ready = not state["done"] and all(len(v) >= 2 for v in out.values())
+            events = probe.step_eager(engine, now) if ready else engine.step(now_ns=now)
+            if ready and probe.cap is not None:
+                torch.cuda.synchronize()
+                cache = engine.executor.runner.kv_cache
+                state["cache"] = (cache.key[idx].cpu(), cache.value[idx].cpu())
+                state["done"] = True
+            for ev in events.token_events:
+                out[ev.request_id].append(ev.token_id)
+            now += step_ns
+            if engine.scheduler.last_decision is ScheduleDecision.IDLE:
+                nxt = engine.scheduler.next_arrival_ns
+                if nxt is not None:
+                    now = max(now, nxt)
+    finally:
+        probe.close()
+    assert probe.cap is not None, "no decode-only step with every row was probed"
+    probe.cap["row_of"] = {ids.index(rid): r for r, rid in enumerate(probe.request_ids)}
+    return probe.cap, state["cache"], [out[rid] for rid in ids]
+
+
+# ---------------------------------------------------------------------- C3 --
+
+def test_c3_qwen3_0_6b_engine_greedy_matches_oracle(device):
+    from tinyvllm import SamplingParams
+    from tinyvllm.bootstrap import build_engine
+
+    cfg = oracle_config("qwen3-0.6b", max_position=1024)
+    model, weights = model_and_weights(cfg, device, seed=3)
+    g = torch.Generator().manual_seed(33)
+    prompts = [torch.randint(0, VOCAB, (512,), generator=g).tolist() for _ in range(32)]
+    new = 8
+    engine = build_engine(model, max_model_len=1024, max_num_seqs=32,
+                          max_num_batched_tokens=4096, num_blocks=blocks_for([512] * 32, new),
+                          prefill_chunk_size=512)
+    outs = run_engine(engine, prompts, SamplingParams(max_new_tokens=new, ignore_eos=True))
+    assert all(len(o) == new for o in outs)
+    manager = engine.scheduler.block_manager
+    assert manager.free_block_count == manager.pool.num_blocks
+    engine.close()
+    agree = total = 0
+    worst = 0.0
+    for r in (0, 9, 20, 31):
+        a, w = teacher_forced(cfg, weights, prompts[r], outs[r])
+        agree, total, worst = agree + a, total + new, max(worst, w)
+    print(f"C3 teacher-forced agreement {agree}/{total}, worst deficit {worst:.2f} ulp")
+    assert agree / total >= 0.99, (agree, total, worst)
+
+
+# ---------------------------------------------------------------------- C4 --
+
+def _c4_workload(n=64, prompt=2048, seed=44):
+    rng = np.random.default_rng(seed)
+    prompts = [rng.integers(0, VOCAB, size=prompt).tolist() for _ in range(n)]
+    arrivals = np.cumsum(rng.exponential(20e6, size=n)).astype(np.int64).tolist()
+    return prompts, arrivals
+
+
+def test_c4_qwen3_8b_geometry_engine_tokens_match_oracle(device):
+    """Two layers of the Qwen3-8B geometry through the C4 workload: greedy
+    tokens agree with the oracle, pipelined steps give the same tokens as
+    serial ones, and every block returns to the pool."""
+    from tinyvllm import SamplingParams
+    from tinyvllm.bootstrap import build_engine
+
+    cfg = oracle_config("qwen3-8b", layers=2, max_position=4096)
+    model, weights = model_and_weights(cfg, device, seed=4)
+    prompts, arrivals = _c4_workload()
+    new = 6
+    params = SamplingParams(max_new_tokens=new, ignore_eos=True)
+    runs = []
+    for pipelined in (True, False):
+        engine = build_engine(model, max_model_len=4096, max_num_seqs=64,
+                              max_num_batched_tokens=4096,
+                              num_blocks=blocks_for([2048] * 64, new),
+                              prefill_chunk_size=512, pipelined=pipelined)
+        assert engine._pipelined == pipelined
+        runs.append(run_engine(engine, prompts, params, arrivals))
+        manager = engine.scheduler.block_manager
+        assert manager.free_block_count == manager.pool.num_blocks
+        assert not engine.scheduler.has_unresolved_steps
+        engine.close()
+    assert runs[0] == runs[1]
+    agree = total = 0
+    worst = 0.0
+    for r in (0, 63):
+        a, w = teacher_forced(cfg, weights, prompts[r], runs[0][r])
+        agree, total, worst = agree + a, total + new, max(worst, w)
+    print(f"C4 teacher-forced agreement {agree}/{total}, worst deficit {worst:.2f} ulp")
+    assert agree / total >= 0.99, (agree, total, worst)
+
+
+def test_c4_qwen3_8b_live_decode_layer_matches_oracle(device):
+    """The full 36-layer Qwen3-8B (random N(0, 0.02), norms 1) through the C4
+    workload; in one decode step at batch 64 (contexts 2050-2100) layer 20 is
+    recomputed by the oracle from its captured input over the engine's own
+    cache. Layer 0's K/V of request 0's whole prompt (written by chunked
+    prefill) is checked against the oracle too."""
+    from tinyvllm import SamplingParams
+    from tinyvllm.bootstrap import build_engine
+    from tinyvllm.models.qwen3 import Qwen3ForCausalLM
+
+    cfg = oracle_config("qwen3-8b", max_position=4096)
+    model = Qwen3ForCausalLM.random_init(_our_config(cfg), device=device, seed=8)
+    prompts, arrivals = _c4_workload(seed=45)
+    engine = build_engine(model, max_model_len=4096, max_num_seqs=64,
+                          max_num_batched_tokens=4096, num_blocks=blocks_for([2048] * 64, 64),
+                          prefill_chunk_size=512)
+    params = SamplingParams(max_new_tokens=64, ignore_eos=True)
+    cap, (kc, vc), outs = probe_run(engine, model, 20, prompts, params, arrivals)
+    assert all(len(o) == 64 for o in outs)
+    assert int(cap["lengths"].min()) >= 2049
+    check_layer_against_oracle(cap, layer_weights(model, 20), kc, vc, cfg)
+    _check_layer0_prompt_kv(engine, model, cfg, prompts[0], cap, row=cap["row_of"][0])
+    engine.close()
+
+
+def _our_config(cfg):
+    from tinyvllm.models.qwen3 import Qwen3Config
+
+    return Qwen3Config.from_dict(dict(
+        model_type="qwen3", vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size,
+        intermediate_size=cfg.intermediate_size, num_hidden_layers=cfg.num_hidden_layers,
+        num_attention_heads=cfg.num_attention_heads,
+        num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+        max_position_embeddings=cfg.max_position_embeddings, rope_theta=cfg.rope_theta,
+        tie_word_embeddings=cfg.tie_word_embeddings))
+
+
+def _check_layer0_prompt_kv(engine, model, cfg, prompt, cap, row, count=None):
+    """Layer 0's K/V of ``prompt`` (the first ``count`` tokens) in the
+    engine's cache - found through the probed step's block table of ``row``
+    - against the oracle's projection of the embeddings."""
+    hq, hkv, d, eps = cfg.num_attention_heads, cfg.num_key_value_heads, 128, 1e-6
+    n = count or len(prompt)
+    ids = torch.tensor(prompt[:n])
+    emb = model.model.embed_tokens.weight[ids.to(model.model.embed_tokens.weight.device)].cpu()
+    w = layer_weights(model, 0)
+    x = OP.rms_norm(emb, w["in"], eps)
+    qkv = OM.linear(x, w["qkv"])
+    q = qkv[:, :hq * d].view(n, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(n, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(n, hkv, d)
+    cos, sin = OP.rope_tables(torch.arange(n), d, cfg.rope_theta, torch.bfloat16)
+    _, k = OP.qk_norm_rope(q, k, w["qn"], w["kn"], cos, sin, eps, eps)
+    table = cap["blocks"][int(cap["offsets"][row]):int(cap["offsets"][row + 1])]
+    pos = torch.arange(n)
+    slots = (table[pos // 16] * 16 + pos % 16).to(model.model.embed_tokens.weight.device)
+    cache = engine.executor.runner.kv_cache
+    check_kv(cache.key[0].index_select(0, slots).cpu(),
+             cache.value[0].index_select(0, slots).cpu(), k, v)
+
+
+# ---------------------------------------------------------------------- C5 --
+
+def test_c5_qwen3_32b_geometry_long_context_shared_prefix(device):
+    """Two layers of the Qwen3-32B geometry, 16 requests of U[16k, 32k]
+    random ids sharing a 4096-token prefix: prefix pages are shared (not
+    copied) between rows, layer 0's K/V of the prefix matches the oracle,
+    and in a live decode step (split-K over ~24k-token contexts, 64Q/8KV)
+    layer 1 matches the oracle layer over the engine's cache."""
+    from tinyvllm import SamplingParams
+    from tinyvllm.bootstrap import build_engine
+    from tinyvllm.models.qwen3 import Qwen3ForCausalLM
+
+    cfg = oracle_config("qwen3-32b", layers=2, max_position=40960)
+    model = Qwen3ForCausalLM.random_init(_our_config(cfg), device=device, seed=32)
+    rng = np.random.default_rng(55)
+    lengths = rng.integers(16384, 32768 + 1, size=16).tolist()
+    shared = rng.integers(0, VOCAB, size=4096).tolist()
+    prompts = [shared + rng.integers(0, VOCAB, size=n - 4096).tolist() for n in lengths]
+    engine = build_engine(model, max_model_len=40960, max_num_seqs=16,
+                          max_num_batched_tokens=4096, num_blocks=blocks_for(lengths, 160),
+                          prefill_chunk_size=512)
+    # ~100 chunked-prefill steps: early requests keep decoding until the last
+    # prompt is in, so one step decodes all 16 rows.
+    params = SamplingParams(max_new_tokens=160, ignore_eos=True)
+    cap, (kc, vc), outs = probe_run(engine, model, 1, prompts, params, [0] * 16)
+    assert all(len(o) == 160 for o in outs)
+    prefix_pages = 4096 // 16
+    tables = [cap["blocks"][int(cap["offsets"][r]):int(cap["offsets"][r + 1])]
+              for r in range(16)]
+    sharing = sum(torch.equal(t[:prefix_pages], tables[0][:prefix_pages]) for t in tables[1:])
+    assert sharing >= 8, sharing  # most requests reuse the published prefix pages
+    assert engine.scheduler.block_manager.prefix_cache.hit_tokens >= 8 * 4096
+    check_layer_against_oracle(cap, layer_weights(model, 1), kc, vc, cfg)
+    _check_layer0_prompt_kv(engine, model, cfg, prompts[0], cap, row=cap["row_of"][0],
+                            count=4096)
+    engine.close()
