@@ -1,43 +1,42 @@
-"""CPU ownership of KV blocks (reference: tinyvllm/cache.py:15-711).
+"""Host-side ownership of KV-cache blocks (the role of the reference's
+tinyvllm/cache.py; the slot arithmetic of cache.py:696-711 is the shared
+contract: logical position p of a request lives at slot
+``table[p // block_size] * block_size + p % block_size``).
 
-``BlockPool`` tracks each physical block's state, reference count and
-generation; ``BlockManager`` owns per-request block tables and stages one
-step's appends as a transaction (``BlockPlanTxn``) whose slot mapping the
-runner validates and uploads. The slot of logical position p of a request
-is ``table[p // block_size] * block_size + p % block_size`` - the contract
-shared with every kernel (``PagedKVCache`` layout).
+Design:
 
-Free list order: never-cached blocks are handed out first; blocks whose
-contents are still indexed by the prefix cache wait at the back, least
-recently released first, and are evicted (their key dropped) only when
-reused.
+* ``BlockPool`` keeps per-block holder counts and generations in numpy
+  arrays. Unheld blocks sit in one of two places: a stack of *blank* blocks
+  (no reusable contents, handed out first) or an eviction heap of *idle*
+  blocks whose contents are still indexed by a prefix digest (handed out
+  oldest-released first, losing their digest). Heap entries are stamped, so
+  re-holding an idle block needs no removal: the stale entry is skipped.
+* ``StepKV`` is one step's journal. Staging applies the step's allocations
+  and prefix pins to the pool at once and records them; ``undo`` reverses
+  exactly those records. ``go_live`` makes the new tables the requests'
+  tables (ownership is visible from the dispatch on), ``writes_done``
+  advances each request's valid KV length and counts prefix hits. After
+  ``go_live`` the only way back is the fail-stop ``teardown``.
+* ``BlockManager`` holds each request's table as an int64 id array plus the
+  generations it was taken at; ``BlockRef`` values are built on demand.
 """
 from __future__ import annotations
 
-from collections import OrderedDict
+import heapq
 from collections.abc import Callable, Sequence
 from dataclasses import dataclass
-from enum import Enum, auto
 
 import numpy as np
 
 from tinyvllm._validation import _check_non_negative_int, _check_positive_int
 from tinyvllm.prefix_cache import PrefixCache
 
-
-_EMPTY = np.zeros(0, dtype=np.int64)
-
-
-class BlockState(Enum):
-    FREE = auto()
-    RESERVED = auto()
-    ACTIVE = auto()
-    CACHED = auto()   # no owner, contents still indexed by the prefix cache
+_NO_IDS = np.zeros(0, dtype=np.int64)
 
 
 @dataclass(frozen=True, slots=True)
 class BlockRef:
-    """Physical block identity; the generation detects reuse."""
+    """A physical block at one generation (a reused block gets a new one)."""
 
     block_id: int
     generation: int
@@ -48,12 +47,10 @@ class BlockRef:
 
 
 @dataclass(frozen=True, slots=True)
-class BlockReservation:
-    block_refs: tuple[BlockRef, ...]
-
-
-@dataclass(frozen=True, slots=True)
 class BlockAppend:
+    """One request's KV growth in a step: ``query_len`` tokens written from
+    ``token_start``; a new request may first attach cached ``prefix`` blocks."""
+
     request_id: int
     token_start: int
     query_len: int
@@ -67,215 +64,233 @@ class BlockAppend:
 
 
 class BlockPool:
-    """Block states for one serial scheduler (no GPU tensors)."""
+    """Holder counts, generations and reuse order of the physical blocks."""
 
     def __init__(self, *, num_blocks: int) -> None:
         _check_positive_int("num_blocks", num_blocks)
-        self._state = [BlockState.FREE] * num_blocks
-        self._gen = [0] * num_blocks
-        self._refs = [0] * num_blocks
-        self._idle: OrderedDict[int, None] = OrderedDict.fromkeys(range(num_blocks))
-        self._by_key: dict[bytes, BlockRef] = {}
-        self._key_of: dict[int, bytes] = {}
-        self._reservation: BlockReservation | None = None
+        self.num_blocks = num_blocks
+        self._holders = np.zeros(num_blocks, dtype=np.int32)
+        self._gen = np.zeros(num_blocks, dtype=np.int64)
+        self._blank: list[int] = list(range(num_blocks - 1, -1, -1))  # pop() -> lowest
+        self._idle_stamp = np.zeros(num_blocks, dtype=np.int64)  # 0: not idle
+        self._idle_heap: list[tuple[int, int]] = []  # (stamp, block)
+        self._idle_count = 0
+        self._tick = 0
+        self._digest_of: dict[int, bytes] = {}
+        self._block_of: dict[bytes, int] = {}
         self.evictions = 0
 
-    @property
-    def num_blocks(self) -> int:
-        return len(self._state)
+    # -- views
 
     @property
     def free_block_count(self) -> int:
-        """Blocks a reservation may take (free or idle-cached)."""
-        return len(self._idle)
-
-    @property
-    def open_reservation_count(self) -> int:
-        return int(self._reservation is not None)
+        """Blocks an allocation may take now (blank plus idle cached)."""
+        return len(self._blank) + self._idle_count
 
     @property
     def cached_block_count(self) -> int:
-        return len(self._by_key)
+        return len(self._block_of)
 
-    def snapshot(self):
-        """Diagnostic view (allocation order is not a contract)."""
-        return tuple(self._idle), tuple(self._gen), tuple(self._state)
+    def ref(self, block: int) -> BlockRef:
+        return BlockRef(int(block), int(self._gen[block]))
 
-    def state(self, ref: BlockRef) -> BlockState:
-        if not isinstance(ref, BlockRef):
-            raise TypeError("ref must be BlockRef")
-        if ref.block_id >= self.num_blocks:
-            raise ValueError("block_id is out of range")
-        if self._gen[ref.block_id] != ref.generation:
-            raise RuntimeError("stale BlockRef generation")
-        return self._state[ref.block_id]
+    def current(self, ref: BlockRef) -> bool:
+        """The ref names its block's present generation."""
+        return (isinstance(ref, BlockRef) and ref.block_id < self.num_blocks
+                and int(self._gen[ref.block_id]) == ref.generation)
 
-    def reserve(self, count: int) -> BlockReservation | None:
+    def held(self, ref: BlockRef) -> int:
+        self._expect_current(ref)
+        return int(self._holders[ref.block_id])
+
+    def is_idle(self, ref: BlockRef) -> bool:
+        """Cached contents with no holder: taking it shrinks the free count."""
+        self._expect_current(ref)
+        return bool(self._idle_stamp[ref.block_id])
+
+    # -- allocation
+
+    def allocate(self, count: int) -> list[int] | None:
+        """``count`` blocks for new contents (blank first, then the oldest idle
+        ones, whose digests are dropped), each with one holder; None if the
+        pool is short (nothing taken)."""
         _check_positive_int("count", count)
-        if self._reservation is not None:
-            raise RuntimeError("a reservation is already open")
-        if count > len(self._idle):
+        if count > self.free_block_count:
             return None
-        refs = []
-        for _ in range(count):
-            block, _ = self._idle.popitem(last=False)
-            key = self._key_of.pop(block, None)
-            if key is not None:
-                del self._by_key[key]
-                self.evictions += 1
+        out = []
+        while len(out) < count:
+            block = self._blank.pop() if self._blank else self._evict_oldest()
             self._gen[block] += 1
-            self._state[block] = BlockState.RESERVED
-            refs.append(BlockRef(block, self._gen[block]))
-        self._reservation = BlockReservation(tuple(refs))
-        return self._reservation
+            self._holders[block] = 1
+            out.append(block)
+        return out
 
-    def commit(self, reservation: BlockReservation) -> None:
-        self._check_reservation(reservation)
-        for ref in reservation.block_refs:
-            self._state[ref.block_id] = BlockState.ACTIVE
-            self._refs[ref.block_id] = 1
-        self._reservation = None
+    def unallocate(self, blocks: Sequence[int]) -> None:
+        """Return blocks taken by ``allocate`` and never used (their
+        generation stays advanced, so refs to the old contents stay stale)."""
+        for block in reversed(blocks):
+            if self._holders[block] != 1:
+                raise RuntimeError(f"block {block} is not exclusively allocated")
+            self._holders[block] = 0
+            self._blank.append(int(block))
 
-    def rollback(self, reservation: BlockReservation) -> None:
-        """Return reserved blocks to the front of the free list (generations
-        are not rewound, so stale refs stay detectable)."""
-        self._check_reservation(reservation)
-        for ref in reversed(reservation.block_refs):
-            self._state[ref.block_id] = BlockState.FREE
-            self._idle[ref.block_id] = None
-            self._idle.move_to_end(ref.block_id, last=False)
-        self._reservation = None
+    def _evict_oldest(self) -> int:
+        while True:
+            stamp, block = heapq.heappop(self._idle_heap)
+            if self._idle_stamp[block] == stamp:
+                break
+        self._idle_stamp[block] = 0
+        self._idle_count -= 1
+        del self._block_of[self._digest_of.pop(block)]
+        self.evictions += 1
+        return block
 
-    def retain(self, ref: BlockRef) -> None:
-        state = self.state(ref)
-        if state is BlockState.CACHED:
-            del self._idle[ref.block_id]
-            self._state[ref.block_id] = BlockState.ACTIVE
-        elif state is not BlockState.ACTIVE:
-            raise RuntimeError("only computed active or cached blocks can be retained")
-        self._refs[ref.block_id] += 1
+    # -- holders
 
-    def release(self, ref: BlockRef) -> None:
-        if self.state(ref) is not BlockState.ACTIVE:
-            raise RuntimeError("block is not active")
+    def hold(self, ref: BlockRef) -> None:
+        """One more holder of a block with valid contents."""
+        self._expect_current(ref)
         block = ref.block_id
-        self._refs[block] -= 1
-        if self._refs[block]:
+        if self._idle_stamp[block]:
+            self._idle_stamp[block] = 0  # its heap entry goes stale
+            self._idle_count -= 1
+        elif not self._holders[block]:
+            raise RuntimeError(f"block {block} has no contents to share")
+        self._holders[block] += 1
+
+    def drop(self, ref: BlockRef) -> None:
+        """One holder fewer; an unheld block becomes idle (digest kept) or blank."""
+        self._expect_current(ref)
+        block = ref.block_id
+        if self._holders[block] <= 0:
+            raise RuntimeError(f"block {block} has no holder to drop")
+        self._holders[block] -= 1
+        if self._holders[block]:
             return
-        self._idle[block] = None
-        if block in self._key_of:
-            self._state[block] = BlockState.CACHED      # reusable, evict last
+        if block in self._digest_of:
+            self._tick += 1
+            self._idle_stamp[block] = self._tick
+            heapq.heappush(self._idle_heap, (self._tick, block))
+            self._idle_count += 1
         else:
-            self._state[block] = BlockState.FREE
-            self._idle.move_to_end(block, last=False)   # hand out first
+            self._blank.append(block)
 
-    def lookup(self, key: bytes) -> BlockRef | None:
-        return self._by_key.get(key)
+    # -- prefix digests
 
-    def publish(self, key: bytes, ref: BlockRef) -> BlockRef:
-        """Index an active computed block under ``key``; returns the block
-        already holding that key, if any."""
-        if self.state(ref) is not BlockState.ACTIVE:
-            raise RuntimeError("only an active computed block can be cached")
-        existing = self._by_key.get(key)
-        if existing is not None:
-            return existing
-        if ref.block_id in self._key_of:
-            raise RuntimeError("a cached block cannot change its prefix identity")
-        self._by_key[key] = ref
-        self._key_of[ref.block_id] = key
+    def find(self, digest: bytes) -> BlockRef | None:
+        block = self._block_of.get(digest)
+        return None if block is None else self.ref(block)
+
+    def label(self, digest: bytes, ref: BlockRef) -> BlockRef:
+        """Index a held block's contents under ``digest``; if another block
+        already holds those contents, that block is returned instead."""
+        if self.held(ref) == 0:
+            raise RuntimeError("only a held, written block can be indexed")
+        other = self._block_of.get(digest)
+        if other is not None:
+            return self.ref(other)
+        if ref.block_id in self._digest_of:
+            raise RuntimeError(f"block {ref.block_id} is already indexed under another prefix")
+        self._block_of[digest] = ref.block_id
+        self._digest_of[ref.block_id] = digest
         return ref
 
-    def clear_cache(self) -> None:
-        if self._reservation is not None:
-            raise RuntimeError("cannot clear cache during a reservation")
-        for ref in self._by_key.values():
-            if self._state[ref.block_id] is BlockState.CACHED:
-                self._state[ref.block_id] = BlockState.FREE
-        self._by_key.clear()
-        self._key_of.clear()
+    def forget_digests(self) -> None:
+        """Drop every digest: idle blocks become blank."""
+        for block in self._digest_of:
+            if self._idle_stamp[block]:
+                self._idle_stamp[block] = 0
+                self._blank.append(block)
+        self._idle_heap.clear()
+        self._idle_count = 0
+        self._digest_of.clear()
+        self._block_of.clear()
         self.evictions = 0
 
-    def _check_reservation(self, reservation: BlockReservation) -> None:
-        if self._reservation is not reservation:
-            raise ValueError("reservation is not open in this pool")
+    def _expect_current(self, ref: BlockRef) -> None:
+        if not self.current(ref):
+            raise RuntimeError(f"stale or foreign block reference {ref}")
 
 
-class BlockTxnState(Enum):
-    PREPARED = auto()
-    DISPATCHED = auto()
-    COMMITTED = auto()
-    ROLLED_BACK = auto()
-    FAILED = auto()
+class StepKV:
+    """One step's KV journal and the batch builder's view of it (plan id,
+    request order, block size, per-request table ids and write slots)."""
 
+    STAGED, LIVE, DONE, UNDONE, FAILED = "staged", "live", "done", "undone", "failed"
 
-class BlockPlanTxn:
-    """One step's staged block-table changes and slot mappings."""
+    __slots__ = ("plan_id", "request_ids", "phase", "_mgr", "_fresh", "_pins", "_rows")
 
-    __slots__ = ("_plan_id", "_state", "_manager", "_reservation", "_tables",
-                 "_ids", "_slots", "_ends", "_prefixes")
-
-    def __init__(self, *, plan_id, manager, reservation, tables, ids, slots, ends, prefixes):
-        self._plan_id = plan_id
-        self._state = BlockTxnState.PREPARED
-        self._manager = manager
-        self._reservation = reservation
-        self._tables: dict[int, tuple[BlockRef, ...]] = tables
-        self._ids: dict[int, np.ndarray] = ids
-        self._slots: dict[int, np.ndarray] = slots
-        self._ends: dict[int, int] = ends
-        self._prefixes: dict[int, tuple[BlockRef, ...]] = prefixes
-
-    @property
-    def state(self) -> BlockTxnState:
-        return self._state
-
-    @property
-    def plan_id(self) -> int:
-        return self._plan_id
-
-    @property
-    def request_ids(self) -> tuple[int, ...]:
-        self._readable()
-        return tuple(self._ends)
+    def __init__(self, plan_id: int, manager: "BlockManager") -> None:
+        self.plan_id = plan_id
+        self.phase = StepKV.STAGED
+        self._mgr = manager
+        self._fresh: list[int] = []                 # allocated by this step
+        self._pins: dict[int, tuple[BlockRef, ...]] = {}   # prefix hits held
+        # request -> (table ids, table generations, write slots, KV end)
+        self._rows: dict[int, tuple[np.ndarray, np.ndarray, np.ndarray, int]] = {}
+        self.request_ids: tuple[int, ...] = ()
 
     @property
     def block_size(self) -> int:
-        return self._manager.block_size
+        return self._mgr.block_size
 
     @property
     def num_blocks(self) -> int:
-        return self._manager.pool.num_blocks
+        return self._mgr.pool.num_blocks
 
     def append_metadata(self, request_id: int, token_start: int,
                         query_len: int) -> tuple[np.ndarray, np.ndarray]:
-        """(physical block ids of the request's table, write slots) as int64
-        arrays (the reference returns BlockRefs and a slot tuple; ids are
-        what every consumer reads, kept as arrays so a step's metadata is
-        flattened with memcpys)."""
-        self._readable()
-        if (request_id not in self._ends
-                or self._ends[request_id] != token_start + query_len
-                or len(self._slots[request_id]) != query_len):
-            raise ValueError("work item does not match its KV append")
-        return self._ids[request_id], self._slots[request_id]
+        """(table block ids, write slots) of one request as int64 arrays."""
+        if self.phase not in (StepKV.STAGED, StepKV.LIVE):
+            raise RuntimeError(f"KV step {self.plan_id} is {self.phase}")
+        row = self._rows.get(request_id)
+        if row is None or row[3] != token_start + query_len or len(row[2]) != query_len:
+            raise ValueError(f"request {request_id} has no KV append "
+                             f"[{token_start}, {token_start + query_len}) in this step")
+        return row[0], row[2]
 
-    def _readable(self) -> None:
-        if self._state not in (BlockTxnState.PREPARED, BlockTxnState.DISPATCHED):
-            raise RuntimeError("block transaction metadata is no longer readable")
+    # -- transitions
 
-    def commit_before_dispatch(self) -> None:
-        self._manager._commit_before_dispatch(self)
+    def go_live(self) -> None:
+        """The staged tables become the requests' tables (at dispatch)."""
+        self._expect(StepKV.STAGED)
+        tables = self._mgr._tables
+        for rid, (ids, gens, _, _) in self._rows.items():
+            tables[rid] = (ids, gens)
+        self.phase = StepKV.LIVE
 
-    def complete_writes(self) -> None:
-        self._manager._complete_writes(self)
+    def writes_done(self) -> None:
+        """The step's K/V are written: valid lengths advance, hits count."""
+        self._expect(StepKV.LIVE)
+        valid = self._mgr._valid
+        for rid, row in self._rows.items():
+            valid[rid] = row[3]
+        self._mgr.prefix_cache.note_hits(self._pins)
+        self.phase = StepKV.DONE
+        self._mgr._open = None
 
-    def rollback(self) -> None:
-        self._manager._rollback(self)
+    def undo(self) -> None:
+        """Reverse a staged (not dispatched) step."""
+        self._expect(StepKV.STAGED)
+        self._revert()
+        self.phase = StepKV.UNDONE
+        self._mgr._open = None
+
+    def _revert(self) -> None:
+        pool = self._mgr.pool
+        pool.unallocate(self._fresh)
+        for refs in self._pins.values():
+            for ref in refs:
+                pool.drop(ref)
+        self._fresh, self._pins = [], {}
+
+    def _expect(self, phase: str) -> None:
+        if self._mgr._open is not self or self.phase != phase:
+            raise RuntimeError(f"KV step {self.plan_id} is {self.phase}, expected {phase}")
 
 
 class BlockManager:
-    """Owns request block tables; stages each step's appends transactionally."""
+    """Request block tables over one BlockPool, grown one StepKV at a time."""
 
     def __init__(self, *, block_size: int, num_blocks: int,
                  enable_prefix_caching: bool = True) -> None:
@@ -286,196 +301,144 @@ class BlockManager:
         self.pool = BlockPool(num_blocks=num_blocks)
         self.prefix_cache = PrefixCache(block_size=block_size, pool=self.pool,
                                         enabled=enable_prefix_caching)
-        self._tables: dict[int, tuple[BlockRef, ...]] = {}
-        self._ids: dict[int, np.ndarray] = {}   # block ids of each table (int64)
+        self._tables: dict[int, tuple[np.ndarray, np.ndarray]] = {}  # ids, generations
         self._valid: dict[int, int] = {}
-        self._open: BlockPlanTxn | None = None
-        self._last: BlockPlanTxn | None = None
+        self._open: StepKV | None = None
 
-    def block_table(self, request_id: int) -> tuple[BlockRef, ...]:
-        return self._tables.get(request_id, ())
-
-    def valid_token_count(self, request_id: int) -> int:
-        return self._valid.get(request_id, 0)
+    # -- views
 
     @property
     def free_block_count(self) -> int:
         return self.pool.free_block_count
 
-    def match_prefix(self, request_id: int, token_ids: Sequence[int]) -> tuple[BlockRef, ...]:
-        return self.prefix_cache.match(request_id, token_ids)
+    def table_length(self, request_id: int) -> int:
+        entry = self._tables.get(request_id)
+        return 0 if entry is None else len(entry[0])
 
-    def cache_full_blocks(self, request_id: int,
-                          token_slice: Callable[[int, int], Sequence[int]],
-                          known_tokens: int | None = None) -> None:
-        """Publish the request's completed blocks; a block whose contents are
-        already cached elsewhere is swapped for the canonical copy.
-        ``known_tokens`` caps the publishable prefix (token ids past it are
-        still on the device)."""
-        if self._open is not None:
-            raise RuntimeError("publish prefix blocks only after successful writes")
-        table = self._tables[request_id]
-        valid = self.valid_token_count(request_id)
-        if known_tokens is not None:
-            valid = min(valid, known_tokens)
-        swaps = self.prefix_cache.publish(request_id, table, valid, token_slice)
-        if not swaps:
-            return
-        updated = list(table)
-        ids = self._ids[request_id].copy()
-        for index, canonical in swaps:
-            self.pool.retain(canonical)
-            self.pool.release(table[index])
-            updated[index] = canonical
-            ids[index] = canonical.block_id
-        self._tables[request_id] = tuple(updated)
-        self._ids[request_id] = ids
+    def block_table(self, request_id: int) -> tuple[BlockRef, ...]:
+        entry = self._tables.get(request_id)
+        if entry is None:
+            return ()
+        return tuple(BlockRef(int(b), int(g)) for b, g in zip(*entry))
 
-    def reset_prefix_cache(self) -> None:
-        if self._open is not None or self._tables:
-            raise RuntimeError("reset_prefix_cache requires an idle block manager")
-        self.prefix_cache.clear()
+    def valid_token_count(self, request_id: int) -> int:
+        return self._valid.get(request_id, 0)
 
-    def required_new_blocks(self, append: BlockAppend) -> int:
-        """Validate an append; number of blocks it adds to its table."""
-        if not isinstance(append, BlockAppend):
-            raise TypeError("appends must contain BlockAppend values")
-        table = self.block_table(append.request_id)
-        if append.prefix:
-            if table:
-                raise ValueError("prefix attachment requires a matched new request")
-            self.prefix_cache.validate_match(append.request_id, append.prefix)
-            valid, table = len(append.prefix) * self.block_size, append.prefix
-        else:
-            valid = self.valid_token_count(append.request_id)
-        if append.token_start != valid:
-            raise ValueError("token_start does not match valid KV length")
-        need = self._blocks_for(append.token_start + append.query_len) - len(table)
-        if need < 0:
-            raise RuntimeError("block table exceeds valid KV length")
-        return need
+    def blocks_for(self, tokens: int) -> int:
+        return -(-tokens // self.block_size)
 
-    def begin_plan(self, *, plan_id: int,
-                   appends: tuple[BlockAppend, ...]) -> BlockPlanTxn | None:
-        """Stage a step's appends; None (and nothing held) if the pool is short."""
+    # -- one step
+
+    def stage(self, plan_id: int, appends: Sequence[BlockAppend]) -> StepKV | None:
+        """Journal a step's appends; None (pool untouched) if blocks run out."""
         _check_non_negative_int("plan_id", plan_id)
         if self._open is not None:
-            raise RuntimeError("a KV transaction is already open")
+            raise RuntimeError(f"KV step {self._open.plan_id} is still open")
         appends = tuple(appends)
         if not appends:
-            raise ValueError("KV plan must contain at least one append")
-        seen: set[int] = set()
-        needs = []
-        for append in appends:
-            if append.request_id in seen:
-                raise ValueError("request appears twice in one KV plan")
-            seen.add(append.request_id)
-            needs.append(self.required_new_blocks(append))
-        prefixes = {a.request_id: a.prefix for a in appends if a.prefix}
-        # Pin prefix hits first so the reservation cannot evict them.
-        for prefix in prefixes.values():
-            for ref in prefix:
-                self.pool.retain(ref)
-        reservation = None
-        total = sum(needs)
-        if total:
-            reservation = self.pool.reserve(total)
-            if reservation is None:
-                self._unpin(prefixes)
-                return None
-        fresh = iter(reservation.block_refs if reservation else ())
-        tables, ids, slots, ends = {}, {}, {}, {}
-        bs = self.block_size
-        for append, need in zip(appends, needs):
-            rid = append.request_id
-            new = tuple(next(fresh) for _ in range(need))
+            raise ValueError("a KV step needs at least one append")
+        if len({a.request_id for a in appends}) != len(appends):
+            raise ValueError("a request may append only once per step")
+        bases = [self._base_of(a) for a in appends]
+        wanted = [self.blocks_for(a.token_start + a.query_len) - len(b[0])
+                  for a, b in zip(appends, bases)]
+        step = StepKV(plan_id, self)
+        pool = self.pool
+        for append in appends:  # pin hits before allocating, so none is evicted
             if append.prefix:
-                base = append.prefix
-                base_ids = np.fromiter((r.block_id for r in base), np.int64, len(base))
-            else:
-                base = self.block_table(rid)
-                base_ids = self._ids.get(rid, _EMPTY)
-            table = base + new
-            table_ids = (np.concatenate((base_ids, np.fromiter(
-                (r.block_id for r in new), np.int64, need))) if need else base_ids)
+                for ref in append.prefix:
+                    pool.hold(ref)
+                step._pins[append.request_id] = append.prefix
+        total = sum(wanted)
+        fresh = pool.allocate(total) if total else []
+        if fresh is None:
+            step._revert()
+            return None
+        step._fresh = fresh
+        bs, cursor = self.block_size, 0
+        for append, (ids, gens), need in zip(appends, bases, wanted):
+            new = np.asarray(fresh[cursor:cursor + need], dtype=np.int64)
+            cursor += need
+            if need:
+                ids = np.concatenate((ids, new))
+                gens = np.concatenate((gens, pool._gen[new]))
             end = append.token_start + append.query_len
             pos = np.arange(append.token_start, end, dtype=np.int64)
-            tables[rid], ids[rid], ends[rid] = table, table_ids, end
-            slots[rid] = table_ids[pos // bs] * bs + pos % bs
-        self._open = BlockPlanTxn(plan_id=plan_id, manager=self, reservation=reservation,
-                                  tables=tables, ids=ids, slots=slots, ends=ends,
-                                  prefixes=prefixes)
-        self._last = None
-        return self._open
+            step._rows[append.request_id] = (ids, gens, ids[pos // bs] * bs + pos % bs, end)
+        step.request_ids = tuple(a.request_id for a in appends)
+        self._open = step
+        return step
+
+    def _base_of(self, append: BlockAppend) -> tuple[np.ndarray, np.ndarray]:
+        """The table an append grows, checked against its start position."""
+        if not isinstance(append, BlockAppend):
+            raise TypeError("appends must be BlockAppend values")
+        rid = append.request_id
+        if append.prefix:
+            if rid in self._tables:
+                raise ValueError(f"request {rid} already owns blocks; prefix not attachable")
+            self.prefix_cache.check_hit(rid, append.prefix)
+            have = len(append.prefix) * self.block_size
+            base = (np.fromiter((r.block_id for r in append.prefix), np.int64),
+                    np.fromiter((r.generation for r in append.prefix), np.int64))
+        else:
+            have = self._valid.get(rid, 0)
+            base = self._tables.get(rid, (_NO_IDS, _NO_IDS))
+        if append.token_start != have:
+            raise ValueError(f"request {rid}: append starts at {append.token_start}, "
+                             f"KV holds {have} tokens")
+        if self.blocks_for(append.token_start + append.query_len) < len(base[0]):
+            raise RuntimeError(f"request {rid}: table longer than its KV")
+        return base
+
+    # -- per request
+
+    def publish_blocks(self, request_id: int,
+                       token_slice: Callable[[int, int], Sequence[int]],
+                       known_tokens: int) -> None:
+        """Index the request's newly full blocks whose token ids are known
+        (``known_tokens``); a block whose contents another block already
+        holds is swapped for that block."""
+        if self._open is not None:
+            raise RuntimeError("prefix blocks are published between steps")
+        entry = self._tables.get(request_id)
+        if entry is None:
+            return
+        full = min(self._valid.get(request_id, 0), known_tokens)
+        swaps = self.prefix_cache.index_blocks(request_id, entry, full, token_slice)
+        if not swaps:
+            return
+        ids, gens = entry[0].copy(), entry[1].copy()
+        for index, canonical in swaps:
+            self.pool.hold(canonical)
+            self.pool.drop(BlockRef(int(ids[index]), int(gens[index])))
+            ids[index], gens[index] = canonical.block_id, canonical.generation
+        self._tables[request_id] = (ids, gens)
 
     def release_request(self, request_id: int) -> None:
         if self._open is not None:
-            raise RuntimeError("cannot release blocks during a KV transaction")
-        table = self._tables.pop(request_id, ())
-        self._ids.pop(request_id, None)
+            raise RuntimeError("requests are released between steps")
+        entry = self._tables.pop(request_id, None)
         self._valid.pop(request_id, None)
-        self.prefix_cache.forget_request(request_id)
-        for ref in reversed(table):
-            self.pool.release(ref)
+        self.prefix_cache.drop_request(request_id)
+        if entry is not None:
+            for block, gen in zip(entry[0][::-1], entry[1][::-1]):
+                self.pool.drop(BlockRef(int(block), int(gen)))
 
-    def teardown(self, txn: BlockPlanTxn | None = None) -> None:
-        """Fail-stop: drop every ownership; partially written KV is never reused."""
-        current = self._open or self._last
-        if txn is not None and (txn._manager is not self or txn is not current):
-            raise ValueError("transaction is not the manager's current step")
-        if self._open is not None:
-            if self._open.state is BlockTxnState.PREPARED:
-                if self._open._reservation is not None:
-                    self.pool.rollback(self._open._reservation)
-                self._unpin(self._open._prefixes)
-            self._open._state = BlockTxnState.FAILED
-            self._open = None
+    def reset_prefix_cache(self) -> None:
+        if self._open is not None or self._tables:
+            raise RuntimeError("the prefix cache resets only with no request holding KV")
+        self.prefix_cache.reset()
+
+    def teardown(self) -> None:
+        """Fail-stop: undo or abandon the open step, release every table and
+        forget every cached prefix (partly written KV is never reused)."""
+        step, self._open = self._open, None
+        if step is not None:
+            if step.phase == StepKV.STAGED:
+                step._revert()
+            step.phase = StepKV.FAILED
         for request_id in tuple(self._tables):
             self.release_request(request_id)
-        self.reset_prefix_cache()
-        self._last = None
-        if txn is not None:
-            txn._state = BlockTxnState.FAILED
-
-    # -- transaction transitions
-
-    def _commit_before_dispatch(self, txn: BlockPlanTxn) -> None:
-        self._require(txn, BlockTxnState.PREPARED)
-        if txn._reservation is not None:
-            self.pool.commit(txn._reservation)
-        self._tables.update(txn._tables)
-        self._ids.update(txn._ids)
-        txn._state = BlockTxnState.DISPATCHED
-
-    def _complete_writes(self, txn: BlockPlanTxn) -> None:
-        self._require(txn, BlockTxnState.DISPATCHED)
-        self._valid.update(txn._ends)
-        self.prefix_cache.commit_matches(txn._prefixes)
-        txn._state = BlockTxnState.COMMITTED
-        self._open = None
-        self._last = txn
-
-    def _rollback(self, txn: BlockPlanTxn) -> None:
-        self._require(txn, BlockTxnState.PREPARED)
-        if txn._reservation is not None:
-            self.pool.rollback(txn._reservation)
-        self._unpin(txn._prefixes)
-        txn._state = BlockTxnState.ROLLED_BACK
-        self._open = None
-
-    def _unpin(self, prefixes: dict[int, tuple[BlockRef, ...]]) -> None:
-        for prefix in prefixes.values():
-            for ref in reversed(prefix):
-                self.pool.release(ref)
-
-    def _require(self, txn: BlockPlanTxn, state: BlockTxnState) -> None:
-        if self._open is not txn or txn.state is not state:
-            raise ValueError("KV transaction is not in the expected state")
-
-    def _blocks_for(self, tokens: int) -> int:
-        return -(-tokens // self.block_size)
-
-    def _slot_for_position(self, table: tuple[BlockRef, ...], position: int) -> int:
-        """Physical slot of a logical position (reference cache.py:696-711)."""
-        block, offset = divmod(position, self.block_size)
-        return table[block].block_id * self.block_size + offset
+        self._valid.clear()
+        self.prefix_cache.reset()

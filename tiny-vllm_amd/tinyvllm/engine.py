@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import time
 from collections.abc import Callable, Sequence
+from contextlib import contextmanager
 from dataclasses import dataclass, replace
 from typing import TYPE_CHECKING, Protocol
 
@@ -130,7 +131,7 @@ class Engine:
 
     def submit(self, prompt_token_ids: Sequence[int], sampling: SamplingParams, *,
                arrival_ns: int | None = None, request_id: int | None = None) -> int:
-        self._healthy()
+        self._usable()
         if self._generating:
             raise RuntimeError("generate() owns the engine until it returns")
         commands, next_id = self._stage((GenerateRequest(
@@ -168,7 +169,7 @@ class Engine:
         self._next_id = next_id
 
     def cancel(self, request_id: int) -> bool:
-        self._healthy()
+        self._usable()
         _check_non_negative_int("request_id", request_id)
         if request_id not in self._active or request_id in self._cancelling:
             return False
@@ -180,85 +181,82 @@ class Engine:
     # -------------------------------------------------------------- steps --
 
     def step(self, now_ns: int | None = None) -> EngineStepEvents:
-        self._healthy()
-        explicit = now_ns is not None
-        start = self._clock() if now_ns is None else now_ns
-        _check_non_negative_int("now_ns", start)
-        commands = tuple(self._commands)
-        self.scheduler.apply_commands(commands, start)
-        del self._commands[:len(commands)]
-        for command in commands:
-            if isinstance(command, CancelCommand):
-                self._cancelling.discard(command.request_id)
-        txn = self.scheduler.begin_step(start)
-        launched = None
-        accepted: tuple[tuple[int, int], ...] | None = None
+        """Plan and run one step. Serial: its tokens come back in its events.
+        Pipelined: it is launched, and the previous launch's tokens resolve."""
+        self._usable()
+        fixed = now_ns is not None
+        t0 = now_ns if fixed else self._clock()
+        _check_non_negative_int("now_ns", t0)
+        pending = tuple(self._commands)
+        self.scheduler.apply_commands(pending, t0)
+        del self._commands[:len(pending)]
+        self._cancelling.difference_update(
+            c.request_id for c in pending if isinstance(c, CancelCommand))
+        launched, accepted = None, None
+        txn = self.scheduler.begin_step(t0)
         if txn is not None:
-            try:
-                requests = tuple(self.scheduler.get_request(i.request_id)
-                                 for i in txn.plan.items)
-                batch = self.builder.prepare(
-                    txn.plan, requests, kv=txn.kv,
-                    pending_rows=self.scheduler.pending_sample_rows())
-                dispatch = start if explicit else max(start, self._clock())
-            except BaseException:
-                self.scheduler.rollback(txn)
-                raise
-            try:
-                self.scheduler.mark_dispatched(txn, dispatch)
-            except BaseException as exc:
-                self._fail_stop(exc)
-                raise
-            try:
-                if self._pipelined:
-                    launched = self.executor.launch(batch)
-                else:
-                    result = self.executor.execute(batch)
-            except BaseException as exc:
-                self._fail_stop(exc)
-                raise RuntimeError("executor failed; engine is failed") from exc
-            try:
-                done = dispatch if explicit else max(dispatch, self._clock())
-                if self._pipelined:
-                    self.scheduler.commit_launch(txn, done)
-                else:
-                    accepted = self.scheduler.commit_step(txn, result, done)
-            except BaseException as exc:
-                self._fail_stop(exc)
-                raise
+            launched, accepted = self._run(txn, t0, fixed)
         previous, self._in_flight = self._in_flight, launched
         if previous is not None:
-            accepted = self._resolve(previous, start if explicit else None)
-        try:
+            accepted = self._collect(previous, t0 if fixed else None)
+        with self._fatal():
             events = self._events(accepted)
-        except BaseException as exc:
-            self._fail_stop(exc)
-            raise
         if not self._active and self._in_flight is not None:
-            # Only rows of finished requests are in flight: drain them.
+            # What is still in flight belongs to finished requests: drain it.
             previous, self._in_flight = self._in_flight, None
-            self._resolve(previous, start if explicit else None)
+            self._collect(previous, t0 if fixed else None)
         return events
 
-    def _resolve(self, pending, now_ns: int | None) -> tuple[tuple[int, int], ...]:
+    def _later(self, t: int, fixed: bool) -> int:
+        return t if fixed else max(t, self._clock())
+
+    def _run(self, txn, t0: int, fixed: bool):
+        """Build, dispatch and execute (or launch) a staged step; returns
+        (launch handle, None) or (None, accepted tokens)."""
         try:
-            result = pending.result()
-        except BaseException as exc:
-            self._fail_stop(exc)
-            raise RuntimeError("executor failed; engine is failed") from exc
-        try:
-            return self.scheduler.resolve(result, self._clock() if now_ns is None
-                                          else now_ns)
-        except BaseException as exc:
-            self._fail_stop(exc)
+            requests = tuple(self.scheduler.get_request(i.request_id) for i in txn.plan.items)
+            batch = self.builder.prepare(txn.plan, requests, kv=txn.kv,
+                                         pending_rows=self.scheduler.pending_sample_rows())
+        except BaseException:
+            self.scheduler.rollback(txn)  # nothing was dispatched
             raise
+        when = self._later(t0, fixed)
+        with self._fatal():
+            self.scheduler.mark_dispatched(txn, when)
+        with self._fatal("executor failed; engine is failed"):
+            out = (self.executor.launch(batch) if self._pipelined
+                   else self.executor.execute(batch))
+        with self._fatal():
+            done = self._later(when, fixed)
+            if self._pipelined:
+                self.scheduler.commit_launch(txn, done)
+                return out, None
+            return None, self.scheduler.commit_step(txn, out, done)
+
+    def _collect(self, launched, now_ns: int | None) -> tuple[tuple[int, int], ...]:
+        """Wait for a launched step's tokens and hand them to the scheduler."""
+        with self._fatal("executor failed; engine is failed"):
+            result = launched.result()
+        with self._fatal():
+            return self.scheduler.resolve(result, self._clock() if now_ns is None else now_ns)
+
+    @contextmanager
+    def _fatal(self, message: str | None = None):
+        """Any failure inside is fail-stop; ``message`` re-raises it wrapped."""
+        try:
+            yield
+        except BaseException as exc:
+            self._fail_stop(exc)
+            if message is None:
+                raise
+            raise RuntimeError(message) from exc
 
     def has_unfinished(self) -> bool:
         return bool(self._active)
 
     def generate(self, requests: Sequence[GenerateRequest]) -> list[RequestOutput]:
         """Run a batch of requests to completion (arrivals honoured)."""
-        self._healthy()
+        self._usable()
         if self._generating or self.has_unfinished():
             raise RuntimeError("generate() requires an idle engine")
         commands, next_id = self._stage(tuple(requests))
@@ -307,44 +305,52 @@ class Engine:
 
     def reset_prefix_cache(self) -> None:
         """Drop reusable prefixes between workloads, without reallocating KV."""
-        self._healthy()
+        self._usable()
         if self._generating or self.has_unfinished():
             raise RuntimeError("reset_prefix_cache requires an idle engine")
         self.scheduler.block_manager.reset_prefix_cache()
 
     def close(self) -> None:
-        """Permanently dispose resources; pending requests are discarded."""
+        """Release the scheduler's KV and the executor for good; requests
+        still pending are dropped. Idempotent."""
         if self._closed:
             return
         if self._generating:
             raise RuntimeError("cannot close while generate() is running")
         self._closed = True
-        error = RuntimeError("engine cleanup failed")
-        self._dispose(error)
-        if getattr(error, "__notes__", None):
-            raise error
+        problems = self._teardown()
+        if problems:
+            raise RuntimeError("engine cleanup failed: " + "; ".join(problems))
 
-    def _healthy(self) -> None:
+    def _usable(self) -> None:
         if self._closed:
             raise RuntimeError("engine is closed")
         if self._failed is not None:
             raise RuntimeError(f"engine is failed: {self._failed}")
 
     def _fail_stop(self, cause: BaseException) -> None:
-        self._failed = f"{type(cause).__name__}: {cause}"
-        self._dispose(cause)
+        """After a failure past dispatch no KV state can be trusted: record
+        why, drop everything, and refuse further work."""
+        if self._failed is None:
+            self._failed = f"{type(cause).__name__}: {cause}"
+        for problem in self._teardown():
+            _note(cause, problem)
 
-    def _dispose(self, cause: BaseException) -> None:
+    def _teardown(self) -> list[str]:
+        """Forget queued work and shut the scheduler and executor down;
+        returns what failed to clean up (every part is attempted)."""
         self._in_flight = None
         self._commands.clear()
         self._active.clear()
         self._cancelling.clear()
-        for name, cleanup in (("scheduler", self.scheduler.shutdown),
-                              ("executor", self.executor.clear)):
+        problems = []
+        for part, shut in (("scheduler", self.scheduler.shutdown),
+                           ("executor", self.executor.clear)):
             try:
-                cleanup()
-            except BaseException as err:  # keep cleaning up the rest
-                _note(cause, f"{name} cleanup failed: {err!r}")
+                shut()
+            except BaseException as err:
+                problems.append(f"{part} cleanup failed: {err!r}")
+        return problems
 
 
 def _note(exc: BaseException, message: str) -> None:
