@@ -293,6 +293,12 @@ int tvllm_resolve_tokens(int64_t* tokens, const int64_t* src, const int64_t* pre
  * tvllm_paged_decode. Items with q_offsets[i+1] - q_offsets[i] <= 0 are
  * skipped. max_query_len bounds every item's query length (grid size).
  * cache_dtype / k_scale / v_scale as for tvllm_paged_decode.
+ * workspace: >= tvllm_paged_prefill_workspace_size(dtype, cache_dtype)
+ * bytes, 4-byte aligned, zero before the first call; every call leaves it
+ * zero. (A bf16 cache's V is converted to fp16 for the P.V products; a call
+ * that meets a V value of 65536 or more in magnitude, an infinity or a NaN
+ * raises a flag there and a second, exact launch recomputes it. Calls that
+ * share one workspace must be ordered on one stream.)
  * Replaces: CudaAttention._attend's per-row gather + SDPA for rows with
  * history (reference tinyvllm/runtime/attention.py:102-151, 235-285). */
 int tvllm_paged_prefill(const void* q, int64_t q_token_stride,
@@ -305,8 +311,14 @@ int tvllm_paged_prefill(const void* q, int64_t q_token_stride,
                         int64_t max_query_len, int64_t num_heads,
                         int64_t num_kv_heads, int64_t head_dim,
                         int64_t num_slots, int64_t block_size, float scale,
+                        void* workspace, int64_t workspace_bytes,
                         int dtype, int cache_dtype, float k_scale,
                         float v_scale, tvllm_stream_t stream);
+
+/* Bytes of workspace tvllm_paged_prefill needs: 8 for a bf16 query and
+ * cache (the fallback guard), 0 otherwise. No counterpart in the reference
+ * (its prefill path allocates nothing of the kind). */
+int64_t tvllm_paged_prefill_workspace_size(int dtype, int cache_dtype);
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = load_kernels()
     for name in sorted(declared_symbols()):
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
-    assert lib.tvllm_abi_version() == 3
+    assert lib.tvllm_abi_version() == 4
     assert lib.tvllm_last_error() == b""
 
 

@@ -193,6 +193,49 @@ def test_prefill_chunks_with_history(device, heads, kv_heads, items, bs):
     assert_bf16_close(out.cpu(), expect)
 
 
+def test_prefill_v_beyond_fp16_range_takes_the_exact_path(device):
+    """P.V runs on fp16 MFMAs with V converted from bf16; V values of 65536
+    or more (or inf/NaN) make the call recompute on bf16 MFMAs. Both calls
+    match the oracle, and the fallback guard is back to zero after each."""
+    from helpers import assert_within_ulp
+    from tinyvllm.kernels import paged_prefill as PP
+    from tinyvllm.kernels.paged_prefill import paged_prefill_attention
+    from tinyvllm.runtime.contracts import MultiQueryMetadata
+
+    g = torch.Generator().manual_seed(41)
+    heads, kv_heads, d, bs, pool = 16, 8, 128, 16, 128
+    items = [(700, 300), (64, 64)]
+    k = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(pool, generator=g).tolist()
+    blocks, boff, qoff = [], [0], [0]
+    for ctx, ql in items:
+        n = math.ceil(ctx / bs)
+        blocks += perm[boff[-1]:boff[-1] + n]
+        boff.append(boff[-1] + n)
+        qoff.append(qoff[-1] + ql)
+    q = torch.randn(qoff[-1], heads, d, generator=g).to(torch.bfloat16)
+    meta_cpu = [torch.tensor(x) for x in (qoff, blocks, boff, [c for c, _ in items])]
+    meta = MultiQueryMetadata(*(t.to(device) for t in meta_cpu),
+                              max_query_len=max(ql for _, ql in items))
+    for huge in (True, False):
+        v = torch.randn(pool * bs, kv_heads, d, generator=g)
+        if huge:  # a few values fp16 cannot hold, in the first item's pages
+            rows = torch.tensor(blocks[:3]) * bs + 5
+            v[rows, 2, 7] = 3.0e5
+            v[rows[:1], 5, 100] = -70000.0
+        v = v.to(torch.bfloat16)
+        expect = torch.zeros_like(q)
+        OA.prefill_attention(q, k, v, *meta_cpu, bs, d ** -0.5, expect)
+        cache = _Cache(k.to(device), v.to(device), bs)
+        out = torch.zeros(q.shape, dtype=q.dtype, device=device)
+        paged_prefill_attention(q.to(device), cache, 0, meta, out, scale=d ** -0.5)
+        torch.cuda.synchronize()
+        print(f"prefill huge={huge}", flush=True)
+        assert_within_ulp(out.cpu(), expect, ulps=2.0)
+        guard = PP._GUARDS[(out.device, torch.cuda.current_stream(out.device).cuda_stream)]
+        assert int(guard.count_nonzero()) == 0
+
+
 # ----------------------------------------------------------------- pointwise --
 
 def _c2_inputs(dtype=torch.bfloat16):

@@ -22,10 +22,13 @@
 //    never moves between lanes.
 //  * O^T += V^T P^T (A = V^T from an LDS copy that staging stores transposed,
 //    with the tokens of each 16-token step ordered the way the MFMA k index
-//    visits them; B = the lane's probabilities as two storage-type terms, P
-//    rounded and the rounded remainder, one MFMA each, so the product keeps
-//    about 16 bits of P - a single rounded P leaves ~1e-3 relative error in
-//    the output, the size of the whole bf16 tolerance).
+//    visits them; B = the lane's probabilities) on fp16 MFMAs: P rounded to
+//    fp16 keeps 11 bits (a bf16 P would leave ~1e-3 relative error in the
+//    output, the whole bf16 tolerance), and a bf16 cache's V is converted to
+//    fp16 as it is staged, which is exact below 65536. A workgroup that meets
+//    a V value beyond that (or an infinity or NaN) redoes its tiles on bf16
+//    MFMAs with P as a rounded value plus its rounded remainder (about 16
+//    bits of P, two MFMAs per product).
 //    The O^T accumulator of a lane belongs to its own query: the softmax
 //    rescale and the final 1/l are lane-local.
 //  * online softmax in base 2 (v_exp_f32) with one running (max, sum) per
@@ -37,6 +40,7 @@
 // start first.
 #include "common.h"
 
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -80,6 +84,9 @@ __device__ __forceinline__ int vt_pos(int tq) {
 // tiles skip the rescale of the output accumulators.
 constexpr float kSlack = 8.f;
 
+// Workgroups of the exact fallback launch (each loops over tasks).
+constexpr int64_t kExactWorkgroups = 32;
+
 template <typename T>
 struct PrefillArgs {
     const T* q;
@@ -95,6 +102,7 @@ struct PrefillArgs {
     int heads, kv_heads, block_size, block_shift, q_tiles, grid;
     float scale_log2;  // softmax scale * log2(e) (* k_scale for an FP8 cache)
     float v_scale;     // FP8 cache: V dequantisation scale (1 otherwise)
+    int* guard;        // bf16 cache: [V out of fp16 range, exact-launch arrivals]
 };
 
 __device__ __forceinline__ float as_f(uint32_t x) { return __uint_as_float(x); }
@@ -112,7 +120,11 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 // F8: K/V rows are FP8 E4M3 bytes; staging loads 8 bytes per 8-element
 // piece and widens them exactly to T before the LDS store.
-template <typename T, int W, bool QUAD, bool F8>
+// EXACT: the bf16 fallback launch. It runs after the main launch on the same
+// stream; its workgroups do nothing unless the main launch raised guard[0].
+// Every workgroup counts its arrival in guard[1] after reading guard[0]; the
+// last one clears both words, so the guard is zero between calls.
+template <typename T, int W, bool QUAD, bool F8, bool EXACT>
 __global__ void __launch_bounds__(64 * W, 8 / W)  // two waves per SIMD
 paged_prefill_d128(PrefillArgs<T> a) {
     using SU = std::conditional_t<F8, uint2, U16x8>;  // one staged piece
@@ -124,6 +136,7 @@ paged_prefill_d128(PrefillArgs<T> a) {
     constexpr int JPT = JOBS / NTH;
     __shared__ __align__(16) uint16_t ks[2][K_TILE];
     __shared__ __align__(16) uint16_t vt[2][V_TILE];
+    __shared__ int v_out_of_range;  // main launch: a V value left fp16 range
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -131,323 +144,440 @@ paged_prefill_d128(PrefillArgs<T> a) {
     const int col = lane & 31;
     const int half = lane >> 5;
 
-    // XCD-aware order: hardware deals block ids round-robin over 8 XCDs;
-    // give each XCD a contiguous range of logical work.
-    int bid = blockIdx.x;
-    if (a.grid % 8 == 0) bid = (bid % 8) * (a.grid / 8) + bid / 8;
-    const int tile = a.q_tiles - 1 - bid % a.q_tiles;  // most keys first
-    const int ih = bid / a.q_tiles;
-    const int h = ih % a.heads;
-    const int item = ih / a.heads;
-    const int kvh = h / (a.heads / a.kv_heads);
-
-    const int64_t q_begin = a.q_offsets[item];
-    const int64_t q_len = a.q_offsets[item + 1] - q_begin;
-    const int64_t q0 = int64_t(tile) * BQ;
-    if (q_len <= 0 || q0 >= q_len) return;  // uniform per workgroup
-    const int64_t ctx = a.context_lens[item];
-    const int64_t first_pos = ctx - q_len;  // absolute position of query 0
-    const int64_t table = a.block_offsets[item];
-    const int64_t kv_end = min(ctx, first_pos + min(q_len - 1, q0 + BQ - 1) + 1);
-
-    // This wave's queries: wq0 + col.
-    const int64_t wq0 = q0 + int64_t(wave) * 32;
-    const bool wave_active = wq0 < q_len;
-    const int64_t wave_kv_end = min(kv_end, first_pos + min(q_len - 1, wq0 + 31) + 1);
-    const int64_t wave_first_pos = first_pos + wq0;
-    const int64_t qi_lane = min(wq0 + col, q_len - 1);
-    const int64_t my_pos = first_pos + qi_lane;
-
-    U16x8 qv[8];  // B operand of k-step c: dims 16c + 8*half .. +7
-    {
-        const T* qrow = a.q + (q_begin + qi_lane) * a.qts + h * a.qhs + 8 * half;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) qv[c] = *reinterpret_cast<const U16x8*>(qrow + 16 * c);
+    if constexpr (EXACT) {
+        __shared__ int redo;
+        if (tid == 0) {
+            const int raised = __hip_atomic_load(&a.guard[0], __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+            __threadfence();  // the read completes before the arrival is counted
+            if (atomicAdd(&a.guard[1], 1) == int(gridDim.x) - 1) {  // the last arrival
+                __hip_atomic_store(&a.guard[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&a.guard[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            redo = raised;
+        }
+        __syncthreads();
+        if (!redo) return;  // uniform
     }
 
-    f32x16 o[4];  // O^T: lane = (dims 32n + 8g + 4*half + i, query col)
-#pragma unroll
-    for (int n = 0; n < 4; ++n) o[n] = f32x16{};
-    float m_run = -INFINITY, l_run = 0.f;
+    // One task = one (item, head, query tile). The main launch has a
+    // workgroup per task; the exact launch, needed only for inputs beyond
+    // fp16's range, loops a few workgroups over all tasks.
+    auto task = [&](int bid) {
+        // XCD-aware order: hardware deals block ids round-robin over 8 XCDs;
+        // give each XCD a contiguous range of logical work.
+        if (a.grid % 8 == 0) bid = (bid % 8) * (a.grid / 8) + bid / 8;
+        const int tile = a.q_tiles - 1 - bid % a.q_tiles;  // most keys first
+        const int ih = bid / a.q_tiles;
+        const int h = ih % a.heads;
+        const int item = ih / a.heads;
+        const int kvh = h / (a.heads / a.kv_heads);
 
-    // Staging: job = (K|V, piece, token quad); 4 tokens x 16 bytes each.
-    const int bs = a.block_size;
-    auto job_coords = [&](int r, bool& is_v, int& tq, int& piece) {
-        const int job = tid + r * NTH;
-        is_v = job >> 8;
-        // K: piece fastest (a token row per 16 lanes, conflict-free 16-byte
-        // LDS writes); V: token quad fastest (conflict-free transposed writes).
-        tq = is_v ? (job & 15) : ((job >> 4) & 15);
-        piece = is_v ? ((job >> 4) & 15) : (job & 15);
-    };
-    // Token positions fit in 32 bits (contexts < 2^31) and slots in 32 bits
-    // (checked on the host); the element offset of a slot is formed in 64 bits.
-    const int end1 = int(kv_end) - 1;
-    const uint32_t slot_elems = uint32_t(a.kv_heads) * D;
-    // QUAD (power-of-two pages of >= 4 tokens): a job's 4 tokens share a
-    // page, so one block id serves all four. A template parameter, not a
-    // branch: two load paths in the loop would make the wait-count pass
-    // treat the prefetch registers as possibly pending and stall on them.
-    constexpr bool quad_pages = QUAD;
-    // Staging is branch-free: tiles past the end (or before the start, in the
-    // prologue) load clamped, valid rows and store them into a buffer nobody
-    // reads again, so every load is consumed on every path and the wait-count
-    // pass never has to assume a prefetch register is still in flight.
-    // Staging runs ahead of the math: at iteration i the K rows of tile i+1
-    // (for S(i+1)) and the V rows of tile i (for P.V) are in LDS, and this
-    // iteration writes K(i+2) and V(i+1) from registers loaded during the
-    // previous one. `lead` is that distance for the job's kind.
-    auto lead_of = [](bool is_v) { return is_v ? 1 : 2; };
-    auto load_ids = [&](int tile_base, uint32_t (&ids)[JPT][4]) {
-#pragma unroll
-        for (int r = 0; r < JPT; ++r) {
-            bool is_v;
-            int tq, piece;
-            job_coords(r, is_v, tq, piece);
-            const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
-            if constexpr (quad_pages) {
-                ids[r][0] = uint32_t(a.blocks[table + (min(t0 + 4 * tq, end1) >> a.block_shift)]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    ids[r][e] = uint32_t(a.blocks[table + min(t0 + 4 * tq + e, end1) / bs]);
-            }
+        const int64_t q_begin = a.q_offsets[item];
+        const int64_t q_len = a.q_offsets[item + 1] - q_begin;
+        const int64_t q0 = int64_t(tile) * BQ;
+        if (q_len <= 0 || q0 >= q_len) return;  // uniform per workgroup
+        const int64_t ctx = a.context_lens[item];
+        const int64_t first_pos = ctx - q_len;  // absolute position of query 0
+        const int64_t table = a.block_offsets[item];
+        const int64_t kv_end = min(ctx, first_pos + min(q_len - 1, q0 + BQ - 1) + 1);
+
+        // This wave's queries: wq0 + col.
+        const int64_t wq0 = q0 + int64_t(wave) * 32;
+        const bool wave_active = wq0 < q_len;
+        const int64_t wave_kv_end = min(kv_end, first_pos + min(q_len - 1, wq0 + 31) + 1);
+        const int64_t wave_first_pos = first_pos + wq0;
+        const int64_t qi_lane = min(wq0 + col, q_len - 1);
+        const int64_t my_pos = first_pos + qi_lane;
+
+        U16x8 qv[8];  // B operand of k-step c: dims 16c + 8*half .. +7
+        {
+            const T* qrow = a.q + (q_begin + qi_lane) * a.qts + h * a.qhs + 8 * half;
+    #pragma unroll
+            for (int c = 0; c < 8; ++c) qv[c] = *reinterpret_cast<const U16x8*>(qrow + 16 * c);
         }
-    };
-    auto load_tile = [&](int tile_base, const uint32_t (&ids)[JPT][4], SU (&stage)[JPT][4]) {
-#pragma unroll
-        for (int r = 0; r < JPT; ++r) {
-            bool is_v;
-            int tq, piece;
-            job_coords(r, is_v, tq, piece);
-            const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
-            const char* src = static_cast<const char*>(is_v ? a.v : a.k) +
-                              int64_t(kvh * D + piece * 8) * EB;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = min(t0 + 4 * tq + e, end1);
-                uint32_t slot;
-                if constexpr (quad_pages) slot = ids[r][0] * uint32_t(bs) + uint32_t(t & (bs - 1));
-                else slot = ids[r][e] * uint32_t(bs) + uint32_t(t % bs);
-                stage[r][e] = *reinterpret_cast<const SU*>(src + uint64_t(slot) * slot_elems * EB);
-            }
+
+        // A bf16 cache's V is converted to fp16 while it is staged (exact below
+        // 65536 in magnitude); a workgroup that meets a larger, infinite or NaN
+        // V value redoes its work in the exact bf16 mode.
+        constexpr bool kConvertV = std::is_same_v<T, __bf16> && !F8 && !EXACT;
+        if constexpr (kConvertV) {
+            if (tid == 0) v_out_of_range = 0;
+            __syncthreads();  // before any staging store may raise it
         }
-    };
-    auto store_tile = [&](int tile_base, const SU (&raw)[JPT][4]) {
-#pragma unroll
-        for (int r = 0; r < JPT; ++r) {
-            bool is_v;
-            int tq, piece;
-            job_coords(r, is_v, tq, piece);
-            const int buf = (tile_base + lead_of(is_v)) & 1;
-            U16x8 pc[4];  // the job's four token pieces as T elements
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if constexpr (F8) pc[e] = fp8x8_widen<T>(raw[r][e]);
-                else pc[e] = raw[r][e];
-            }
-            if (is_v) {
-                // V^T: dim row (piece*8 + dd), the quad's 4 tokens -> one 8-byte write;
-                // v_perm picks the low (even dd) or high (odd dd) halves of two words.
-#pragma unroll
-                for (int dd = 0; dd < 8; ++dd) {
-                    const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-                    uint2 w;
-                    w.x = __builtin_amdgcn_perm(pc[1].w[dd >> 1], pc[0].w[dd >> 1], sel);
-                    w.y = __builtin_amdgcn_perm(pc[3].w[dd >> 1], pc[2].w[dd >> 1], sel);
-                    *reinterpret_cast<uint2*>(&vt[buf][(piece * 8 + dd) * V_LD + vt_pos(tq)]) = w;
+
+        const int bs = a.block_size;
+        // Staging: job = (K|V, piece, token quad); 4 tokens x 16 bytes each.
+        auto job_coords = [&](int r, bool& is_v, int& tq, int& piece) {
+            const int job = tid + r * NTH;
+            is_v = job >> 8;
+            // K: piece fastest (a token row per 16 lanes, conflict-free 16-byte
+            // LDS writes); V: token quad fastest (conflict-free transposed writes).
+            tq = is_v ? (job & 15) : ((job >> 4) & 15);
+            piece = is_v ? ((job >> 4) & 15) : (job & 15);
+        };
+        // Token positions fit in 32 bits (contexts < 2^31) and slots in 32 bits
+        // (checked on the host); the element offset of a slot is formed in 64 bits.
+        const int end1 = int(kv_end) - 1;
+        const uint32_t slot_elems = uint32_t(a.kv_heads) * D;
+        // QUAD (power-of-two pages of >= 4 tokens): a job's 4 tokens share a
+        // page, so one block id serves all four. A template parameter, not a
+        // branch: two load paths in the loop would make the wait-count pass
+        // treat the prefetch registers as possibly pending and stall on them.
+        constexpr bool quad_pages = QUAD;
+        // Staging is branch-free: tiles past the end (or before the start, in the
+        // prologue) load clamped, valid rows and store them into a buffer nobody
+        // reads again, so every load is consumed on every path and the wait-count
+        // pass never has to assume a prefetch register is still in flight.
+        // Staging runs ahead of the math: at iteration i the K rows of tile i+1
+        // (for S(i+1)) and the V rows of tile i (for P.V) are in LDS, and this
+        // iteration writes K(i+2) and V(i+1) from registers loaded during the
+        // previous one. `lead` is that distance for the job's kind.
+        auto lead_of = [](bool is_v) { return is_v ? 1 : 2; };
+        auto load_ids = [&](int tile_base, uint32_t (&ids)[JPT][4]) {
+    #pragma unroll
+            for (int r = 0; r < JPT; ++r) {
+                bool is_v;
+                int tq, piece;
+                job_coords(r, is_v, tq, piece);
+                const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
+                if constexpr (quad_pages) {
+                    ids[r][0] = uint32_t(a.blocks[table + (min(t0 + 4 * tq, end1) >> a.block_shift)]);
+                } else {
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        ids[r][e] = uint32_t(a.blocks[table + min(t0 + 4 * tq + e, end1) / bs]);
                 }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    *reinterpret_cast<U16x8*>(&ks[buf][(4 * tq + e) * K_LD + piece * 8]) =
-                        pc[e];
             }
-        }
-    };
-
-    // ---- per-wave math on one tile j ----------------------------------
-    f32x16 sc[2];  // raw S^T of the tile: sc[tb][v] = token 32tb + 8(v/4) + 4*half + v%4
-    U16x8 pb[4];   // P of the tile, k-step st: token 16st + 8jj + 4*half + i at k = 4jj + i
-    U16x8 pr[4];   // P - pb (the rounding remainder), rounded, same layout
-    auto scores = [&](int j) {
-        const uint16_t* kt = ks[j & 1];
-        sc[0] = f32x16{};
-        sc[1] = f32x16{};
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb) {
-                const U16x8 kk = *reinterpret_cast<const U16x8*>(
-                    &kt[(32 * tb + col) * K_LD + 16 * c + 8 * half]);
-                sc[tb] = mfma32<T>(kk, qv[c], sc[tb]);
-            }
-    };
-    auto softmax = [&](int j) {
-        const int64_t t0 = int64_t(j) * BK;
-        if (t0 + BK - 1 > wave_first_pos) {  // tile crosses the diagonal
-            // Keys past this lane's query: offset within the tile > lim.
-            const int lim = int(my_pos - t0) - 4 * half;
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    if (32 * tb + 8 * (v >> 2) + (v & 3) > lim) sc[tb][v] = -INFINITY;
-        }
-        // Maxima and sums in four independent chains (a single chain of 32
-        // dependent instructions stalls the wave).
-        float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) mx[v & 3] = fmaxf(mx[v & 3], sc[tb][v]);
-        const float cmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
-        const float cm = pair_max(cmax) * a.scale_log2;  // scale > 0
-        const bool grow = cm > m_run + kSlack;  // also: first finite max
-        float alpha = 1.f;
-        if (grow) {
-            alpha = __builtin_amdgcn_exp2f(m_run - cm);
-            m_run = cm;
-        }
-        if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform
-            l_run *= alpha;
-#pragma unroll
-            for (int n = 0; n < 4; ++n) o[n] *= alpha;
-        }
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float ps[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            float p[16];
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tb][v], a.scale_log2, -m_use));
-                ps[v & 3] += p[v];
-            }
-#pragma unroll
-            for (int sh = 0; sh < 2; ++sh)
-#pragma unroll
+        };
+        auto load_tile = [&](int tile_base, const uint32_t (&ids)[JPT][4], SU (&stage)[JPT][4]) {
+    #pragma unroll
+            for (int r = 0; r < JPT; ++r) {
+                bool is_v;
+                int tq, piece;
+                job_coords(r, is_v, tq, piece);
+                const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
+                const char* src = static_cast<const char*>(is_v ? a.v : a.k) +
+                                  int64_t(kvh * D + piece * 8) * EB;
+    #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float p0 = p[8 * sh + 2 * e], p1 = p[8 * sh + 2 * e + 1];
-                    const uint32_t hw = pack2<T>(p0, p1);
-                    pb[2 * tb + sh].w[e] = hw;
-                    pr[2 * tb + sh].w[e] = pack2<T>(p0 - half_lo<T>(hw), p1 - half_hi<T>(hw));
+                    const int t = min(t0 + 4 * tq + e, end1);
+                    uint32_t slot;
+                    if constexpr (quad_pages) slot = ids[r][0] * uint32_t(bs) + uint32_t(t & (bs - 1));
+                    else slot = ids[r][e] * uint32_t(bs) + uint32_t(t % bs);
+                    stage[r][e] = *reinterpret_cast<const SU*>(src + uint64_t(slot) * slot_elems * EB);
                 }
+            }
+        };
+        // EXACT: V^T staged as the cache's own bf16 values; otherwise as fp16.
+        auto store_tile = [&](int tile_base, const SU (&raw)[JPT][4]) {
+            constexpr bool convert = kConvertV;
+    #pragma unroll
+            for (int r = 0; r < JPT; ++r) {
+                bool is_v;
+                int tq, piece;
+                job_coords(r, is_v, tq, piece);
+                const int buf = (tile_base + lead_of(is_v)) & 1;
+                U16x8 pc[4];  // the job's four token pieces, as staged
+                typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+                u16x2_t wide = {0, 0};  // largest |V| bit patterns (v_pk_max_u16)
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (F8) {
+                        pc[e] = is_v ? fp8x8_widen<_Float16>(raw[r][e]) : fp8x8_widen<T>(raw[r][e]);
+                    } else {
+                        pc[e] = raw[r][e];
+                        if constexpr (convert) {
+                            if (is_v) {
+    #pragma unroll
+                                for (int w = 0; w < 4; ++w) {
+                                    const uint32_t b = pc[e].w[w];
+                                    wide = __builtin_elementwise_max(
+                                        wide, __builtin_bit_cast(u16x2_t, b & 0x7fff7fffu));
+                                    pc[e].w[w] = pack2<_Float16>(half_lo<T>(b), half_hi<T>(b));
+                                }
+                            }
+                        }
+                    }
+                }
+                if constexpr (convert) {
+                    // bf16 0x4780 = 65536: the first magnitude fp16 cannot hold
+                    // (infinities and NaNs compare above it too).
+                    if (is_v && (wide[0] >= 0x4780u || wide[1] >= 0x4780u))
+                        v_out_of_range = 1;
+                }
+                if (is_v) {
+                    // V^T: dim row (piece*8 + dd), the quad's 4 tokens -> one 8-byte write;
+                    // v_perm picks the low (even dd) or high (odd dd) halves of two words.
+    #pragma unroll
+                    for (int dd = 0; dd < 8; ++dd) {
+                        const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
+                        uint2 w;
+                        w.x = __builtin_amdgcn_perm(pc[1].w[dd >> 1], pc[0].w[dd >> 1], sel);
+                        w.y = __builtin_amdgcn_perm(pc[3].w[dd >> 1], pc[2].w[dd >> 1], sel);
+                        *reinterpret_cast<uint2*>(&vt[buf][(piece * 8 + dd) * V_LD + vt_pos(tq)]) = w;
+                    }
+                } else {
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        *reinterpret_cast<U16x8*>(&ks[buf][(4 * tq + e) * K_LD + piece * 8]) =
+                            pc[e];
+                }
+            }
+        };
+
+        const int ntiles = int((kv_end + BK - 1) / BK);
+        const int wt = wave_active ? int((wave_kv_end + BK - 1) / BK) : 0;  // this wave's tiles
+        // Ping-pong: waves 0..W/2-1 ("matrix first") and W/2..W-1 ("vector
+        // first") pair up on each SIMD. Every tile is split in two halves at a
+        // barrier; in each half one wave of a pair issues MFMAs (P.V of tile i
+        // and S of tile i+1) while the other runs exponentials, so the matrix
+        // cores and the vector ALUs work at the same time.
+        const bool matrix_first = wave < W / 2;
+        // With eight waves, waves 0-3 own the K staging jobs and waves 4-7 the V
+        // jobs; each group stages in the half where it issues MFMAs, so staging
+        // runs alongside the other group's exponentials instead of in a phase of
+        // its own. K(i+2) goes to the buffer of K(i), V(i+1) to that of V(i-1):
+        // both were last read before the previous barrier, and neither buffer is
+        // read in the half that writes it.
+        constexpr bool split_staging = W == 8;
+
+        f32x16 o[4];  // O^T: lane = (dims 32n + 8g + 4*half + i, query col)
+        float m_run, l_run;
+
+        // The pass over the key tiles. EXACT: P.V on bf16 MFMAs with P as the
+        // rounded value plus the rounded remainder (about 16 bits of P), V as
+        // cached. Otherwise P.V on fp16 MFMAs: P rounded to fp16 (11 bits; a
+        // single bf16 P would leave ~1e-3 relative error, the whole tolerance)
+        // and V converted to fp16 (exact for a bf16 or FP8 cache in range).
+        {
+            using PV = std::conditional_t<EXACT, T, _Float16>;
+    #pragma unroll
+            for (int n = 0; n < 4; ++n) o[n] = f32x16{};
+            m_run = -INFINITY;
+            l_run = 0.f;
+
+            // ---- per-wave math on one tile j ----------------------------------
+            f32x16 sc[2];  // raw S^T of the tile: sc[tb][v] = token 32tb + 8(v/4) + 4*half + v%4
+            U16x8 pb[4];   // P of the tile, k-step st: token 16st + 8jj + 4*half + i at k = 4jj + i
+            U16x8 pr[4];   // EXACT: P - pb (the rounding remainder), same layout
+            // LDS operands are read ahead of the MFMAs that use them (K two
+            // k-steps ahead, V one 16-token step ahead), so a read's latency
+            // hides behind the matrix instructions already issued.
+            auto scores = [&](int j) {
+                const uint16_t* kt = ks[j & 1];
+                sc[0] = f32x16{};
+                sc[1] = f32x16{};
+                constexpr int KB = EXACT ? 1 : 3;  // k-steps read ahead (fewer in the rare exact pass)
+                U16x8 kk[KB][2];
+                auto load_k = [&](int c, U16x8 (&dst)[2]) {
+    #pragma unroll
+                    for (int tb = 0; tb < 2; ++tb)
+                        dst[tb] = *reinterpret_cast<const U16x8*>(
+                            &kt[(32 * tb + col) * K_LD + 16 * c + 8 * half]);
+                };
+    #pragma unroll
+                for (int c = 0; c < KB - 1; ++c) load_k(c, kk[c]);
+    #pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    if (c + KB - 1 < 8) load_k(c + KB - 1, kk[(c + KB - 1) % KB]);
+    #pragma unroll
+                    for (int tb = 0; tb < 2; ++tb) sc[tb] = mfma32<T>(kk[c % KB][tb], qv[c], sc[tb]);
+                }
+            };
+            auto softmax = [&](int j) {
+                const int64_t t0 = int64_t(j) * BK;
+                if (t0 + BK - 1 > wave_first_pos) {  // tile crosses the diagonal
+                    // Keys past this lane's query: offset within the tile > lim.
+                    const int lim = int(my_pos - t0) - 4 * half;
+    #pragma unroll
+                    for (int tb = 0; tb < 2; ++tb)
+    #pragma unroll
+                        for (int v = 0; v < 16; ++v)
+                            if (32 * tb + 8 * (v >> 2) + (v & 3) > lim) sc[tb][v] = -INFINITY;
+                }
+                // Maxima and sums in four independent chains (a single chain of 32
+                // dependent instructions stalls the wave).
+                float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    #pragma unroll
+                for (int tb = 0; tb < 2; ++tb)
+    #pragma unroll
+                    for (int v = 0; v < 16; ++v) mx[v & 3] = fmaxf(mx[v & 3], sc[tb][v]);
+                const float cmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+                const float cm = pair_max(cmax) * a.scale_log2;  // scale > 0
+                const bool grow = cm > m_run + kSlack;  // also: first finite max
+                float alpha = 1.f;
+                if (grow) {
+                    alpha = __builtin_amdgcn_exp2f(m_run - cm);
+                    m_run = cm;
+                }
+                if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform
+                    l_run *= alpha;
+    #pragma unroll
+                    for (int n = 0; n < 4; ++n) o[n] *= alpha;
+                }
+                const float m_use = m_run == -INFINITY ? 0.f : m_run;
+                float ps[4] = {0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+                for (int tb = 0; tb < 2; ++tb) {
+                    float p[16];
+    #pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[tb][v], a.scale_log2, -m_use));
+    #pragma unroll
+                    for (int sh = 0; sh < 2; ++sh)
+    #pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float p0 = p[8 * sh + 2 * e], p1 = p[8 * sh + 2 * e + 1];
+                            const uint32_t hw = pack2<PV>(p0, p1);
+                            pb[2 * tb + sh].w[e] = hw;
+                            if constexpr (EXACT) {
+                                pr[2 * tb + sh].w[e] =
+                                    pack2<PV>(p0 - half_lo<PV>(hw), p1 - half_hi<PV>(hw));
+                                ps[e] += p0 + p1;
+                            } else {
+                                // The denominator sums the fp16 weights P.V uses.
+                                typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+                                const h2_t ones = {1.f16, 1.f16};
+                                ps[e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, hw), ones,
+                                                               ps[e], false);
+                            }
+                        }
+                }
+                l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+            };
+            auto pv = [&](int j) {  // O^T += V^T P^T over four 16-token steps
+                const uint16_t* vtt = vt[j & 1];
+                constexpr int VB = EXACT ? 1 : 2;
+                U16x8 va[VB][4];
+                auto load_v = [&](int st, U16x8 (&dst)[4]) {
+    #pragma unroll
+                    for (int n = 0; n < 4; ++n)
+                        dst[n] = *reinterpret_cast<const U16x8*>(
+                            &vtt[(32 * n + col) * V_LD + 16 * st + 8 * half]);
+                };
+                if constexpr (VB > 1) load_v(0, va[0]);
+    #pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    if constexpr (VB > 1) {
+                        if (st + 1 < 4) load_v(st + 1, va[(st + 1) % VB]);
+                    } else {
+                        load_v(st, va[0]);
+                    }
+                    if constexpr (EXACT) {  // remainders first: four accumulators apart
+    #pragma unroll
+                        for (int n = 0; n < 4; ++n) o[n] = mfma32<PV>(va[st % VB][n], pr[st], o[n]);
+                    }
+    #pragma unroll
+                    for (int n = 0; n < 4; ++n) o[n] = mfma32<PV>(va[st % VB][n], pb[st], o[n]);
+                }
+            };
+
+            // Prologue: K(0), K(1), V(0) into LDS, and K(2), V(1) into registers,
+            // with the three tiles' block ids and rows fetched concurrently. (The
+            // first staging call also writes V(0) into the spare V buffer.)
+            SU stage[JPT][4];
+            uint32_t ids[JPT][4];
+            {
+                SU st0[JPT][4], st1[JPT][4];
+                uint32_t id0[JPT][4], id1[JPT][4];
+                load_ids(-2, id0);
+                load_ids(-1, id1);
+                load_ids(0, ids);
+                load_tile(-2, id0, st0);
+                load_tile(-1, id1, st1);
+                load_tile(0, ids, stage);
+                load_ids(1, ids);
+                store_tile(-2, st0);
+                store_tile(-1, st1);
+            }
+            __syncthreads();
+            if (wt > 0) {
+                scores(0);
+                if (matrix_first) softmax(0);
+            }
+            auto stage_next = [&](int i) {
+                store_tile(i, stage);
+                load_tile(i + 1, ids, stage);
+                load_ids(i + 2, ids);
+            };
+            // K(2) overwrites K(0), which every wave read above in scores(0).
+            if constexpr (split_staging) __syncthreads();
+            // A wave's MFMA half with its staging in one basic block (the common
+            // case i + 1 < wt), so the scheduler can slot the staging instructions
+            // between the matrix instructions.
+            auto matrix_half = [&](int i) {
+                if (i + 1 < wt) {
+                    pv(i);
+                    scores(i + 1);
+                    if constexpr (split_staging) stage_next(i);
+                } else if (i < wt) {
+                    pv(i);
+                    if constexpr (split_staging) stage_next(i);
+                } else if constexpr (split_staging) {
+                    stage_next(i);
+                }
+            };
+            for (int i = 0; i < ntiles; ++i) {
+                // First half: tile i's P.V and tile i+1's S (matrix first), or
+                // tile i's softmax (vector first).
+                if (matrix_first) matrix_half(i);
+                else if (i < wt) softmax(i);
+                __syncthreads();
+                // Second half: the roles swap.
+                if (matrix_first) {
+                    if (i + 1 < wt) softmax(i + 1);
+                } else {
+                    matrix_half(i);
+                }
+                if constexpr (!split_staging) stage_next(i);
+                __syncthreads();
+            }
         }
-        l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-    };
-    auto pv = [&](int j) {  // O^T += V^T P^T over four 16-token steps
-        const uint16_t* vtt = vt[j & 1];
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-            for (int n = 0; n < 4; ++n) {
-                const U16x8 va = *reinterpret_cast<const U16x8*>(
-                    &vtt[(32 * n + col) * V_LD + 16 * st + 8 * half]);
-                o[n] = mfma32<T>(va, pr[st], o[n]);
-                o[n] = mfma32<T>(va, pb[st], o[n]);
+
+        if constexpr (kConvertV) {
+            if (v_out_of_range) {  // uniform (read after the last barrier)
+                if (tid == 0) a.guard[0] = 1;  // the EXACT launch redoes this call
+                return;
+            }
+        }
+        if (!wave_active) return;
+
+        const float l = pair_sum(l_run);
+        const int64_t qi = wq0 + col;
+        if (qi >= q_len) return;
+        const float inv = a.v_scale / l;
+        T* orow = a.out + (q_begin + qi) * a.ots + h * a.ohs + 4 * half;
+    #pragma unroll
+        for (int n = 0; n < 4; ++n)
+    #pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                uint2 w;
+                w.x = pack2<T>(o[n][4 * g + 0] * inv, o[n][4 * g + 1] * inv);
+                w.y = pack2<T>(o[n][4 * g + 2] * inv, o[n][4 * g + 3] * inv);
+                *reinterpret_cast<uint2*>(orow + 32 * n + 8 * g) = w;
             }
     };
-
-    const int ntiles = int((kv_end + BK - 1) / BK);
-    const int wt = wave_active ? int((wave_kv_end + BK - 1) / BK) : 0;  // this wave's tiles
-    // Ping-pong: waves 0..W/2-1 ("matrix first") and W/2..W-1 ("vector
-    // first") pair up on each SIMD. Every tile is split in two halves at a
-    // barrier; in each half one wave of a pair issues MFMAs (P.V of tile i
-    // and S of tile i+1) while the other runs exponentials, so the matrix
-    // cores and the vector ALUs work at the same time.
-    const bool matrix_first = wave < W / 2;
-
-    // Prologue: K(0), K(1), V(0) into LDS, and K(2), V(1) into registers,
-    // with the three tiles' block ids and rows fetched concurrently. (The
-    // first staging call also writes V(0) into the spare V buffer.)
-    SU stage[JPT][4];
-    uint32_t ids[JPT][4];
-    {
-        SU st0[JPT][4], st1[JPT][4];
-        uint32_t id0[JPT][4], id1[JPT][4];
-        load_ids(-2, id0);
-        load_ids(-1, id1);
-        load_ids(0, ids);
-        load_tile(-2, id0, st0);
-        load_tile(-1, id1, st1);
-        load_tile(0, ids, stage);
-        load_ids(1, ids);
-        store_tile(-2, st0);
-        store_tile(-1, st1);
-    }
-    __syncthreads();
-    if (wt > 0) {
-        scores(0);
-        if (matrix_first) softmax(0);
-    }
-
-    // With eight waves, waves 0-3 own the K staging jobs and waves 4-7 the V
-    // jobs; each group stages in the half where it issues MFMAs, so staging
-    // runs alongside the other group's exponentials instead of in a phase of
-    // its own. K(i+2) goes to the buffer of K(i), V(i+1) to that of V(i-1):
-    // both were last read before the previous barrier, and neither buffer is
-    // read in the half that writes it.
-    constexpr bool split_staging = W == 8;
-    auto stage_next = [&](int i) {
-        store_tile(i, stage);
-        load_tile(i + 1, ids, stage);
-        load_ids(i + 2, ids);
-    };
-    // K(2) overwrites K(0), which every wave read above in scores(0).
-    if constexpr (split_staging) __syncthreads();
-    // A wave's MFMA half with its staging in one basic block (the common
-    // case i + 1 < wt), so the scheduler can slot the staging instructions
-    // between the matrix instructions.
-    auto matrix_half = [&](int i) {
-        if (i + 1 < wt) {
-            pv(i);
-            scores(i + 1);
-            if constexpr (split_staging) stage_next(i);
-        } else if (i < wt) {
-            pv(i);
-            if constexpr (split_staging) stage_next(i);
-        } else if constexpr (split_staging) {
-            stage_next(i);
+    if constexpr (EXACT) {
+        for (int t = blockIdx.x; t < a.grid; t += gridDim.x) {
+            __syncthreads();  // the previous task's LDS reads are done
+            task(t);
         }
-    };
-    for (int i = 0; i < ntiles; ++i) {
-        // First half: tile i's P.V and tile i+1's S (matrix first), or
-        // tile i's softmax (vector first).
-        if (matrix_first) matrix_half(i);
-        else if (i < wt) softmax(i);
-        __syncthreads();
-        // Second half: the roles swap.
-        if (matrix_first) {
-            if (i + 1 < wt) softmax(i + 1);
-        } else {
-            matrix_half(i);
-        }
-        if constexpr (!split_staging) stage_next(i);
-        __syncthreads();
+    } else {
+        task(blockIdx.x);
     }
-    if (!wave_active) return;
-
-    const float l = pair_sum(l_run);
-    const int64_t qi = wq0 + col;
-    if (qi >= q_len) return;
-    const float inv = a.v_scale / l;
-    T* orow = a.out + (q_begin + qi) * a.ots + h * a.ohs + 4 * half;
-#pragma unroll
-    for (int n = 0; n < 4; ++n)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            uint2 w;
-            w.x = pack2<T>(o[n][4 * g + 0] * inv, o[n][4 * g + 1] * inv);
-            w.y = pack2<T>(o[n][4 * g + 2] * inv, o[n][4 * g + 3] * inv);
-            *reinterpret_cast<uint2*>(orow + 32 * n + 8 * g) = w;
-        }
 }
 
 }  // namespace
 }  // namespace tvllm
 
 using namespace tvllm;
+
+extern "C" int64_t tvllm_paged_prefill_workspace_size(int dtype, int cache_dtype) {
+    // The fallback guard (two ints) of a bf16 cache, whose V is converted to
+    // fp16 for the P.V products.
+    return dtype == TVLLM_BF16 && cache_dtype == TVLLM_BF16 ? 2 * int64_t(sizeof(int)) : 0;
+}
 
 extern "C" int tvllm_paged_prefill(
     const void* q, int64_t q_token_stride, int64_t q_head_stride,
@@ -456,6 +586,7 @@ extern "C" int tvllm_paged_prefill(
     const int64_t* block_offsets, const int64_t* context_lens, int64_t num_items,
     int64_t max_query_len, int64_t num_heads, int64_t num_kv_heads,
     int64_t head_dim, int64_t num_slots, int64_t block_size, float scale,
+    void* workspace, int64_t workspace_bytes,
     int dtype, int cache_dtype, float k_scale, float v_scale, tvllm_stream_t stream) {
     TVLLM_CHECK(head_dim == 128, "paged_prefill: head_dim must be 128");
     const bool f8 = cache_dtype == TVLLM_FP8_E4M3;
@@ -473,6 +604,12 @@ extern "C" int tvllm_paged_prefill(
     TVLLM_CHECK(num_items >= 0 && max_query_len >= 0,
                 "paged_prefill: negative sizes");
     TVLLM_CHECK(scale > 0.f && scale < INFINITY, "paged_prefill: scale must be positive");
+    const int64_t need = tvllm_paged_prefill_workspace_size(dtype, cache_dtype);
+    TVLLM_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                "paged_prefill: workspace of %lld bytes required, %lld given",
+                (long long)need, (long long)workspace_bytes);
+    TVLLM_CHECK(need == 0 || (reinterpret_cast<uintptr_t>(workspace) & 3) == 0,
+                "paged_prefill: workspace must be 4-byte aligned");
     if (num_items == 0 || max_query_len == 0) return TVLLM_OK;
     TVLLM_CHECK(q && k_cache && v_cache && out && q_offsets && blocks &&
                     block_offsets && context_lens,
@@ -517,20 +654,33 @@ extern "C" int tvllm_paged_prefill(
         args.grid = int(grid);
         args.scale_log2 = scale * kLog2e * k_scale;
         args.v_scale = v_scale;
+        args.guard = static_cast<int*>(workspace);
         args.block_shift = (block_size & (block_size - 1)) == 0
                                ? __builtin_ctzll(uint64_t(block_size)) : -1;
         const bool quad = args.block_shift >= 2;
-        auto go = [&]<bool F8>() {
+        auto go = [&]<bool F8, bool EXACT>() {
+            // The exact launch: few workgroups (few arrivals on the guard).
+            const int g = EXACT ? int(std::min<int64_t>(grid, kExactWorkgroups)) : int(grid);
             if (waves == 8) {
-                if (quad) paged_prefill_d128<T, 8, true, F8><<<int(grid), 512, 0, s>>>(args);
-                else paged_prefill_d128<T, 8, false, F8><<<int(grid), 512, 0, s>>>(args);
+                if (quad) paged_prefill_d128<T, 8, true, F8, EXACT><<<g, 512, 0, s>>>(args);
+                else paged_prefill_d128<T, 8, false, F8, EXACT><<<g, 512, 0, s>>>(args);
             } else {
-                if (quad) paged_prefill_d128<T, 4, true, F8><<<int(grid), 256, 0, s>>>(args);
-                else paged_prefill_d128<T, 4, false, F8><<<int(grid), 256, 0, s>>>(args);
+                if (quad) paged_prefill_d128<T, 4, true, F8, EXACT><<<g, 256, 0, s>>>(args);
+                else paged_prefill_d128<T, 4, false, F8, EXACT><<<g, 256, 0, s>>>(args);
             }
         };
-        if (f8) go.template operator()<true>();
-        else go.template operator()<false>();
-        return launch_status("paged_prefill");
+        if (f8) {
+            go.template operator()<true, false>();
+            return launch_status("paged_prefill");
+        }
+        go.template operator()<false, false>();
+        int st = launch_status("paged_prefill");
+        if constexpr (std::is_same_v<T, __bf16>) {
+            if (st == TVLLM_OK) {
+                go.template operator()<false, true>();  // no-op unless V left fp16 range
+                st = launch_status("paged_prefill exact fallback");
+            }
+        }
+        return st;
     });
 }

@@ -19,7 +19,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libtinyvllm_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -63,7 +63,9 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_resolve_tokens": (_INT, [_P, _P, _P, _I64, _I64, _P]),
     "tvllm_paged_prefill": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _P,
                                    _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
-                                   _I64, _I64, _F32, _INT, _INT, _F32, _F32, _P]),
+                                   _I64, _I64, _F32, _P, _I64, _INT, _INT, _F32, _F32,
+                                   _P]),
+    "tvllm_paged_prefill_workspace_size": (_I64, [_INT, _INT]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -47,6 +47,9 @@ def paged_prefill_attention(
         raise RuntimeError("metadata lengths must align")
     if items == 0 or m.max_query_len == 0:
         return
+    cache_dtype, k_scale, v_scale = cache_format(cache)
+    guard = _guard(device, int(lib.tvllm_paged_prefill_workspace_size(
+        dtype_code(q.dtype), cache_dtype)))
     check(lib.tvllm_paged_prefill(
         q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
         output.data_ptr(), output.stride(0), output.stride(1),
@@ -54,5 +57,23 @@ def paged_prefill_attention(
         m.block_table_offsets.data_ptr(), m.context_lens.data_ptr(),
         items, m.max_query_len, q.shape[1], cache.num_kv_heads, q.shape[2],
         cache.num_slots, cache.block_size, float(scale),
-        dtype_code(q.dtype), *cache_format(cache), stream_of(device),
+        None if guard is None else guard.data_ptr(), 0 if guard is None else guard.numel(),
+        dtype_code(q.dtype), cache_dtype, k_scale, v_scale, stream_of(device),
     ))
+
+
+_GUARDS: dict[tuple[torch.device, int], torch.Tensor] = {}
+
+
+def _guard(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """The zero-initialised fallback guard of ``device``'s current stream
+    (calls on one stream are ordered, so they can share it; the kernels
+    leave it zero)."""
+    if nbytes == 0:
+        return None
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    guard = _GUARDS.get(key)
+    if guard is None or guard.numel() < nbytes:
+        guard = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _GUARDS[key] = guard
+    return guard
