@@ -73,6 +73,7 @@ class DecodeWorkload:
         from tinyvllm.request import SamplingParams
 
         self.greedy = SamplingParams(max_new_tokens=1 << 20)
+        self.full_tables = False  # True: upload every block table each step
 
     def batch_for_step(self, from_previous: bool = False):
         """The next decode step's PreparedBatch (block tables and slots as
@@ -104,6 +105,10 @@ class DecodeWorkload:
             kv_block_table_offsets=tuple(offsets.tolist()), kv_slot_mapping=slots,
             request_ids=tuple(range(n)),
             input_token_sources=tuple(range(n)) if from_previous else None,
+            # As the engine's builder emits them: one slot per sequence, and a
+            # table epoch that never changes (the tables only grow).
+            request_slots=None if self.full_tables else tuple(range(n)),
+            kv_table_epochs=None if self.full_tables else (1,) * n,
         )
 
     def advance(self, tokens):
@@ -152,6 +157,7 @@ def attention_roofline(executor, workload, cfg, iters: int = 30,
     runner = executor.runner
     batch = workload.batch_for_step()
     model_input = runner.decode_inputs.prepare(batch, [0] * batch.num_items)
+    runner.decode_inputs.apply_table_updates()
     meta = model_input.kv.decode
     rows, hq, hkv, d = (batch.num_items, cfg.num_attention_heads, cfg.num_key_value_heads,
                         cfg.head_dim)
@@ -851,6 +857,8 @@ def main() -> None:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--full-tables", action="store_true",
+                    help="upload every block table each step (no device-resident tables)")
     ap.add_argument("--kv-cache-dtype", choices=["auto", "fp8_e4m3"], default="auto",
                     help="decode workload: KV cache in the model dtype (the metric's "
                          "configuration) or the optional FP8 E4M3 layout")
@@ -919,17 +927,28 @@ def main() -> None:
         cache.key.normal_(generator=gen)
         cache.value.normal_(generator=gen)
     workload = DecodeWorkload(args.batch, args.context, bs, num_blocks, cfg.vocab_size)
+    workload.full_tables = args.full_tables
 
     # Pipelined like the engine: the host builds and launches step i+1
     # while the GPU runs step i.
     pending = workload.run(executor, args.warmup)
     torch.cuda.synchronize()
+    stats = executor.runner.decode_inputs.stats
+    before = dict(stats)
     t0 = time.perf_counter()
     pending = workload.run(executor, args.steps, pending)
     workload.tokens = list(pending.result().sampled_token_ids)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     tok_s = args.batch * args.steps / elapsed
+    steps = max(1, stats["steps"] - before["steps"])
+    inputs_cost = {  # per step: host packing of the decode inputs, H2D upload
+        "host_prepare_us": round((stats["host_ns"] - before["host_ns"]) / steps / 1e3, 1),
+        "h2d_bytes": round((stats["bytes"] - before["bytes"]) / steps),
+        "table_entries_uploaded": round((stats["table_entries"] - before["table_entries"])
+                                        / steps, 2),
+        "device_resident_tables": not args.full_tables,
+    }
 
     roof = attention_roofline(executor, workload, cfg, headline=(
         args.model == "qwen3-8b" and args.batch == 64 and args.context == 2048
@@ -950,6 +969,7 @@ def main() -> None:
                    "kv_cache_dtype": "fp8_e4m3" if fp8 else "bf16"},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "decode_inputs": inputs_cost,
     }
     print(json.dumps(line), flush=True)
 

@@ -73,6 +73,17 @@ int tvllm_store_kv(const void* key, const void* value,
                    int dtype, int cache_dtype, float k_scale, float v_scale,
                    tvllm_stream_t stream);
 
+/* Apply a step's block-table updates to a device-resident table:
+ * updates = [n, index_0, id_0, index_1, id_1, ...] (int64, on the device);
+ * table[index_i] = id_i for i < min(n, capacity); indices outside
+ * [0, table_size) are skipped. n is read on the device (graph-capturable).
+ * No counterpart in the reference (it re-uploads every block table each
+ * step, tinyvllm/runtime/inputs.py:70-117); the decode step keeps one table
+ * row per request slot and uploads only the entries that changed. */
+int tvllm_apply_table_updates(int64_t* table, int64_t table_size,
+                              const int64_t* updates, int64_t capacity,
+                              tvllm_stream_t stream);
+
 /* Bytes of device workspace tvllm_paged_decode needs for this geometry
  * (split-K partial results). 0 means no workspace is needed.
  * max_context_len bounds the context of any row (the engine's
@@ -100,7 +111,8 @@ int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
  *   of KV head h / (num_heads / num_kv_heads). lengths[r] == 0 -> zeros.
  * q, out: [*, num_heads, head_dim] with element strides (last == 1).
  * k_cache, v_cache: contiguous [num_slots, num_kv_heads, head_dim].
- * rows, offsets (num_rows + 1), lengths, blocks: int64 device vectors.
+ * rows, offsets (num_rows + 1; only offsets[r], the start of row r's table, is
+ * read - a CSR or pitched per-slot rows), lengths, blocks: int64 device vectors.
  * workspace: >= tvllm_paged_decode_workspace_size(...) bytes (may be NULL
  * when that size is 0). head_dim 128 with group <= 16 runs the MFMA kernel
  * (GQA heads share each K/V load); any other head_dim <= 256 or group runs a

@@ -17,6 +17,24 @@ def factory(**kw):
     return lambda: make_engine(**kw)[0]
 
 
+def slow_factory(delay_s=0.002, **kw):
+    """An engine whose simulated executor takes ``delay_s`` per step, so a
+    request cannot finish between two submits of the test."""
+    import time
+
+    def build():
+        engine, ex = make_engine(**kw)
+        for name in ("execute", "launch"):
+            fn = getattr(ex, name, None)
+            if fn is not None:
+                def slowed(batch, _fn=fn):
+                    time.sleep(delay_s)
+                    return _fn(batch)
+                setattr(ex, name, slowed)
+        return engine
+    return build
+
+
 def run(coro):
     return asyncio.run(asyncio.wait_for(coro, timeout=60))
 
@@ -51,7 +69,7 @@ def test_async_engine_cancel_overload_and_rejection(pipelined):
     params = SamplingParams(max_new_tokens=60, ignore_eos=True)
 
     async def main():
-        async with AsyncEngine(factory(pipelined=pipelined), max_requests=2) as bridge:
+        async with AsyncEngine(slow_factory(pipelined=pipelined), max_requests=2) as bridge:
             a = await bridge.submit([7] * 5, params)
             b = await bridge.submit([8] * 5, params)
             with pytest.raises(OverloadedError):

@@ -139,8 +139,16 @@ class LayerProbe:
     def _post(self, module, args, kwargs, output):
         if self._buf and self.cap is None:
             self._buf["residual_out"] = output[1].detach().clone()
-            self.cap = {k: (v.cpu() if torch.is_tensor(v) else v)
-                        for k, v in self._buf.items()}
+            cap = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in self._buf.items()}
+            # Decode rows read ceil(length / 16) table entries from offsets[r]
+            # (device-resident tables: one pitched row per request slot);
+            # restate them as the CSR the oracle takes.
+            pages = (cap["lengths"] + 15) // 16
+            tables = [cap["blocks"][int(o):int(o) + int(n)]
+                      for o, n in zip(cap["offsets"][:-1], pages)]
+            cap["blocks"] = torch.cat(tables)
+            cap["offsets"] = torch.cat((torch.zeros(1, dtype=torch.long), pages.cumsum(0)))
+            self.cap = cap
         self._buf = {}
 
     def step_eager(self, engine, now_ns):

@@ -143,3 +143,28 @@ def test_teardown_releases_every_table_and_forgets_prefixes():
     assert m.free_block_count == 8 and m.pool.cached_block_count == 0
     assert m.block_table(1) == () and isinstance(BlockRef(0, 0), BlockRef)
     assert np.all(m.pool._holders == 0)
+
+
+def test_table_epochs_change_only_when_an_entry_may_be_replaced():
+    """Growth keeps a request's table epoch (readers append), a prefix swap
+    or a new request gets a new one (readers re-read the whole table)."""
+    bs = 4
+    m = BlockManager(block_size=bs, num_blocks=32)
+    prompt = list(range(200, 209))  # 9 tokens: 2 full blocks
+    epochs = {}
+    for rid in (1, 2):
+        step = m.stage(rid, [BlockAppend(rid, 0, len(prompt))])
+        epochs[rid] = step.table_epoch(rid)
+        step.go_live()
+        step.writes_done()
+    assert epochs[1] != epochs[2]
+    step = m.stage(5, [BlockAppend(1, 9, 4)])  # growth into a new block
+    assert step.table_epoch(1) == epochs[1]
+    step.go_live()
+    step.writes_done()
+    m.publish_blocks(1, lambda a, b: (prompt + [0] * 8)[a:b], len(prompt))
+    m.publish_blocks(2, lambda a, b: prompt[a:b], len(prompt))  # swaps to 1's blocks
+    step = m.stage(6, [BlockAppend(1, 13, 1), BlockAppend(2, 9, 1)])
+    assert step.table_epoch(1) == epochs[1]      # request 1 kept its own blocks
+    assert step.table_epoch(2) != epochs[2]      # request 2's entries were replaced
+    step.undo()

@@ -11,6 +11,8 @@
 // projection output.
 #include "common.h"
 
+#include <algorithm>
+
 namespace tvllm {
 namespace {
 
@@ -174,4 +176,41 @@ extern "C" int tvllm_store_kv(const void* key, const void* value,
             head_dim);
     }
     return launch_status("store_kv");
+}
+
+// ------------------------------------------------- device block tables --
+// updates = [n, index_0, id_0, index_1, id_1, ...]: table[index_i] = id_i for
+// i < min(n, capacity), skipping indices outside the table. n is read on
+// the device, so a captured graph applies each step's own uploaded count.
+namespace tvllm {
+namespace {
+
+__global__ void __launch_bounds__(256)
+apply_table_updates_kernel(int64_t* __restrict__ table, int64_t table_size,
+                           const int64_t* __restrict__ updates, int64_t capacity) {
+    const int64_t n = min(updates[0], capacity);
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t index = updates[1 + 2 * i];
+        if (index >= 0 && index < table_size) table[index] = updates[2 + 2 * i];
+    }
+}
+
+}  // namespace
+}  // namespace tvllm
+
+extern "C" int tvllm_apply_table_updates(int64_t* table, int64_t table_size,
+                                         const int64_t* updates, int64_t capacity,
+                                         tvllm_stream_t stream) {
+    using namespace tvllm;
+    TVLLM_CHECK(table_size >= 0 && capacity >= 0,
+                "apply_table_updates: negative sizes");
+    if (capacity == 0) return TVLLM_OK;
+    TVLLM_CHECK(table && updates, "apply_table_updates: null pointer");
+    // Enough threads for a typical step (a page per row); larger uploads
+    // (rows entering decode with whole tables) loop.
+    const int blocks = int(std::min<int64_t>((capacity + 255) / 256, 64));
+    apply_table_updates_kernel<<<blocks, 256, 0, as_hip(stream)>>>(table, table_size,
+                                                                     updates, capacity);
+    return launch_status("apply_table_updates");
 }

@@ -106,6 +106,11 @@ class PreparedBatch:
     # input_ids, j >= 0 = row j of the previous launched step's sampled tokens,
     # still on the device when this batch is built. None = all from input_ids.
     input_token_sources: tuple[int, ...] | np.ndarray | None = None
+    # Device-resident block tables (beyond the reference): per item, its
+    # request slot (unique among active requests) and its table epoch
+    # (equal epochs: the table only grew since). None: upload whole tables.
+    request_slots: tuple[int, ...] | None = None
+    kv_table_epochs: tuple[int, ...] | None = None
 
     @property
     def num_items(self) -> int:
@@ -181,6 +186,7 @@ class BatchBuilder:
         params: list[SamplingParams] = []
         tables: list[np.ndarray] = []
         table_off = [0]
+        epoch_of = getattr(kv, "table_epoch", None)
         slots: list[np.ndarray] = []
         rids: list[int] = []
         sources: list[int] | None = None
@@ -234,4 +240,7 @@ class BatchBuilder:
             kv_slot_mapping=np.concatenate(slots) if slots else np.zeros(0, np.int64),
             request_ids=tuple(rids),
             input_token_sources=None if sources is None else tuple(sources),
+            request_slots=tuple(i.request_slot for i in plan.items),
+            kv_table_epochs=None if epoch_of is None else tuple(
+                epoch_of(i.request_id) for i in plan.items),
         )

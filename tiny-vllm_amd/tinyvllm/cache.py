@@ -218,7 +218,8 @@ class StepKV:
 
     STAGED, LIVE, DONE, UNDONE, FAILED = "staged", "live", "done", "undone", "failed"
 
-    __slots__ = ("plan_id", "request_ids", "phase", "_mgr", "_fresh", "_pins", "_rows")
+    __slots__ = ("plan_id", "request_ids", "phase", "_mgr", "_fresh", "_pins", "_rows",
+                 "_epochs")
 
     def __init__(self, plan_id: int, manager: "BlockManager") -> None:
         self.plan_id = plan_id
@@ -228,6 +229,7 @@ class StepKV:
         self._pins: dict[int, tuple[BlockRef, ...]] = {}   # prefix hits held
         # request -> (table ids, table generations, write slots, KV end)
         self._rows: dict[int, tuple[np.ndarray, np.ndarray, np.ndarray, int]] = {}
+        self._epochs: dict[int, int] = {}  # table epoch of each request
         self.request_ids: tuple[int, ...] = ()
 
     @property
@@ -249,6 +251,13 @@ class StepKV:
                              f"[{token_start}, {token_start + query_len}) in this step")
         return row[0], row[2]
 
+    def table_epoch(self, request_id: int) -> int:
+        """Changes whenever an entry of the request's table other than an
+        appended one may differ from an earlier step's (a new table, or a
+        prefix-cache swap): a reader holding a copy from the same epoch only
+        needs the appended entries."""
+        return self._epochs[request_id]
+
     # -- transitions
 
     def go_live(self) -> None:
@@ -257,6 +266,7 @@ class StepKV:
         tables = self._mgr._tables
         for rid, (ids, gens, _, _) in self._rows.items():
             tables[rid] = (ids, gens)
+        self._mgr._epoch.update(self._epochs)
         self.phase = StepKV.LIVE
 
     def writes_done(self) -> None:
@@ -303,6 +313,8 @@ class BlockManager:
                                         enabled=enable_prefix_caching)
         self._tables: dict[int, tuple[np.ndarray, np.ndarray]] = {}  # ids, generations
         self._valid: dict[int, int] = {}
+        self._epoch: dict[int, int] = {}   # table epochs (see StepKV.table_epoch)
+        self._epochs_issued = 0
         self._open: StepKV | None = None
 
     # -- views
@@ -365,9 +377,15 @@ class BlockManager:
             end = append.token_start + append.query_len
             pos = np.arange(append.token_start, end, dtype=np.int64)
             step._rows[append.request_id] = (ids, gens, ids[pos // bs] * bs + pos % bs, end)
+            epoch = self._epoch.get(append.request_id)
+            step._epochs[append.request_id] = self._new_epoch() if epoch is None else epoch
         step.request_ids = tuple(a.request_id for a in appends)
         self._open = step
         return step
+
+    def _new_epoch(self) -> int:
+        self._epochs_issued += 1
+        return self._epochs_issued
 
     def _base_of(self, append: BlockAppend) -> tuple[np.ndarray, np.ndarray]:
         """The table an append grows, checked against its start position."""
@@ -414,12 +432,14 @@ class BlockManager:
             self.pool.drop(BlockRef(int(ids[index]), int(gens[index])))
             ids[index], gens[index] = canonical.block_id, canonical.generation
         self._tables[request_id] = (ids, gens)
+        self._epoch[request_id] = self._new_epoch()
 
     def release_request(self, request_id: int) -> None:
         if self._open is not None:
             raise RuntimeError("requests are released between steps")
         entry = self._tables.pop(request_id, None)
         self._valid.pop(request_id, None)
+        self._epoch.pop(request_id, None)
         self.prefix_cache.drop_request(request_id)
         if entry is not None:
             for block, gen in zip(entry[0][::-1], entry[1][::-1]):

@@ -61,6 +61,7 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_sample": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
                             _I64, _INT, _P]),
     "tvllm_resolve_tokens": (_INT, [_P, _P, _P, _I64, _I64, _P]),
+    "tvllm_apply_table_updates": (_INT, [_P, _I64, _P, _I64, _P]),
     "tvllm_paged_prefill": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _P,
                                    _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                    _I64, _I64, _F32, _P, _I64, _INT, _INT, _F32, _F32,

@@ -47,3 +47,19 @@ def store_kv(
         key.shape[0], key.shape[1], key.shape[2], key_cache.shape[0],
         dtype_code(key.dtype), *cache_format(cache), stream_of(device),
     ))
+
+
+def apply_table_updates(table: torch.Tensor, updates: torch.Tensor) -> None:
+    """In place on the device: ``table[updates[1 + 2i]] = updates[2 + 2i]``
+    for ``i < updates[0]`` (the count is read on the device, so a captured
+    graph applies each step's own upload). Both int64, contiguous, 1-D."""
+    lib = load_kernels()
+    device = require_gpu(table, updates)
+    for tensor in (table, updates):
+        if tensor.dtype != torch.long or tensor.dim() != 1 or not tensor.is_contiguous():
+            raise RuntimeError("apply_table_updates takes contiguous 1-D int64 tensors")
+    if updates.numel() < 1:
+        raise RuntimeError("updates needs its count word")
+    capacity = (updates.numel() - 1) // 2
+    check(lib.tvllm_apply_table_updates(table.data_ptr(), table.numel(), updates.data_ptr(),
+                                        capacity, stream_of(device)))

@@ -37,6 +37,12 @@ class SingleQueryMetadata:
     ``max_context_len`` is an upper bound on every ``context_lens`` entry
     (the engine's max_model_len, or the batch maximum in eager mode); it only
     sizes the split-K decomposition. None means "bounded by the cache".
+
+    Row r's table is ``block_table_ids[block_table_offsets[r]:][:ceil(
+    context_lens[r] / block_size)]``: a CSR (offsets ascending, as the
+    reference builds them) is one layout, the decode step's device-resident
+    tables (one pitched row per request slot) another; the kernels read
+    only ``block_table_offsets[r]``.
     """
 
     query_rows: torch.Tensor

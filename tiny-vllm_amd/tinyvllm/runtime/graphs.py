@@ -1,7 +1,8 @@
 """hipGraph capture and replay of the whole decode step
 (reference: tinyvllm/runtime/graphs.py:12-139).
 
-One graph per batch-size bucket holds embedding -> all layers (fused
+One graph per batch-size bucket holds the block-table update and token
+resolution -> embedding -> all layers (fused
 QK-norm/RoPE/KV-write, split-K paged decode, GEMMs, norms) -> LM head ->
 sampling kernel, reading only the fixed ``DecodeInputs`` views. A replay is
 a single host call, so the per-step host cost no longer scales with
@@ -72,7 +73,8 @@ class DecodeGraphs:
         d["slots"][:n].copy_(inputs.rows[:n] * cache.block_size)
         d["offsets"][:n + 1].copy_(torch.arange(n + 1, device=inputs.device))
         d["lengths"][:n].fill_(1)
-        d["blocks"][:n].copy_(inputs.rows[:n])
+        inputs.table[:n].copy_(inputs.rows[:n])
+        d["updates"][:1].zero_()
         if tokens is None:
             tokens = torch.zeros(inputs.capacity, dtype=torch.long, device=inputs.device)
         if tokens.dtype != torch.long or tokens.numel() < inputs.capacity:
@@ -94,6 +96,7 @@ class DecodeGraphs:
             # Leave the padding state behind for the first real batch.
             d["slots"].fill_(-1)
             d["lengths"].zero_()
+            inputs.forget_tables()  # the capture overwrote table rows
             torch.cuda.current_stream(inputs.device).synchronize()
         self.entries = dict(sorted(self.entries.items()))
 
@@ -119,6 +122,7 @@ class DecodeGraphs:
         sources = inputs.d["sources"][:size]
 
         def step():
+            inputs.apply_table_updates()
             resolve_tokens(model_input.input_ids, sources, self.tokens)
             attention = HipAttention(model_input, cache, decode_workspace=workspace)
             hidden = model(model_input.input_ids, model_input.positions, attention=attention)

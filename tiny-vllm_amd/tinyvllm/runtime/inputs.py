@@ -1,16 +1,27 @@
 """Fixed-address device inputs of the graph-replayed decode step
 (reference: tinyvllm/runtime/inputs.py:14-137).
 
-All per-step decode metadata - token ids, positions, write slots, block-table
-CSR, context lengths and the sampling parameters - is packed into one pinned
-host buffer and moved with a single asynchronous H2D copy into one device
-buffer whose sub-views never move, so captured graphs can replay against them.
+All per-step decode metadata - token ids, positions, write slots, context
+lengths, the sampling parameters and the block-table changes - is packed
+into one pinned host buffer and moved with a single asynchronous H2D copy
+into one device buffer whose sub-views never move, so captured graphs can
+replay against them.
 
-Layout (bytes, N = capacity rows, P = N * pages_per_row):
+Block tables stay on the device: one row of ``pitch`` ids per request slot
+(``PreparedBatch.request_slots``), kept across steps. A step uploads only
+the entries a row lacks - for a request already decoding in that slot with
+the same table epoch, the pages appended since its last upload (usually
+none, at most one per row) - as (index, id) pairs that
+``tvllm_apply_table_updates`` writes at the head of the step. The reference
+re-packs and uploads every table each step (inputs.py:70-117).
+
+Upload layout (bytes, N = capacity rows, P = N * pitch):
   float32 [N] temperature | float32 [N] top_p |
   int64 [N] tokens | [N] positions | [N] slots | [N + 1] table offsets |
   [N] context lengths | [N] top_k | [N] seeds | [N] sample counters |
-  [N] token sources | [P] block ids
+  [N] token sources | [1 + 2P] table updates (count, then index/id pairs)
+Device only: int64 [P] block tables. Row r's table starts at offsets[r]
+(its slot times the pitch).
 A token source j >= 0 replaces the row's token, on the device, by row j of
 the previous step's sampled tokens (-1: keep the uploaded id).
 Rows past the live count are padding: slot -1 (no KV write), length 0 (zero
@@ -18,14 +29,18 @@ attention output), greedy sampling.
 """
 from __future__ import annotations
 
+import time
+
+import numpy as np
 import torch
 
 from tinyvllm._validation import _check_positive_int
 from tinyvllm.batch import PreparedBatch
+from tinyvllm.kernels.kv_store import apply_table_updates
 from tinyvllm.runtime.contracts import ModelInput, PagedKVMetadata, SingleQueryMetadata
 
 _INT_FIELDS = ("tokens", "positions", "slots", "offsets", "lengths", "top_k", "seeds",
-               "counters", "sources", "blocks")
+               "counters", "sources", "updates")
 
 
 class DecodeInputs:
@@ -34,8 +49,8 @@ class DecodeInputs:
 
     @staticmethod
     def device_bytes(*, max_num_seqs: int, max_model_len: int, block_size: int) -> int:
-        pages = -(-max_model_len // block_size)
-        return 4 * 2 * max_num_seqs + 8 * (9 * max_num_seqs + 1 + max_num_seqs * pages)
+        table = max_num_seqs * -(-max_model_len // block_size)
+        return 4 * 2 * max_num_seqs + 8 * (9 * max_num_seqs + 1 + 1 + 2 * table) + 8 * table
 
     def __init__(self, *, max_num_seqs: int, max_model_len: int, block_size: int,
                  device: torch.device | str) -> None:
@@ -49,14 +64,16 @@ class DecodeInputs:
         self.capacity = n
         self.max_model_len = max_model_len
         self.block_size = block_size
-        self.table_capacity = n * -(-max_model_len // block_size)
+        self.pitch = -(-max_model_len // block_size)
+        self.table_capacity = n * self.pitch
         sizes = {"tokens": n, "positions": n, "slots": n, "offsets": n + 1, "lengths": n,
                  "top_k": n, "seeds": n, "counters": n, "sources": n,
-                 "blocks": self.table_capacity}
+                 "updates": 1 + 2 * self.table_capacity}
         self.float_bytes = 8 * n
         total = self.float_bytes + 8 * sum(sizes.values())
         self.host = torch.zeros(total, dtype=torch.uint8, pin_memory=True)
         self.device_data = torch.zeros(total, dtype=torch.uint8, device=self.device)
+        self.table = torch.zeros(self.table_capacity, dtype=torch.long, device=self.device)
         self.stream = torch.cuda.current_stream(self.device)
         self.upload_done = torch.cuda.Event()
         self.uploaded = False
@@ -73,18 +90,34 @@ class DecodeInputs:
 
         self.h = {k: v.numpy() for k, v in carve(self.host).items()}
         self.d = carve(self.device_data)
-        self._blocks_offset = self.float_bytes + 8 * (9 * n + 1)
+        self.d["blocks"] = self.table
+        self._updates_offset = self.float_bytes + 8 * (9 * n + 1)
+        # What each slot's device row holds: owner request, table epoch, pages.
+        self._row_request = np.full(n, -1, dtype=np.int64)
+        self._row_epoch = np.full(n, -1, dtype=np.int64)
+        self._row_pages = np.zeros(n, dtype=np.int64)
+        # Per-step cost counters (host packing time, bytes uploaded, table
+        # entries uploaded) for measurement.
+        self.stats = {"steps": 0, "host_ns": 0, "bytes": 0, "table_entries": 0}
         self.rows = torch.arange(n, dtype=torch.long, device=self.device)
         # Graph capture and padding defaults: every row is padding.
-        self._reset_padding(0, 0)
+        self._reset_padding(0)
+        self.h["updates"][0] = 0
         self.device_data.copy_(self.host)
 
-    def _reset_padding(self, count: int, table_size: int) -> None:
+    def forget_tables(self) -> None:
+        """The device rows no longer match the host record (their contents
+        were overwritten, e.g. by graph capture): upload whole tables next."""
+        self._row_request.fill(-1)
+        self._row_epoch.fill(-1)
+        self._row_pages.fill(0)
+
+    def _reset_padding(self, count: int) -> None:
         h = self.h
         h["tokens"][count:] = 0
         h["positions"][count:] = 0
         h["slots"][count:] = -1
-        h["offsets"][count + 1:] = table_size
+        h["offsets"][count:] = 0
         h["lengths"][count:] = 0
         h["temperature"][count:] = 0.0
         h["top_p"][count:] = 1.0
@@ -92,6 +125,46 @@ class DecodeInputs:
         h["seeds"][count:] = 0
         h["counters"][count:] = 0
         h["sources"][count:] = -1
+
+    def _table_rows(self, batch: PreparedBatch, count: int) -> np.ndarray:
+        """Each item's device table row; also uploads what those rows lack
+        (writes the update list into the host buffer)."""
+        offsets = np.asarray(batch.kv_block_table_offsets, dtype=np.int64)
+        pages = np.diff(offsets)
+        if len(pages) != count or (pages > self.pitch).any():
+            raise ValueError("batch exceeds decode input block-table capacity")
+        ids = np.asarray(batch.kv_block_table_ids, dtype=np.int64)
+        rid = np.asarray(batch.request_ids, dtype=np.int64)
+        if batch.request_slots is not None and batch.kv_table_epochs is not None:
+            rows = np.asarray(batch.request_slots, dtype=np.int64)
+            if len(rows) != count or rows.min() < 0 or rows.max() >= self.capacity \
+                    or len(np.unique(rows)) != count:
+                raise ValueError("request slots must be distinct and below capacity")
+            epochs = np.asarray(batch.kv_table_epochs, dtype=np.int64)
+            kept = ((self._row_request[rows] == rid) & (self._row_epoch[rows] == epochs)
+                    & (self._row_pages[rows] <= pages))
+            first = np.where(kept, self._row_pages[rows], 0)
+        else:  # no slot/epoch record: rows in batch order, whole tables
+            rows = np.arange(count, dtype=np.int64)
+            epochs = np.full(count, -1, dtype=np.int64)
+            first = np.zeros(count, dtype=np.int64)
+        fresh = pages - first
+        total = int(fresh.sum())
+        upd = self.h["updates"]
+        upd[0] = total
+        if total:
+            item = np.repeat(np.arange(count), fresh)
+            k = np.arange(total) - np.repeat(np.cumsum(fresh) - fresh, fresh)
+            page = first[item] + k
+            upd[1:1 + 2 * total:2] = rows[item] * self.pitch + page
+            upd[2:2 + 2 * total:2] = ids[offsets[item] + page]
+        self._row_request[rows] = rid
+        self._row_epoch[rows] = epochs
+        self._row_pages[rows] = pages
+        if batch.kv_table_epochs is None:  # nothing to compare against next time
+            self._row_request[rows] = -1
+        self.stats["table_entries"] += total
+        return rows
 
     def prepare(self, batch: PreparedBatch, counters) -> ModelInput | None:
         """Upload a validated all-decode batch; None if it is not one."""
@@ -102,47 +175,53 @@ class DecodeInputs:
             raise ValueError("batch exceeds decode input request capacity")
         if batch.num_query_tokens != count or batch.num_samples != count:
             return None
-        table_size = len(batch.kv_block_table_ids)
-        if table_size > self.table_capacity:
-            raise ValueError("batch exceeds decode input block-table capacity")
+        started = time.perf_counter_ns()
         # Stream order cannot protect the host buffer from an early CPU write.
         if self.uploaded:
             self.upload_done.synchronize()
         h = self.h
-        self._reset_padding(count, table_size)
+        self._reset_padding(count)
+        rows = self._table_rows(batch, count)
         h["tokens"][:count] = batch.input_ids
         h["positions"][:count] = batch.positions
         h["slots"][:count] = batch.kv_slot_mapping
-        h["offsets"][:count + 1] = batch.kv_block_table_offsets
+        h["offsets"][:count] = rows * self.pitch
         h["lengths"][:count] = batch.context_lens_after
-        h["blocks"][:table_size] = batch.kv_block_table_ids
         params = batch.sampling_params
         first = params[0]
         if all(p == first for p in params):  # one policy for the whole batch
-            rows = [first]
+            prow = [first]
         else:
-            rows = params
-        h["temperature"][:count] = [p.temperature for p in rows]
-        h["top_p"][:count] = [p.top_p for p in rows]
-        h["top_k"][:count] = [p.top_k for p in rows]
+            prow = params
+        h["temperature"][:count] = [p.temperature for p in prow]
+        h["top_p"][:count] = [p.top_p for p in prow]
+        h["top_k"][:count] = [p.top_k for p in prow]
         h["seeds"][:count] = [p.seed - (1 << 64) if p.seed >= (1 << 63) else p.seed
-                              for p in rows]
+                              for p in prow]
         h["counters"][:count] = counters
         sources = batch.input_token_sources
         h["sources"][:count] = -1 if sources is None else sources
-        size = self._blocks_offset + 8 * table_size
+        size = self._updates_offset + 8 * (1 + 2 * int(h["updates"][0]))
         self.device_data[:size].copy_(self.host[:size], non_blocking=True)
         self.upload_done.record(self.stream)
         self.uploaded = True
-        return self.view(count, table_size, max(batch.context_lens_after))
+        self.stats["steps"] += 1
+        self.stats["bytes"] += size
+        self.stats["host_ns"] += time.perf_counter_ns() - started
+        return self.view(count, max_context_len=max(batch.context_lens_after))
+
+    def apply_table_updates(self) -> None:
+        """Write the uploaded table changes into the device tables (the first
+        node of every decode step; reads the count on the device)."""
+        apply_table_updates(self.table, self.d["updates"])
 
     def view(self, count: int, table_size: int | None = None,
              max_context_len: int | None = None) -> ModelInput:
-        """Borrow fixed storage; graph capture uses the full table capacity.
-        ``max_context_len`` bounds every row's context (default: the
-        engine's max_model_len); it only sizes the decode split-K plan."""
+        """Borrow fixed storage. ``max_context_len`` bounds every row's context
+        (default: the engine's max_model_len); it only sizes the decode
+        split-K plan. (``table_size`` is accepted for older callers; rows
+        read their tables through the offsets.)"""
         d = self.d
-        table = d["blocks"] if table_size is None else d["blocks"][:table_size]
         rows = self.rows[:count]
         return ModelInput(
             input_ids=d["tokens"][:count],
@@ -152,7 +231,7 @@ class DecodeInputs:
                 slot_mapping=d["slots"][:count],
                 decode=SingleQueryMetadata(
                     query_rows=rows,
-                    block_table_ids=table,
+                    block_table_ids=self.table,
                     block_table_offsets=d["offsets"][:count + 1],
                     context_lens=d["lengths"][:count],
                     max_context_len=max_context_len or self.max_model_len,

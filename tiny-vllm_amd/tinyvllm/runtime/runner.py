@@ -277,11 +277,12 @@ class ModelRunner:
         if self.decode_inputs is not None:
             model_input = self.decode_inputs.prepare(batch, counters)
             if model_input is not None:
-                if self.decode_graphs is not None:
+                if self.decode_graphs is not None:  # the graph applies the table updates
                     replayed = self.decode_graphs.replay(
                         batch.num_items, max(batch.context_lens_after))
                     if replayed is not None:
                         return replayed
+                self.decode_inputs.apply_table_updates()
                 if batch.input_token_sources is not None:
                     resolve_tokens(model_input.input_ids,
                                    self.decode_inputs.d["sources"][:batch.num_items],
