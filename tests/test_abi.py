@@ -94,6 +94,39 @@ def test_decode_workspace_sizes():
     assert lib.tvllm_paged_decode_workspace_size(64, 16, 8, 128, 1024, 16) == 0
     # One row, 8 KV heads: 16 splits of a 512 context -> 2 workgroups per head.
     assert lib.tvllm_paged_decode_workspace_size(1, 16, 8, 128, 512, 16) == 16 * 2 * 130 * 4
-    # 32B shape at bs16, 32k context: 128 units -> 16 splits = 8 waves x 2 groups.
+    # 32B shape at bs16, 32k context: 128 units -> 16 splits, long ranges ->
+    # 4 waves x 4 workgroups, two KV heads per workgroup.
     assert lib.tvllm_paged_decode_workspace_size(16, 64, 8, 128, 32768, 16) == \
-        16 * 64 * 2 * 130 * 4
+        16 * 64 * 4 * 130 * 4
+
+
+def _plan(lib, *args):
+    packed = lib.tvllm_paged_decode_split_plan(*args)
+    return packed >> 16, (packed >> 8) & 0xFF, packed & 0xFF  # waves, grid, heads
+
+
+def test_decode_split_plans():
+    """Many (row, KV head) units: splits inside one workgroup. Few units with
+    long page ranges per split: two KV heads x four ranges per workgroup.
+    Few units with short ranges: one head, up to eight ranges."""
+    from tinyvllm.kernels._extension import load_kernels
+
+    lib = load_kernels()
+    assert _plan(lib, 64, 32, 8, 128, 2048, 16) == (2, 1, 2)      # 8B bs64
+    assert _plan(lib, 16, 64, 8, 128, 32768, 16) == (4, 4, 2)     # C5 decode
+    assert _plan(lib, 8, 16, 8, 128, 1024, 16) == (8, 4, 1)       # C1
+    assert _plan(lib, 16, 32, 8, 128, 8192, 16) == (4, 4, 2)      # 512 tokens per split
+    assert _plan(lib, 16, 32, 8, 128, 8191, 16) == (8, 2, 1)
+
+
+def test_decode_workspace_at_the_longest_context_covers_shorter_ones():
+    """The runner sizes the decode workspace once, at max_model_len, for every
+    row count; a launch's plan follows its batch's longest context."""
+    from tinyvllm.kernels._extension import load_kernels
+
+    lib = load_kernels()
+    for max_len in (2048, 8192, 40960):
+        for rows in (1, 2, 3, 4, 8, 12, 16, 31, 32, 33, 64):
+            cap = lib.tvllm_paged_decode_workspace_size(rows, 64, 8, 128, max_len, 16)
+            for ctx in range(16, max_len + 1, 16 * 37):
+                assert lib.tvllm_paged_decode_workspace_size(rows, 64, 8, 128, ctx, 16) <= cap

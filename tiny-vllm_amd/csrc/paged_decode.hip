@@ -862,6 +862,7 @@ struct Tuning {
     int tiles = 0;  // 16-token tiles per iteration: 0 = 2 (16-bit cache) or 4 (FP8)
     int waves = 4;
     int split_waves = kMaxWaves;  // most page ranges of one head per workgroup
+    bool overridden = false;      // set from the environment: no shape heuristics
 };
 
 // Defaults can be overridden for measurement with
@@ -881,6 +882,7 @@ const Tuning& tuning() {
                 v.tiles = tiles;
                 v.waves = waves;
                 v.split_waves = split_waves;
+                v.overridden = true;
             }
         }
         return v;
@@ -912,24 +914,35 @@ struct SplitPlan {
     int heads;  // KV heads per workgroup
 };
 
-int heads_per_group(int64_t kv_heads, int64_t splits);
+int heads_per_group(int64_t kv_heads, int64_t splits, int64_t waves);
 
 SplitPlan plan_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
                       int64_t block_size) {
     const int64_t total = choose_splits(rows, kv_heads, max_context, block_size);
+    int split_waves = tuning().split_waves, waves = tuning().waves;
+    // Few (row, KV head) units with long page ranges per split (small batch,
+    // long context): workgroups of two KV heads x four page ranges. The two
+    // heads' waves read the two halves of the same 512-byte stretch of each
+    // token's cache row at about the same time, which the DRAM serves better
+    // than one head's 256-byte pieces alone (C5 decode shape, cold cache:
+    // 276 -> 257 us). Short ranges keep one head per workgroup: the extra
+    // grid-level partials would cost more than the locality gains.
+    if (!tuning().overridden && rows * kv_heads < 256 && max_context >= 512 * total) {
+        split_waves = 4;
+        waves = 8;
+    }
     SplitPlan p;
-    p.waves = std::min<int64_t>(total, tuning().split_waves);
+    p.waves = std::min<int64_t>(total, split_waves);
     p.grid = (total + p.waves - 1) / p.waves;
-    p.heads = heads_per_group(kv_heads, p.waves);
+    p.heads = heads_per_group(kv_heads, p.waves, waves);
     return p;
 }
 
 // KV heads per workgroup: the largest power of two dividing kv_heads with
 // heads * splits <= the preferred waves per workgroup.
-int heads_per_group(int64_t kv_heads, int64_t splits) {
+int heads_per_group(int64_t kv_heads, int64_t splits, int64_t waves) {
     int h = 1;
-    while (h * 2 * splits <= std::max<int64_t>(tuning().waves, splits) &&
-           kv_heads % (h * 2) == 0)
+    while (h * 2 * splits <= std::max<int64_t>(waves, splits) && kv_heads % (h * 2) == 0)
         h *= 2;
     return h;
 }

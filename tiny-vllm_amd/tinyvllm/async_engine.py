@@ -46,6 +46,15 @@ class RequestStream:
         self._reserved = reserved
         self._queue: asyncio.Queue = asyncio.Queue()
         self._done = False
+        # Tokens handed over by the worker and not yet taken by the consumer
+        # (items still in flight to the event loop count too).
+        self._buffered = 0
+        self._count_lock = threading.Lock()
+
+    def _add_buffered(self, n: int) -> int:
+        with self._count_lock:
+            self._buffered += n
+            return self._buffered
 
     @property
     def request_id(self) -> int:
@@ -58,6 +67,8 @@ class RequestStream:
         if self._done:
             raise StopAsyncIteration
         item = await self._queue.get()
+        if isinstance(item, TokenEvent):
+            self._add_buffered(-1)
         if isinstance(item, BaseException):
             self._done = True
             raise item
@@ -202,7 +213,8 @@ class AsyncEngine:
             stream = self._streams.get(token.request_id)
             if stream is None:
                 continue
-            if stream._queue.qsize() >= self._max_buffered:
+            if stream._add_buffered(1) > self._max_buffered:
+                stream._add_buffered(-1)
                 engine.cancel(token.request_id)
                 self._deliver(stream, SlowConsumerError("stream consumer is too slow"))
                 continue
