@@ -308,9 +308,10 @@ int tvllm_resolve_tokens(int64_t* tokens, const int64_t* src, const int64_t* pre
  * workspace: >= tvllm_paged_prefill_workspace_size(dtype, cache_dtype)
  * bytes, 4-byte aligned, zero before the first call; every call leaves it
  * zero. (A bf16 cache's V is converted to fp16 for the P.V products; a call
- * that meets a V value of 65536 or more in magnitude, an infinity or a NaN
- * raises a flag there and a second, exact launch recomputes it. Calls that
- * share one workspace must be ordered on one stream.)
+ * in which a V value of 65536 or more in magnitude, an infinity or a NaN
+ * enters a product raises a flag there, and a second, exact launch
+ * recomputes it. Calls that share one workspace must be ordered on one
+ * stream.)
  * Replaces: CudaAttention._attend's per-row gather + SDPA for rows with
  * history (reference tinyvllm/runtime/attention.py:102-151, 235-285). */
 int tvllm_paged_prefill(const void* q, int64_t q_token_stride,

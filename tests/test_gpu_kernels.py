@@ -195,8 +195,13 @@ def test_prefill_chunks_with_history(device, heads, kv_heads, items, bs):
 
 def test_prefill_v_beyond_fp16_range_takes_the_exact_path(device):
     """P.V runs on fp16 MFMAs with V converted from bf16; V values of 65536
-    or more (or inf/NaN) make the call recompute on bf16 MFMAs. Both calls
-    match the oracle, and the fallback guard is back to zero after each."""
+    or more (or inf/NaN) reach the outputs as fp16 infinities, and a wave
+    whose accumulators end non-finite makes the call recompute on bf16
+    MFMAs. Every case matches the oracle (a missed recompute would leave
+    infinities or NaNs in the output), and the fallback guard is back to
+    zero after each. 65280 is the largest bf16 below 65536 (exact in fp16);
+    65536 is the smallest that overflows; a value in the last pages is seen
+    only by the chunk's last queries."""
     from helpers import assert_within_ulp
     from tinyvllm.kernels import paged_prefill as PP
     from tinyvllm.kernels.paged_prefill import paged_prefill_attention
@@ -217,12 +222,20 @@ def test_prefill_v_beyond_fp16_range_takes_the_exact_path(device):
     meta_cpu = [torch.tensor(x) for x in (qoff, blocks, boff, [c for c, _ in items])]
     meta = MultiQueryMetadata(*(t.to(device) for t in meta_cpu),
                               max_query_len=max(ql for _, ql in items))
-    for huge in (True, False):
+    first_rows = torch.tensor(blocks[:3]) * bs + 5     # item 0, keys 5, 21, 37
+    late_row = torch.tensor([blocks[boff[1] - 1] * bs + (700 - 1) % bs])  # key 699
+    for case in ("large", "none", "65536_late", "65280", "-65536_first"):
         v = torch.randn(pool * bs, kv_heads, d, generator=g)
-        if huge:  # a few values fp16 cannot hold, in the first item's pages
-            rows = torch.tensor(blocks[:3]) * bs + 5
-            v[rows, 2, 7] = 3.0e5
-            v[rows[:1], 5, 100] = -70000.0
+        if case == "large":  # a few values fp16 cannot hold, in the first item's pages
+            v[first_rows, 2, 7] = 3.0e5
+            v[first_rows[:1], 5, 100] = -70000.0
+        elif case == "65536_late":
+            v[late_row, 3, 64] = 65536.0
+        elif case == "65280":
+            v[first_rows, 1, 0] = 65280.0
+            v[late_row, 6, 127] = -65280.0
+        elif case == "-65536_first":
+            v[first_rows[:1], 0, 1] = -65536.0
         v = v.to(torch.bfloat16)
         expect = torch.zeros_like(q)
         OA.prefill_attention(q, k, v, *meta_cpu, bs, d ** -0.5, expect)
@@ -230,7 +243,7 @@ def test_prefill_v_beyond_fp16_range_takes_the_exact_path(device):
         out = torch.zeros(q.shape, dtype=q.dtype, device=device)
         paged_prefill_attention(q.to(device), cache, 0, meta, out, scale=d ** -0.5)
         torch.cuda.synchronize()
-        print(f"prefill huge={huge}", flush=True)
+        print(f"prefill V case {case}", flush=True)
         assert_within_ulp(out.cpu(), expect, ulps=2.0)
         guard = PP._GUARDS[(out.device, torch.cuda.current_stream(out.device).cuda_stream)]
         assert int(guard.count_nonzero()) == 0

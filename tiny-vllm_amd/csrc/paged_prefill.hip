@@ -25,10 +25,12 @@
 //    visits them; B = the lane's probabilities) on fp16 MFMAs: P rounded to
 //    fp16 keeps 11 bits (a bf16 P would leave ~1e-3 relative error in the
 //    output, the whole bf16 tolerance), and a bf16 cache's V is converted to
-//    fp16 as it is staged, which is exact below 65536. A workgroup that meets
-//    a V value beyond that (or an infinity or NaN) redoes its tiles on bf16
-//    MFMAs with P as a rounded value plus its rounded remainder (about 16
-//    bits of P, two MFMAs per product).
+//    fp16 as it is staged, which is exact below 65536. A V value beyond that
+//    (or an infinity or NaN) becomes an fp16 infinity or NaN and makes the
+//    outputs it reaches non-finite; a wave whose accumulators end
+//    non-finite raises a guard, and a second launch recomputes the call on
+//    bf16 MFMAs with P as a rounded value plus its rounded remainder (about
+//    16 bits of P, two MFMAs per product).
 //    The O^T accumulator of a lane belongs to its own query: the softmax
 //    rescale and the final 1/l are lane-local.
 //  * online softmax in base 2 (v_exp_f32) with one running (max, sum) per
@@ -102,7 +104,7 @@ struct PrefillArgs {
     int heads, kv_heads, block_size, block_shift, q_tiles, grid;
     float scale_log2;  // softmax scale * log2(e) (* k_scale for an FP8 cache)
     float v_scale;     // FP8 cache: V dequantisation scale (1 otherwise)
-    int* guard;        // bf16 cache: [V out of fp16 range, exact-launch arrivals]
+    int* guard;        // bf16 cache: [recompute needed, exact-launch arrivals]
 };
 
 __device__ __forceinline__ float as_f(uint32_t x) { return __uint_as_float(x); }
@@ -136,7 +138,6 @@ paged_prefill_d128(PrefillArgs<T> a) {
     constexpr int JPT = JOBS / NTH;
     __shared__ __align__(16) uint16_t ks[2][K_TILE];
     __shared__ __align__(16) uint16_t vt[2][V_TILE];
-    __shared__ int v_out_of_range;  // main launch: a V value left fp16 range
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -197,14 +198,14 @@ paged_prefill_d128(PrefillArgs<T> a) {
             for (int c = 0; c < 8; ++c) qv[c] = *reinterpret_cast<const U16x8*>(qrow + 16 * c);
         }
 
-        // A bf16 cache's V is converted to fp16 while it is staged (exact below
-        // 65536 in magnitude); a workgroup that meets a larger, infinite or NaN
-        // V value redoes its work in the exact bf16 mode.
+        // A bf16 cache's V is converted to fp16 while it is staged. A finite
+        // bf16 value below 65536 in magnitude converts exactly (or, below
+        // 2^-14, to within 2^-25); a larger, infinite or NaN one becomes an
+        // fp16 infinity or NaN, and then so does every output it reaches
+        // (p * inf, 0 * inf = NaN; with p <= 2^kSlack and |v| < 65536 the
+        // fp32 sums stay finite otherwise). So a wave whose accumulators end
+        // non-finite raises the guard, and the exact launch redoes the call.
         constexpr bool kConvertV = std::is_same_v<T, __bf16> && !F8 && !EXACT;
-        if constexpr (kConvertV) {
-            if (tid == 0) v_out_of_range = 0;
-            __syncthreads();  // before any staging store may raise it
-        }
 
         const int bs = a.block_size;
         // Staging: job = (K|V, piece, token quad); 4 tokens x 16 bytes each.
@@ -279,8 +280,6 @@ paged_prefill_d128(PrefillArgs<T> a) {
                 job_coords(r, is_v, tq, piece);
                 const int buf = (tile_base + lead_of(is_v)) & 1;
                 U16x8 pc[4];  // the job's four token pieces, as staged
-                typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
-                u16x2_t wide = {0, 0};  // largest |V| bit patterns (v_pk_max_u16)
     #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (F8) {
@@ -292,19 +291,11 @@ paged_prefill_d128(PrefillArgs<T> a) {
     #pragma unroll
                                 for (int w = 0; w < 4; ++w) {
                                     const uint32_t b = pc[e].w[w];
-                                    wide = __builtin_elementwise_max(
-                                        wide, __builtin_bit_cast(u16x2_t, b & 0x7fff7fffu));
                                     pc[e].w[w] = pack2<_Float16>(half_lo<T>(b), half_hi<T>(b));
                                 }
                             }
                         }
                     }
-                }
-                if constexpr (convert) {
-                    // bf16 0x4780 = 65536: the first magnitude fp16 cannot hold
-                    // (infinities and NaNs compare above it too).
-                    if (is_v && (wide[0] >= 0x4780u || wide[1] >= 0x4780u))
-                        v_out_of_range = 1;
                 }
                 if (is_v) {
                     // V^T: dim row (piece*8 + dd), the quad's 4 tokens -> one 8-byte write;
@@ -536,8 +527,13 @@ paged_prefill_d128(PrefillArgs<T> a) {
         }
 
         if constexpr (kConvertV) {
-            if (v_out_of_range) {  // uniform (read after the last barrier)
-                if (tid == 0) a.guard[0] = 1;  // the EXACT launch redoes this call
+            float total = 0.f;  // inf or NaN if any accumulator is
+    #pragma unroll
+            for (int n = 0; n < 4; ++n)
+    #pragma unroll
+                for (int v = 0; v < 16; ++v) total += o[n][v];
+            if (__builtin_amdgcn_ballot_w64(!(__builtin_fabsf(total) < INFINITY))) {
+                if (lane == 0) a.guard[0] = 1;  // the EXACT launch redoes this call
                 return;
             }
         }
