@@ -286,18 +286,24 @@ paged_prefill_d128(PrefillArgs<T> a) {
                         pc[e] = is_v ? fp8x8_widen<_Float16>(raw[r][e]) : fp8x8_widen<T>(raw[r][e]);
                     } else {
                         pc[e] = raw[r][e];
-                        if constexpr (convert) {
-                            if (is_v) {
-    #pragma unroll
-                                for (int w = 0; w < 4; ++w) {
-                                    const uint32_t b = pc[e].w[w];
-                                    pc[e].w[w] = pack2<_Float16>(half_lo<T>(b), half_hi<T>(b));
-                                }
-                            }
-                        }
                     }
                 }
-                if (is_v) {
+                if (convert && is_v) {
+                    // V^T in fp16: each conversion takes one dim of two tokens,
+                    // so its result is already the transposed (token, token)
+                    // word (bf16 -> f32 is a shift or a mask of the raw word).
+    #pragma unroll
+                    for (int dd = 0; dd < 8; ++dd) {
+                        auto f = [&](int e) {
+                            const uint32_t b = pc[e].w[dd >> 1];
+                            return (dd & 1) ? half_hi<T>(b) : half_lo<T>(b);
+                        };
+                        uint2 w;
+                        w.x = pack2<_Float16>(f(0), f(1));
+                        w.y = pack2<_Float16>(f(2), f(3));
+                        *reinterpret_cast<uint2*>(&vt[buf][(piece * 8 + dd) * V_LD + vt_pos(tq)]) = w;
+                    }
+                } else if (is_v) {
                     // V^T: dim row (piece*8 + dd), the quad's 4 tokens -> one 8-byte write;
                     // v_perm picks the low (even dd) or high (odd dd) halves of two words.
     #pragma unroll
