@@ -124,8 +124,8 @@ __device__ __forceinline__ float pair_sum(float x) {
 // piece and widens them exactly to T before the LDS store.
 // EXACT: the bf16 fallback launch. It runs after the main launch on the same
 // stream; its workgroups do nothing unless the main launch raised guard[0].
-// Every workgroup counts its arrival in guard[1] after reading guard[0]; the
-// last one clears both words, so the guard is zero between calls.
+// Then every workgroup counts its arrival in guard[1] after reading guard[0];
+// the last one clears both words, so the guard is zero between calls.
 template <typename T, int W, bool QUAD, bool F8, bool EXACT>
 __global__ void __launch_bounds__(64 * W, 8 / W)  // two waves per SIMD
 paged_prefill_d128(PrefillArgs<T> a) {
@@ -150,10 +150,17 @@ paged_prefill_d128(PrefillArgs<T> a) {
         if (tid == 0) {
             const int raised = __hip_atomic_load(&a.guard[0], __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
-            __threadfence();  // the read completes before the arrival is counted
-            if (atomicAdd(&a.guard[1], 1) == int(gridDim.x) - 1) {  // the last arrival
-                __hip_atomic_store(&a.guard[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&a.guard[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // A clear guard has nothing to reset: return without counting.
+            // A raised one is seen by every workgroup (it is cleared only
+            // after the last of them has read it and arrived).
+            if (raised) {
+                __threadfence();  // the read completes before the arrival is counted
+                if (atomicAdd(&a.guard[1], 1) == int(gridDim.x) - 1) {  // the last arrival
+                    __hip_atomic_store(&a.guard[1], 0, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&a.guard[0], 0, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
             redo = raised;
         }
