@@ -755,36 +755,69 @@ paged_decode_d128(DecodeArgs<T> a) {
 }
 
 // Merge split partials: out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
+// One wave per (row, query head) of the 128-dim fast path. Every load is
+// issued before any result is needed: lane s holds split s's (max, sum)
+// (splits <= 64), lane l the output dims 2l, 2l+1 of eight splits at a time;
+// the maxima and sums reduce across the wave and each split's weight is
+// broadcast from its lane.
 template <typename T>
 __global__ void __launch_bounds__(64)
 paged_decode_merge(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                    T* __restrict__ out, const int64_t* __restrict__ rows,
                    int64_t ots, int64_t ohs, int heads, int splits, int head_dim,
                    float v_scale) {
+    constexpr int D = 128, B = 8;  // head dim; splits loaded per batch
     const int id = blockIdx.x;
     const int r = id / heads;
     const int h = id - r * heads;
+    const int lane = threadIdx.x;
     const int64_t base = (int64_t(r) * heads + h) * splits;
-    float mx = -INFINITY;
-    for (int s = 0; s < splits; ++s) mx = fmaxf(mx, part_ml[(base + s) * 2]);
-    T* o = out + rows[r] * ots + h * ohs;
-    if (mx == -INFINITY) {
-        for (int d = threadIdx.x; d < head_dim; d += 64) o[d] = static_cast<T>(0.f);
+    (void)head_dim;
+    const float* po = part_o + base * D + 2 * lane;
+    float2 ov[B];
+#pragma unroll
+    for (int i = 0; i < B; ++i)
+        ov[i] = i < splits ? *reinterpret_cast<const float2*>(po + int64_t(i) * D)
+                           : make_float2(0.f, 0.f);
+    float m = -INFINITY, l = 0.f;
+    if (lane < splits) {
+        const float2 ml = *reinterpret_cast<const float2*>(part_ml + (base + lane) * 2);
+        m = ml.x;
+        l = ml.y;
+    }
+    const int64_t row = rows[r];
+    float mx = m;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    T* o = out + row * ots + h * ohs + 2 * lane;
+    if (mx == -INFINITY) {  // zero-length row
+        o[0] = static_cast<T>(0.f);
+        o[1] = static_cast<T>(0.f);
         return;
     }
-    float denom = 0.f;
-    for (int s = 0; s < splits; ++s) {
-        const float m = part_ml[(base + s) * 2];
-        if (m != -INFINITY) denom += exp2f(m - mx) * part_ml[(base + s) * 2 + 1];
-    }
-    for (int d = threadIdx.x; d < head_dim; d += 64) {
-        float num = 0.f;
-        for (int s = 0; s < splits; ++s) {
-            const float m = part_ml[(base + s) * 2];
-            if (m != -INFINITY) num += exp2f(m - mx) * part_o[(base + s) * head_dim + d];
+    const float w = m == -INFINITY ? 0.f : exp2f(m - mx);  // this lane's split
+    float den = w * l;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off, 64);
+    float2 acc = make_float2(0.f, 0.f);
+    for (int s0 = 0; s0 < splits; s0 += B) {
+        if (s0 > 0) {
+#pragma unroll
+            for (int i = 0; i < B; ++i)
+                ov[i] = s0 + i < splits
+                            ? *reinterpret_cast<const float2*>(po + int64_t(s0 + i) * D)
+                            : make_float2(0.f, 0.f);
         }
-        o[d] = static_cast<T>(num * v_scale / denom);
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const float ws = __shfl(w, s0 + i, 64);  // 0 past the last split
+            acc.x += ws * ov[i].x;
+            acc.y += ws * ov[i].y;
+        }
     }
+    const float scale = v_scale / den;
+    o[0] = static_cast<T>(acc.x * scale);
+    o[1] = static_cast<T>(acc.y * scale);
 }
 
 
