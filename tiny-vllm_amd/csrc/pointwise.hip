@@ -461,6 +461,123 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
     }
 }
 
+// head_dim 128 with 8-byte aligned rows: 16 lanes per (token, head) row,
+// four rows per wave. Lane j owns the rotation pairs (d, d + 64) for
+// d = 4j .. 4j+3, so every load and store moves 4 elements. The sum of
+// squares reproduces the one-pair-per-lane kernel's butterfly exactly: the
+// steps across lanes d ^ 32 .. d ^ 4 are shuffles across lanes j ^ 8 .. j ^ 1
+// of the same pair index, the steps d ^ 2 and d ^ 1 adds within a lane, so
+// every addition pairs the same two partial sums (the results, including
+// the fused KV write, are bit-identical to that kernel and to the decode
+// kernel's fused write).
+template <typename T, bool F8>
+__global__ void __launch_bounds__(256)
+qk_norm_rope_d128(const T* __restrict__ q, int64_t qts, int64_t qhs,
+                  const T* __restrict__ k, int64_t kts, int64_t khs,
+                  const T* __restrict__ qw, const T* __restrict__ kw,
+                  const T* __restrict__ cos_t, const T* __restrict__ sin_t,
+                  int64_t tokens, int heads, int kv_heads, float q_eps, float k_eps,
+                  T* __restrict__ q_out, T* __restrict__ k_out, const T* __restrict__ v,
+                  int64_t vts, int64_t vhs, void* __restrict__ key_cache,
+                  void* __restrict__ value_cache, const int64_t* __restrict__ slots,
+                  float k_inv, float v_inv) {
+    constexpr int D = 128, H = 64;
+    const int j = threadIdx.x & 15;
+    const int64_t row = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4);
+    const int64_t q_rows = tokens * heads;
+    if (row >= q_rows + tokens * kv_heads) return;  // whole 16-lane groups
+
+    const bool is_q = row < q_rows;
+    const int64_t r = is_q ? row : row - q_rows;
+    const int nh = is_q ? heads : kv_heads;
+    const int64_t tok = r / nh;
+    const int h = int(r - tok * nh);
+    const T* src = is_q ? q + tok * qts + h * qhs : k + tok * kts + h * khs;
+    const T* w = is_q ? qw : kw;
+    const float eps = is_q ? q_eps : k_eps;
+
+    auto load4 = [](const T* p, float (&x)[4]) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        x[0] = half_lo<T>(u.x);
+        x[1] = half_hi<T>(u.x);
+        x[2] = half_lo<T>(u.y);
+        x[3] = half_hi<T>(u.y);
+    };
+    float x1[4], x2[4], w1[4], w2[4], cs[4], sn[4];
+    load4(src + 4 * j, x1);
+    load4(src + H + 4 * j, x2);
+    load4(w + 4 * j, w1);
+    load4(w + H + 4 * j, w2);
+    load4(cos_t + tok * H + 4 * j, cs);
+    load4(sin_t + tok * H + 4 * j, sn);
+    int64_t slot = -1;
+    if (!is_q && key_cache != nullptr) slot = slots[tok];
+
+    float ss[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) ss[t] = x1[t] * x1[t] + x2[t] * x2[t];
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1)  // pair distance 4 * off
+#pragma unroll
+        for (int t = 0; t < 4; ++t) ss[t] += __shfl_xor(ss[t], off, 64);
+    float s2[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s2[t] = ss[t] + ss[t ^ 2];  // distance 2
+    const float total = s2[0] + s2[1];                      // distance 1
+    const float inv = rsqrtf(total * (1.0f / float(D)) + eps);
+
+    float o1[4], o2[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const float n1 = rnd<T>(rnd<T>(x1[t] * inv) * w1[t]);
+        const float n2 = rnd<T>(rnd<T>(x2[t] * inv) * w2[t]);
+        o1[t] = rnd<T>(rnd<T>(n1 * cs[t]) - rnd<T>(n2 * sn[t]));
+        o2[t] = rnd<T>(rnd<T>(n2 * cs[t]) + rnd<T>(n1 * sn[t]));
+    }
+    auto store4 = [](T* p, const float (&x)[4]) {
+        uint2 u;
+        u.x = pack2<T>(x[0], x[1]);
+        u.y = pack2<T>(x[2], x[3]);
+        *reinterpret_cast<uint2*>(p) = u;
+    };
+    if (is_q) {
+        T* dst = q_out + r * D;
+        store4(dst + 4 * j, o1);
+        store4(dst + H + 4 * j, o2);
+        return;
+    }
+    if (key_cache == nullptr || k_out != nullptr) {  // the dense K rows
+        T* dst = k_out + r * D;
+        store4(dst + 4 * j, o1);
+        store4(dst + H + 4 * j, o2);
+    }
+    if (key_cache == nullptr || slot < 0) return;
+    const int64_t off = (slot * kv_heads + h) * D;
+    const T* vsrc = v + tok * vts + h * vhs + 8 * j;
+    const uint2 va = *reinterpret_cast<const uint2*>(vsrc);
+    const uint2 vb = *reinterpret_cast<const uint2*>(vsrc + 4);
+    if constexpr (F8) {
+        uint8_t* kd = static_cast<uint8_t*>(key_cache) + off;
+        *reinterpret_cast<uint32_t*>(kd + 4 * j) =
+            fp8x4_pack(o1[0] * k_inv, o1[1] * k_inv, o1[2] * k_inv, o1[3] * k_inv);
+        *reinterpret_cast<uint32_t*>(kd + H + 4 * j) =
+            fp8x4_pack(o2[0] * k_inv, o2[1] * k_inv, o2[2] * k_inv, o2[3] * k_inv);
+        uint2 vq;
+        vq.x = fp8x4_pack(half_lo<T>(va.x) * v_inv, half_hi<T>(va.x) * v_inv,
+                          half_lo<T>(va.y) * v_inv, half_hi<T>(va.y) * v_inv);
+        vq.y = fp8x4_pack(half_lo<T>(vb.x) * v_inv, half_hi<T>(vb.x) * v_inv,
+                          half_lo<T>(vb.y) * v_inv, half_hi<T>(vb.y) * v_inv);
+        *reinterpret_cast<uint2*>(static_cast<uint8_t*>(value_cache) + off + 8 * j) = vq;
+    } else {
+        T* kd = static_cast<T*>(key_cache) + off;
+        store4(kd + 4 * j, o1);
+        store4(kd + H + 4 * j, o2);
+        T* vd = static_cast<T*>(value_cache) + off + 8 * j;
+        *reinterpret_cast<uint2*>(vd) = va;
+        *reinterpret_cast<uint2*>(vd + 4) = vb;
+    }
+}
+
 }  // namespace
 }  // namespace tvllm
 
@@ -605,11 +722,35 @@ extern "C" int tvllm_qk_norm_rope(
     TVLLM_CHECK(q && k && q_weight && k_weight && cos && sin && q_out,
                 "qk_norm_rope: null pointer");
     hipStream_t s = as_hip(stream);
+    const auto a8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; };
+    const bool d128 = head_dim == 128 && q_token_stride % 4 == 0 && q_head_stride % 4 == 0 &&
+                      k_token_stride % 4 == 0 && k_head_stride % 4 == 0 && a8(q) && a8(k) &&
+                      a8(q_weight) && a8(k_weight) && a8(cos) && a8(sin) && a8(q_out) &&
+                      (k_out == nullptr || a8(k_out)) &&
+                      (!fused || (v_token_stride % 4 == 0 && v_head_stride % 4 == 0 && a8(v) &&
+                                  a8(key_cache) && a8(value_cache)));
     return dispatch_half(dtype, [&]<int DT>() {
         using T = typename Elem<DT>::T;
         const int blocks = int((rows + 3) / 4);
         const int half = int(head_dim / 2);
         const float k_inv = 1.f / k_scale, v_inv = 1.f / v_scale;
+        if (d128) {
+            const int64_t groups = (rows + 15) / 16;
+            TVLLM_CHECK(groups <= INT32_MAX, "qk_norm_rope: grid too large");
+            auto go128 = [&]<bool F8>() {
+                qk_norm_rope_d128<T, F8><<<int(groups), 256, 0, s>>>(
+                    static_cast<const T*>(q), q_token_stride, q_head_stride,
+                    static_cast<const T*>(k), k_token_stride, k_head_stride,
+                    static_cast<const T*>(q_weight), static_cast<const T*>(k_weight),
+                    static_cast<const T*>(cos), static_cast<const T*>(sin), tokens,
+                    int(num_heads), int(num_kv_heads), q_eps, k_eps, static_cast<T*>(q_out),
+                    static_cast<T*>(k_out), static_cast<const T*>(v), v_token_stride,
+                    v_head_stride, key_cache, value_cache, slots, k_inv, v_inv);
+            };
+            if (f8) go128.template operator()<true>();
+            else go128.template operator()<false>();
+            return launch_status("qk_norm_rope");
+        }
         auto go = [&]<bool F8>() {
 #define TVLLM_QKR(NP)                                                            \
     qk_norm_rope_kernel<T, NP, F8><<<blocks, 256, 0, s>>>(                       \
