@@ -154,16 +154,20 @@ def test_decode_fp16(device):
 
 PREFILL_ITEMS = {
     # (context, query_len): fresh prompt, chunk with history, short tail, 1-token;
-    # the largest query length selects 64, 128 or 256 queries per workgroup.
+    # the query lengths and the grid select 128 or 256 queries per workgroup.
     "q512": [(70, 70), (600, 128), (513, 1), (300, 45), (1024, 512)],
     "q100": [(100, 100), (700, 99), (65, 1), (129, 64)],
     "q50": [(50, 50), (333, 17), (64, 64), (1, 1)],
+    # eight items x 64 heads: enough workgroups for the four-wave kernel
+    "q128x8": [(300, 128), (129, 128), (700, 99), (65, 1), (128, 128), (900, 64),
+               (2000, 7), (128, 33)],
 }
 
 
 @pytest.mark.parametrize("heads,kv_heads,items,bs", [
     (16, 8, "q512", 16), (32, 8, "q512", 16), (32, 8, "q100", 16), (64, 8, "q50", 16),
-    (32, 4, "q100", 8), (16, 16, "q50", 32), (32, 8, "q512", 12), (16, 8, "q100", 2)])
+    (32, 4, "q100", 8), (16, 16, "q50", 32), (32, 8, "q512", 12), (16, 8, "q100", 2),
+    (64, 8, "q128x8", 16), (64, 8, "q128x8", 12)])
 def test_prefill_chunks_with_history(device, heads, kv_heads, items, bs):
     from tinyvllm.kernels.paged_prefill import paged_prefill_attention
     from tinyvllm.runtime.contracts import MultiQueryMetadata
