@@ -267,13 +267,26 @@ paged_prefill_d128(PrefillArgs<T> a) {
                 const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
                 const char* src = static_cast<const char*>(is_v ? a.v : a.k) +
                                   int64_t(kvh * D + piece * 8) * EB;
+                const uint32_t row_bytes = slot_elems * EB;
+                if constexpr (quad_pages) {
+                    // The quad's tokens are consecutive slots of one page:
+                    // token min(tb + e, end1) is row min(e, d) past the first.
+                    const int tb = t0 + 4 * tq;
+                    const int tc = min(tb, end1);
+                    const uint32_t d = uint32_t(end1 - tc);
+                    const char* p0 = src + uint64_t(ids[r][0] * uint32_t(bs) +
+                                                    uint32_t(tc & (bs - 1))) * row_bytes;
     #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int t = min(t0 + 4 * tq + e, end1);
-                    uint32_t slot;
-                    if constexpr (quad_pages) slot = ids[r][0] * uint32_t(bs) + uint32_t(t & (bs - 1));
-                    else slot = ids[r][e] * uint32_t(bs) + uint32_t(t % bs);
-                    stage[r][e] = *reinterpret_cast<const SU*>(src + uint64_t(slot) * slot_elems * EB);
+                    for (int e = 0; e < 4; ++e)
+                        stage[r][e] = *reinterpret_cast<const SU*>(
+                            p0 + uint64_t(min(uint32_t(e), d)) * row_bytes);
+                } else {
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = min(t0 + 4 * tq + e, end1);
+                        const uint32_t slot = ids[r][e] * uint32_t(bs) + uint32_t(t % bs);
+                        stage[r][e] = *reinterpret_cast<const SU*>(src + uint64_t(slot) * row_bytes);
+                    }
                 }
             }
         };
