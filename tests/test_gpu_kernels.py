@@ -394,6 +394,74 @@ def test_silu_and_mul_c2(device):
     assert_bf16_close(silu_and_mul(odd.to(device)).cpu(), OP.silu_and_mul(odd))
 
 
+@pytest.mark.parametrize("head_dim", [64, 256])
+def test_qk_norm_rope_other_head_dims(device, head_dim):
+    """Head dims other than 128 take the one-pair-per-lane kernel: outputs
+    against the oracle, the fused KV write bit-exact."""
+    from tinyvllm.kernels.pointwise import qk_norm_rope_store
+
+    g = torch.Generator().manual_seed(head_dim)
+    t, hq, hkv, d = 40, 4, 2, head_dim
+    qkv = torch.randn(t, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16)
+    q = qkv[:, :hq * d].view(t, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    qw = (1 + 0.02 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.02 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    cos, sin = OP.rope_tables(torch.randint(0, 4096, (t,), generator=g), d, 1e6, torch.bfloat16)
+    eq, ek = OP.qk_norm_rope(q, k, qw, kw, cos, sin)
+    slots = torch.randperm(256, generator=g)[:t]
+    slots[3] = -1
+    dq = qkv.to(device)
+    gq = dq[:, :hq * d].view(t, hq, d)
+    gk = dq[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    gv = dq[:, (hq + hkv) * d:].view(t, hkv, d)
+    kc = torch.zeros(256, hkv, d, dtype=torch.bfloat16, device=device)
+    vc = torch.zeros_like(kc)
+    oq, ok = qk_norm_rope_store(gq, gk, gv, *(x.to(device) for x in (qw, kw, cos, sin)),
+                                1e-6, 1e-6, kc, vc, slots.to(device), key_out=True)
+    assert_bf16_close(oq.cpu(), eq)
+    assert_bf16_close(ok.cpu(), ek)
+    ekc, evc = torch.zeros(256, hkv, d).to(torch.bfloat16), torch.zeros(256, hkv, d).to(torch.bfloat16)
+    OK.kv_write(ekc, evc, slots, ok.cpu(), v.contiguous())
+    assert torch.equal(kc.cpu(), ekc) and torch.equal(vc.cpu(), evc)
+
+
+def test_qk_norm_rope_vector_and_scalar_kernels_agree_bitwise(device):
+    """head_dim 128 with 8-byte aligned rows runs 16 lanes per row; the same
+    rows one element off alignment run one RoPE pair per lane. Both sum the
+    squares in the same order, so every output bit and every cache byte
+    agree."""
+    from tinyvllm.kernels.pointwise import qk_norm_rope_store
+
+    g = torch.Generator().manual_seed(128)
+    t, hq, hkv, d = 64, 8, 4, 128
+    width = (hq + 2 * hkv) * d
+    base = torch.randn(t, width, generator=g).to(torch.bfloat16).to(device)
+    qw = (1 + 0.05 * torch.randn(d, generator=g)).to(torch.bfloat16).to(device)
+    kw = (1 + 0.05 * torch.randn(d, generator=g)).to(torch.bfloat16).to(device)
+    cos, sin = (x.to(device) for x in OP.rope_tables(
+        torch.randint(0, 8192, (t,), generator=g), d, 1e6, torch.bfloat16))
+    slots = torch.randperm(512, generator=g)[:t].to(device)
+    outs = []
+    for shift in (0, 1):  # shift 1: the same values, rows 2 bytes past alignment
+        buf = torch.zeros(t, width + 1, dtype=torch.bfloat16, device=device)
+        buf[:, shift:shift + width] = base
+        qkv = buf[:, shift:shift + width]
+        q = qkv[:, :hq * d].view(t, hq, d)
+        k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+        v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+        assert (q.data_ptr() % 8 == 0) == (shift == 0)
+        kc = torch.zeros(512, hkv, d, dtype=torch.bfloat16, device=device)
+        vc = torch.zeros_like(kc)
+        oq, ok = qk_norm_rope_store(q, k, v, qw, kw, cos, sin, 1e-6, 1e-6, kc, vc, slots,
+                                    key_out=True)
+        outs.append((oq, ok, kc, vc))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def test_qk_norm_rope_c2_and_fused_kv_write(device):
     from tinyvllm.kernels.pointwise import qk_norm_rope, qk_norm_rope_store
 
