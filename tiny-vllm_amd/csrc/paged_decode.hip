@@ -1186,6 +1186,8 @@ int paged_decode_impl(
 #undef TVLLM_DEC
         const int st = launch_status("paged_decode");
         if (st != TVLLM_OK || plan.grid <= 1) return st;
+        // The merge holds one split per lane (the plan makes at most kMaxSplits).
+        TVLLM_CHECK(plan.grid <= 64, "paged_decode: at most 64 workgroup splits per row");
         paged_decode_merge<T><<<int(num_rows * num_heads), 64, 0, s>>>(
             args.part_o, args.part_ml, static_cast<T*>(out), rows, out_token_stride,
             out_head_stride, int(num_heads), int(plan.grid), int(head_dim), v_scale);
