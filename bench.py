@@ -704,9 +704,11 @@ def end_to_end(name: str, args) -> None:
     model = Qwen3ForCausalLM.random_init(cfg, device=device, dtype=torch.bfloat16, seed=0)
     # Worst-case KV of every request (no preemption), rounded to blocks.
     blocks = sum(-(-(L + spec["new"]) // 16) for L in lengths) + 64
+    init_t0 = time.perf_counter()  # KV allocation and graph capture
     engine = build_engine(model, max_model_len=max_model_len, max_num_seqs=n,
                           max_num_batched_tokens=4096, num_blocks=blocks,
                           prefill_chunk_size=512)
+    init_s = time.perf_counter() - init_t0
     params = SamplingParams(max_new_tokens=spec["new"], ignore_eos=True)
     start_ns = time.monotonic_ns()
     offsets = np.zeros(n)
@@ -738,7 +740,7 @@ def end_to_end(name: str, args) -> None:
         "metric": f"end-to-end output tok/s ({name})", "value": round(generated / elapsed, 1),
         "unit": "tok/s", "elapsed_s": round(elapsed, 2), "requests": n,
         "prompt_tokens": sum(lengths), "output_tokens": generated,
-        "prefix_hit_tokens": hits, "dtype": "bf16",
+        "prefix_hit_tokens": hits, "dtype": "bf16", "engine_init_s": round(init_s, 2),
         "mean_ttft_s": round(sum(first_token.values()) / max(1, len(first_token)), 3),
         "data": "synthetic: random-init weights N(0,0.02), random token-id prompts",
         "config": {"workload": name, "model": spec["model"], **{
@@ -816,11 +818,12 @@ def published(args) -> dict:
         num_layers=cfg.num_hidden_layers, block_size=16, num_kv_heads=cfg.num_key_value_heads,
         head_dim=cfg.head_dim, dtype=torch.bfloat16)
     blocks = (896 << 20) // per_block  # the reference's equal KV storage
+    init_t0 = time.perf_counter()
     engine = build_engine(model, max_model_len=2048, max_num_seqs=64, num_blocks=blocks,
                           max_num_batched_tokens=4096, prefill_chunk_size=512)
+    result = {"engine_init_s": round(time.perf_counter() - init_t0, 2)}
     rng = np.random.default_rng(0)
     replays = 3
-    result = {}
     for name, (spec, ref) in PUBLISHED.items():
         runs = []
         for rep in range(replays + 1):  # the first pass warms up (not counted)

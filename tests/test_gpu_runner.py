@@ -164,3 +164,57 @@ def test_token_sources_are_validated(device):
         executor.execute(dataclasses.replace(batch, input_token_sources=(-1, -1, 0)))
     with pytest.raises(ValueError, match="one entry per token"):
         executor.execute(dataclasses.replace(batch, input_token_sources=(-1,)))
+
+
+def test_prefill_graphs_match_eager_prefill(device, monkeypatch):
+    """Prefill and mixed steps replayed from the captured bucket graphs
+    (padded tokens write no KV, padded items are empty, single-token items
+    go through the prefill kernel) give the eager path's logits within bf16
+    tolerance and the same greedy tokens; the KV both write then decodes to
+    the same tokens."""
+    from tinyvllm.executor import Executor
+    from tinyvllm.runtime.prefill_graphs import PrefillGraphs
+
+    replays = []
+    original = PrefillGraphs.replay
+
+    def counted(self, tokens, items):
+        replays.append((tokens, items))
+        return original(self, tokens, items)
+
+    monkeypatch.setattr(PrefillGraphs, "replay", counted)
+    weights = OM.random_weights(CFG, seed=7, dtype=torch.bfloat16, std=0.2)
+    model = _our_model(weights, device)
+    g = torch.Generator().manual_seed(8)
+    prompts = [torch.randint(0, CFG.vocab_size, (n,), generator=g).tolist()
+               for n in (37, 5, 80, 300, 2, 9, 64, 17, 33, 700)]
+    steps = ([(0, 37, True), (1, 5, True)], [(2, 40, False), (3, 150, False)],
+             [(2, 40, True), (3, 150, True), (4, 2, True), (5, 9, True)],
+             [(0, 1, True), (1, 1, True), (6, 64, True), (7, 17, True), (8, 33, True)],
+             [(9, 700, True)],
+             [(s, 1, True) for s in range(10)])
+    results = {}
+    for eager in (True, False):
+        executor = Executor(model, block_size=16, num_blocks=480, max_model_len=1024,
+                            max_num_seqs=12, enforce_eager=eager)
+        mb = ManualBatches(prompts, block_size=16, num_blocks=480)
+        logits, tokens = [], []
+        for items in steps:
+            batch = mb.step(items)
+            out = executor.runner.run_and_sample(batch, [0] * batch.num_samples)
+            if out is None:
+                mb.commit(items, [])
+                continue
+            logits.append(out[0].float().cpu())
+            tokens.append(out[1].cpu().tolist())
+            mb.commit(items, tokens[-1])
+        results[eager] = (logits, tokens)
+        executor.clear()
+    assert replays == [(64, 2), (192, 2), (256, 4), (128, 8), (768, 1)]
+    # Single-token items run the prefill kernel instead of the split-K
+    # decode kernel: a different summation order, whose rounding the next
+    # layer carries into the logits: the end-to-end logit bar of these tests.
+    for a, b in zip(results[True][0], results[False][0]):
+        diff = (a - b).abs()
+        assert diff.max() < 0.15 and diff.mean() / a.abs().mean() < 2e-2, diff.max()
+    assert results[True][1] == results[False][1]

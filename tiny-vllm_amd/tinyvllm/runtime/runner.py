@@ -22,6 +22,7 @@ from tinyvllm.runtime.contracts import (
 )
 from tinyvllm.runtime.graphs import DecodeGraphs
 from tinyvllm.runtime.inputs import DecodeInputs
+from tinyvllm.runtime.prefill_graphs import ITEM_BUCKETS, PrefillGraphs, PrefillInputs
 
 
 class ModelRunner:
@@ -40,10 +41,17 @@ class ModelRunner:
         graph_sizes: tuple[int, ...] | None = None,
         kv_cache_dtype: torch.dtype | None = None,
         kv_scales: tuple[float, float] = (1.0, 1.0),
+        prefill_graph_tokens: int = 2048,
     ) -> None:
         """``kv_cache_dtype``: None keeps K/V in the model dtype;
         ``torch.float8_e4m3fn`` stores them as FP8 E4M3 with ``kv_scales``
-        (k_scale, v_scale) - a layout beyond the reference (hip backend)."""
+        (k_scale, v_scale) - a layout beyond the reference (hip backend).
+        ``prefill_graph_tokens``: prefill and mixed steps of up to this many
+        tokens (and up to 16 items; single-token items of short context only)
+        replay captured graphs (0: always eager; beyond the reference, which
+        runs these steps eagerly)."""
+        if type(prefill_graph_tokens) is not int or prefill_graph_tokens < 0:
+            raise ValueError("prefill_graph_tokens must be a non-negative int")
         if type(enforce_eager) is not bool:
             raise TypeError("enforce_eager must be bool")
         self.model = model.eval()
@@ -61,6 +69,8 @@ class ModelRunner:
         self.vocab_size = config.vocab_size
         self.decode_inputs: DecodeInputs | None = None
         self.decode_graphs: DecodeGraphs | None = None
+        self.prefill_inputs: PrefillInputs | None = None
+        self.prefill_graphs: PrefillGraphs | None = None
         self.kv_cache: PagedKVCache | None = None
         self.decode_workspace: torch.Tensor | None = None
         # Sampled ids of the last launched step stay here on the device; the
@@ -98,6 +108,17 @@ class ModelRunner:
                     self.decode_graphs.capture(model, self.decode_inputs, self.kv_cache,
                                                self.decode_workspace,
                                                sizes=graph_sizes, tokens=self.sampled)
+                    # A step writes at most one KV slot per token.
+                    graph_tokens = min(prefill_graph_tokens, self.kv_cache.num_slots)
+                    if graph_tokens:
+                        self.prefill_inputs = PrefillInputs(
+                            max_tokens=graph_tokens,
+                            max_items=min(max(ITEM_BUCKETS), max_num_seqs),
+                            max_model_len=max_model_len, block_size=block_size,
+                            device=self.device)
+                        self.prefill_graphs = PrefillGraphs(self.prefill_inputs.stream)
+                        self.prefill_graphs.capture(model, self.prefill_inputs,
+                                                    self.kv_cache, self.sampled)
         except Exception:
             self.clear()
             raise
@@ -296,6 +317,16 @@ class ModelRunner:
                 if want_tokens:
                     tokens = sample(logits, *self.decode_inputs.sampling_views(batch.num_items))
                 return logits, tokens
+        if self.prefill_graphs is not None:
+            buckets = self.prefill_inputs.prepare(batch, counters)
+            if buckets is not None:
+                replayed = self.prefill_graphs.replay(*buckets)
+                if replayed is not None:
+                    logits, tokens = replayed
+                    samples = batch.num_samples
+                    if samples == 0:
+                        return None
+                    return logits[:samples], tokens[:samples] if want_tokens else None
         model_input = self._lower(batch)
         if batch.input_token_sources is not None:
             src = torch.tensor(np.asarray(batch.input_token_sources, dtype=np.int64)).to(
@@ -318,9 +349,15 @@ class ModelRunner:
 
     def clear(self) -> None:
         try:
-            if self.decode_graphs is not None:
-                self.decode_graphs.close()
+            try:
+                if self.prefill_graphs is not None:
+                    self.prefill_graphs.close()
+            finally:
+                if self.decode_graphs is not None:
+                    self.decode_graphs.close()
         finally:
+            self.prefill_graphs = None
+            self.prefill_inputs = None
             self.decode_graphs = None
             self.decode_inputs = None
             self.decode_workspace = None
