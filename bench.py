@@ -286,7 +286,7 @@ def kernel_only(args) -> None:
 
     from tinyvllm.kernels.paged_decode import decode_workspace_bytes, paged_decode_qk_norm_rope
     from tinyvllm.layers import RotaryEmbedding
-    from tinyvllm.paged_kv import PagedKVCache
+    from tinyvllm.paged_kv import PagedKVCache, resolve_layout
     from tinyvllm.runtime.contracts import SingleQueryMetadata
 
     cfg = qwen3_config(args.model, max_position=40960)
@@ -296,7 +296,8 @@ def kernel_only(args) -> None:
     pages = math.ceil(ctx / bs)
     layers = 8  # visited in turn: no launch finds its KV in the memory-side cache
     cache = PagedKVCache(num_layers=layers, num_blocks=rows * pages, block_size=bs,
-                         num_kv_heads=hkv, head_dim=d, device=device, dtype=torch.bfloat16)
+                         num_kv_heads=hkv, head_dim=d, device=device, dtype=torch.bfloat16,
+                         layout=resolve_layout(args.kv_layout, rows, hkv))
     gen = torch.Generator(device=device).manual_seed(1)
     cache.key.normal_(generator=gen)
     cache.value.normal_(generator=gen)
@@ -446,7 +447,7 @@ def op_c1(args) -> dict:
 
     from oracle import attention as OA
     from tinyvllm.kernels.paged_decode import decode_workspace_bytes, paged_decode_attention
-    from tinyvllm.paged_kv import PagedKVCache
+    from tinyvllm.paged_kv import PagedKVCache, resolve_layout
     from tinyvllm.runtime.contracts import SingleQueryMetadata
 
     device = torch.device("cuda", 0)
@@ -473,7 +474,8 @@ def op_c1(args) -> dict:
         layers = max(1, min(64, math.ceil(4e9 / (2 * cache.key[0].numel() * 2))))
         gcache = PagedKVCache(num_layers=layers, num_blocks=pool, block_size=16,
                               num_kv_heads=8, head_dim=128, device=device,
-                              dtype=torch.bfloat16)
+                              dtype=torch.bfloat16,
+                              layout=resolve_layout(args.kv_layout, rows, 8))
         for layer_idx in range(layers):
             gcache.key[layer_idx].copy_(cache.key[0])
             gcache.value[layer_idx].copy_(cache.value[0])
@@ -502,7 +504,7 @@ def op_c1(args) -> dict:
                        + 8 * sum(pages) + 8 * (3 * rows + 1))
         result[name] = {**_hbm(algorithmic, seconds), "max_abs_err_vs_oracle":
                         round(err.max().item(), 5),
-                        "cpu_oracle_us": round(cpu * 1e6, 1)}
+                        "cpu_oracle_us": round(cpu * 1e6, 1), "kv_layout": gcache.layout}
         if rows < 16:
             continue
         # The optional FP8 E4M3 cache layout at the same shape (scales 1).
@@ -511,7 +513,8 @@ def op_c1(args) -> dict:
         layers8 = max(1, min(64, math.ceil(4e9 / (2 * k8.numel()))))
         gcache8 = PagedKVCache(num_layers=layers8, num_blocks=pool, block_size=16,
                                num_kv_heads=8, head_dim=128, device=device,
-                               dtype=torch.float8_e4m3fn)
+                               dtype=torch.float8_e4m3fn,
+                               layout=resolve_layout(args.kv_layout, rows, 8))
         for layer_idx in range(layers8):
             gcache8.key[layer_idx].copy_(k8)
             gcache8.value[layer_idx].copy_(v8)
@@ -530,7 +533,8 @@ def op_c1(args) -> dict:
         algorithmic8 = (int(lengths.sum()) * 8 * 128 * 2 + 2 * rows * hq * 128 * 2
                         + 8 * sum(pages) + 8 * (3 * rows + 1))
         result[name + "_kv_fp8"] = {**_hbm(algorithmic8, seconds8),
-                                    "max_abs_err_vs_oracle": round(err8.max().item(), 5)}
+                                    "max_abs_err_vs_oracle": round(err8.max().item(), 5),
+                                    "kv_layout": gcache8.layout}
         del gcache8
     return result
 
@@ -619,7 +623,7 @@ def op_prefill(args) -> dict:
 
     from oracle import attention as OA
     from tinyvllm.kernels.paged_prefill import paged_prefill_attention
-    from tinyvllm.paged_kv import PagedKVCache
+    from tinyvllm.paged_kv import PagedKVCache, resolve_layout
     from tinyvllm.runtime.contracts import MultiQueryMetadata
 
     device = torch.device("cuda", 0)
@@ -632,7 +636,8 @@ def op_prefill(args) -> dict:
         pages = ctx // bs
         pool = items * pages
         cache = PagedKVCache(num_layers=1, num_blocks=pool, block_size=bs, num_kv_heads=hkv,
-                             head_dim=d, device=device, dtype=torch.bfloat16)
+                             head_dim=d, device=device, dtype=torch.bfloat16,
+                             layout=resolve_layout(args.kv_layout, items, hkv))
         gen = torch.Generator(device=device).manual_seed(1)
         cache.key.normal_(generator=gen)
         cache.value.normal_(generator=gen)
@@ -657,7 +662,7 @@ def op_prefill(args) -> dict:
         err = (out[:qlen].cpu().float() - ref.float()).abs().max().item()
         result[name] = {"us": round(seconds * 1e6, 1), "flops": flops,
                         "TFLOP/s": round(tflops, 1), "frac_bf16_mfma": round(tflops / 2500, 4),
-                        "max_abs_err_vs_oracle_item0": round(err, 5)}
+                        "max_abs_err_vs_oracle_item0": round(err, 5), "kv_layout": cache.layout}
     return result
 
 
@@ -808,7 +813,7 @@ def published(args) -> dict:
 
     from tinyvllm.bootstrap import build_engine
     from tinyvllm.models.qwen3 import Qwen3ForCausalLM
-    from tinyvllm.paged_kv import PagedKVCache
+    from tinyvllm.paged_kv import PagedKVCache, resolve_layout
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
@@ -862,6 +867,10 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--full-tables", action="store_true",
                     help="upload every block table each step (no device-resident tables)")
+    ap.add_argument("--kv-layout", choices=["auto", "head_major", "token_major"],
+                    default="auto",
+                    help="KV-cache storage order (both keep the [slots, heads, dim] view); "
+                         "auto: the engine's choice (op benchmarks: token-major)")
     ap.add_argument("--kv-cache-dtype", choices=["auto", "fp8_e4m3"], default="auto",
                     help="decode workload: KV cache in the model dtype (the metric's "
                          "configuration) or the optional FP8 E4M3 layout")
@@ -919,7 +928,8 @@ def main() -> None:
     executor = Executor(model, block_size=bs, num_blocks=num_blocks,
                         max_model_len=max_model_len, max_num_seqs=args.batch,
                         graph_sizes=(args.batch,),
-                        kv_cache_dtype=torch.float8_e4m3fn if fp8 else None)
+                        kv_cache_dtype=torch.float8_e4m3fn if fp8 else None,
+                        kv_cache_layout=args.kv_layout)
     cache = executor.runner.kv_cache
     gen = torch.Generator(device=device).manual_seed(1)
     if fp8:  # N(0, 1) values quantised layer by layer
@@ -969,7 +979,8 @@ def main() -> None:
                    "model": args.model, "global_batch": args.batch,
                    "seq_len": args.context, "parallelism": "single-gpu",
                    "attention_backend": "hip", "graphs": True,
-                   "kv_cache_dtype": "fp8_e4m3" if fp8 else "bf16"},
+                   "kv_cache_dtype": "fp8_e4m3" if fp8 else "bf16",
+                   "kv_cache_layout": cache.layout},
         "roofline": roof,
         "cpu_baseline": cpu,
         "decode_inputs": inputs_cost,

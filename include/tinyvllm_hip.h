@@ -16,6 +16,16 @@
  * Element types: TVLLM_BF16 / TVLLM_F16 for every op; TVLLM_F32 is also
  * accepted by the row-wise pointwise ops (rms_norm, silu_and_mul), like the
  * reference's pointwise.cu dispatch.
+ *
+ * Paged KV cache (every entry point with key/value caches): num_slots =
+ * num_blocks * block_size slots; the row of (slot, KV head) holds head_dim
+ * contiguous elements at slot * cache_slot_stride + head * cache_head_stride
+ * elements from the cache pointer. Two nestings are accepted, so rows never
+ * overlap: token-major (the reference's contiguous [num_slots, kv_heads,
+ * head_dim]: slot stride kv_heads * head_dim, head stride head_dim) and
+ * head-major ([kv_heads, num_slots, head_dim]: slot stride head_dim, head
+ * stride num_slots * head_dim, a page of one head contiguous), or either
+ * with padding. The fast kernels need both strides in whole 16-byte units.
  */
 #ifndef TINYVLLM_HIP_H
 #define TINYVLLM_HIP_H
@@ -60,7 +70,7 @@ const char* tvllm_source_hash(void);
  * TVLLM_FP8_E4M3 the E4M3 byte of clamp(x * (1 / scale), -448, 448) per
  * element (nearest-even). slot == -1 skips the row (graph padding).
  * key/value: [tokens, kv_heads, head_dim] with the given element strides
- * (last stride must be 1); caches: contiguous [num_slots, kv_heads, head_dim].
+ * (last stride must be 1); caches: the paged layout above.
  * Replaces: torch.ops.tinyvllm_cuda.store_kv
  *           (reference tinyvllm/kernels/kv_store.cu:101-232, wrapper
  *            tinyvllm/kernels/kv_store.py:10-30). */
@@ -70,6 +80,7 @@ int tvllm_store_kv(const void* key, const void* value,
                    void* key_cache, void* value_cache,
                    const int64_t* slots, int64_t num_tokens,
                    int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
+                   int64_t cache_slot_stride, int64_t cache_head_stride,
                    int dtype, int cache_dtype, float k_scale, float v_scale,
                    tvllm_stream_t stream);
 
@@ -110,7 +121,7 @@ int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
  *   t < lengths[r], token t at slot blocks[offsets[r] + t / bs] * bs + t % bs
  *   of KV head h / (num_heads / num_kv_heads). lengths[r] == 0 -> zeros.
  * q, out: [*, num_heads, head_dim] with element strides (last == 1).
- * k_cache, v_cache: contiguous [num_slots, num_kv_heads, head_dim].
+ * k_cache, v_cache: the paged layout above.
  * rows, offsets (num_rows + 1; only offsets[r], the start of row r's table, is
  * read - a CSR or pitched per-slot rows), lengths, blocks: int64 device vectors.
  * workspace: >= tvllm_paged_decode_workspace_size(...) bytes (may be NULL
@@ -118,7 +129,7 @@ int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
  * (GQA heads share each K/V load); any other head_dim <= 256 or group runs a
  * slower generic kernel (one wave per query head, no MFMA).
  * cache_dtype: dtype (caches hold q's element type; k_scale = v_scale = 1)
- * or TVLLM_FP8_E4M3 (caches hold E4M3 bytes, [num_slots, kv_heads, head_dim];
+ * or TVLLM_FP8_E4M3 (caches hold E4M3 bytes in the paged layout;
  * K = stored * k_scale, V = stored * v_scale; head_dim 128, group <= 16).
  * Replaces: torch.ops.tinyvllm_cuda.paged_decode
  *           (reference tinyvllm/kernels/paged_decode.cu:469-669, wrapper
@@ -131,7 +142,8 @@ int tvllm_paged_decode(const void* q, int64_t q_token_stride,
                        const int64_t* offsets, const int64_t* lengths,
                        int64_t num_rows, int64_t num_heads,
                        int64_t num_kv_heads, int64_t head_dim,
-                       int64_t num_slots, int64_t block_size,
+                       int64_t num_slots, int64_t cache_slot_stride,
+                       int64_t cache_head_stride, int64_t block_size,
                        int64_t max_context_len, float scale,
                        void* workspace, int64_t workspace_bytes,
                        int dtype, int cache_dtype, float k_scale, float v_scale,
@@ -155,7 +167,8 @@ int tvllm_paged_decode_noalloc(const void* q, int64_t q_token_stride,
                                const int64_t* offsets, const int64_t* lengths,
                                int64_t num_rows, int64_t num_heads,
                                int64_t num_kv_heads, int64_t head_dim,
-                               int64_t num_slots, int64_t block_size,
+                               int64_t num_slots, int64_t cache_slot_stride,
+                               int64_t cache_head_stride, int64_t block_size,
                                int64_t max_context_len, float scale,
                                int dtype, int cache_dtype, float k_scale,
                                float v_scale, tvllm_stream_t stream);
@@ -181,7 +194,8 @@ int tvllm_paged_decode_qk_norm_rope(
     void* v_cache, void* out, int64_t out_token_stride, int64_t out_head_stride,
     const int64_t* rows, const int64_t* blocks, const int64_t* offsets,
     const int64_t* lengths, int64_t num_rows, int64_t num_heads, int64_t num_kv_heads,
-    int64_t head_dim, int64_t num_slots, int64_t block_size, int64_t max_context_len,
+    int64_t head_dim, int64_t num_slots, int64_t cache_slot_stride,
+    int64_t cache_head_stride, int64_t block_size, int64_t max_context_len,
     float scale, void* workspace, int64_t workspace_bytes, int dtype, int cache_dtype,
     float k_scale, float v_scale, tvllm_stream_t stream);
 
@@ -236,8 +250,8 @@ int tvllm_silu_and_mul(const void* input, int64_t tokens, int64_t heads,
  * Fused KV write (not in the reference, which runs store_kv afterwards):
  * when key_cache != NULL, the rotated K row and the V row
  * (v: [tokens, num_kv_heads, head_dim] with the given strides) are also
- * written to key_cache/value_cache[slots[t]] (slot -1 skips); k_out may then
- * be NULL. cache_dtype / k_scale / v_scale as for tvllm_store_kv (the FP8
+ * written to key_cache/value_cache at slot slots[t] (the paged layout
+ * above; slot -1 skips); k_out may then be NULL. cache_dtype / k_scale / v_scale as for tvllm_store_kv (the FP8
  * cache stores the E4M3 byte of the rounded rotated K element times 1/k_scale).
  * Replaces: torch.ops.tinyvllm_cuda.qk_norm_rope
  *           (reference tinyvllm/kernels/pointwise.cu:453-546) and, when
@@ -253,7 +267,8 @@ int tvllm_qk_norm_rope(const void* q, int64_t q_token_stride,
                        const void* v, int64_t v_token_stride,
                        int64_t v_head_stride, void* key_cache,
                        void* value_cache, const int64_t* slots,
-                       int64_t num_slots, int dtype, int cache_dtype,
+                       int64_t num_slots, int64_t cache_slot_stride,
+                       int64_t cache_head_stride, int dtype, int cache_dtype,
                        float k_scale, float v_scale, tvllm_stream_t stream);
 
 /* Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
@@ -323,7 +338,8 @@ int tvllm_paged_prefill(const void* q, int64_t q_token_stride,
                         const int64_t* context_lens, int64_t num_items,
                         int64_t max_query_len, int64_t num_heads,
                         int64_t num_kv_heads, int64_t head_dim,
-                        int64_t num_slots, int64_t block_size, float scale,
+                        int64_t num_slots, int64_t cache_slot_stride,
+                        int64_t cache_head_stride, int64_t block_size, float scale,
                         void* workspace, int64_t workspace_bytes,
                         int dtype, int cache_dtype, float k_scale,
                         float v_scale, tvllm_stream_t stream);

@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = load_kernels()
     for name in sorted(declared_symbols()):
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
-    assert lib.tvllm_abi_version() == 4
+    assert lib.tvllm_abi_version() == 5
     assert lib.tvllm_last_error() == b""
 
 
@@ -38,28 +38,59 @@ def test_argument_errors_surface_without_touching_a_gpu():
 
     lib = load_kernels()
     status = lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
-                                4, 8, 128, 64, 7, 7, 1.0, 1.0, None)
+                                4, 8, 128, 64, 1024, 128, 7, 7, 1.0, 1.0, None)
     assert status == -1
     with pytest.raises(RuntimeError, match="float16 or bfloat16"):
         check(status)
     status = lib.tvllm_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None,
-                                    None, None, 1, 6, 4, 128, 64, 16, 64, 1.0,
+                                    None, None, 1, 6, 4, 128, 64, 512, 128, 16, 64, 1.0,
                                     None, 0, 0, 0, 1.0, 1.0, None)
     with pytest.raises(RuntimeError, match="GQA"):
         check(status)
     # Zero-sized work is a no-op that never dereferences pointers.
     assert lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
-                              0, 8, 128, 64, 0, 0, 1.0, 1.0, None) == 0
+                              0, 8, 128, 64, 1024, 128, 0, 0, 1.0, 1.0, None) == 0
     # KV scales belong to FP8 caches; a 16-bit cache must keep them at 1.
     status = lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
-                                0, 8, 128, 64, 0, 0, 2.0, 1.0, None)
+                                0, 8, 128, 64, 1024, 128, 0, 0, 2.0, 1.0, None)
     with pytest.raises(RuntimeError, match="FP8 cache only"):
         check(status)
     status = lib.tvllm_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None,
-                                    None, None, 1, 8, 8, 128, 64, 16, 64, 1.0,
+                                    None, None, 1, 8, 8, 128, 64, 1024, 128, 16, 64, 1.0,
                                     None, 0, 0, 1, 1.0, 1.0, None)
     with pytest.raises(RuntimeError, match="cache dtype"):
         check(status)
+
+
+def test_cache_layout_contract():
+    """Both cache nestings are accepted (token-major [slots, heads, dim] and
+    head-major [heads, slots, dim]); strides whose head rows would overlap
+    are refused by every entry point that takes the cache."""
+    from tinyvllm.kernels._extension import check, load_kernels
+
+    lib = load_kernels()
+    slots, heads, dim = 64, 8, 128
+    for ss, hs in ((heads * dim, dim), (dim, slots * dim), (2 * heads * dim, 2 * dim)):
+        assert lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
+                                  0, heads, dim, slots, ss, hs, 0, 0, 1.0, 1.0, None) == 0
+        assert lib.tvllm_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None,
+                                      None, None, 0, 16, heads, dim, slots, ss, hs, 16,
+                                      64, 1.0, None, 0, 0, 0, 1.0, 1.0, None) == 0
+    for ss, hs in ((dim, dim), (heads * dim, dim // 2), (dim, (slots - 1) * dim), (0, 0)):
+        status = lib.tvllm_store_kv(None, None, 0, 0, 0, 0, None, None, None,
+                                    0, heads, dim, slots, ss, hs, 0, 0, 1.0, 1.0, None)
+        with pytest.raises(RuntimeError, match="non-overlapping"):
+            check(status)
+        status = lib.tvllm_paged_decode(None, 0, 0, None, None, None, 0, 0, None, None,
+                                        None, None, 0, 16, heads, dim, slots, ss, hs, 16,
+                                        64, 1.0, None, 0, 0, 0, 1.0, 1.0, None)
+        with pytest.raises(RuntimeError, match="non-overlapping"):
+            check(status)
+        status = lib.tvllm_paged_prefill(None, 0, 0, None, None, None, 0, 0, None, None,
+                                         None, None, 1, 16, 16, heads, dim, slots, ss, hs, 16,
+                                         0.1, None, 0, 0, 0, 1.0, 1.0, None)
+        with pytest.raises(RuntimeError, match="non-overlapping"):
+            check(status)
 
 
 def test_resolve_tokens_and_sample_workspace_contracts():

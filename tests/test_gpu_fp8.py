@@ -23,17 +23,19 @@ pytestmark = pytest.mark.gpu
 F8 = torch.float8_e4m3fn
 
 
-def _fp8_cache(k, v, bs, device, k_scale=1.0, v_scale=1.0):
+def _fp8_cache(k, v, bs, device, k_scale=1.0, v_scale=1.0, layout="head_major"):
     """GPU FP8 cache holding the oracle's quantisation of k/v (and the CPU
     dequantised copies the oracle attends over)."""
     kq, vq = OK.fp8_quantize(k, k_scale), OK.fp8_quantize(v, v_scale)
-    cache = _Cache(kq.view(F8).to(device), vq.view(F8).to(device), bs, k_scale, v_scale)
+    cache = _Cache(kq.view(F8).to(device), vq.view(F8).to(device), bs, k_scale, v_scale,
+                   layout=layout)
     return cache, OK.fp8_dequantize(kq, k_scale), OK.fp8_dequantize(vq, v_scale)
 
 
+@pytest.mark.parametrize("layout", ["head_major", "token_major"])
 @pytest.mark.parametrize("strided", [False, True])
 @pytest.mark.parametrize("scales", [(1.0, 1.0), (0.25, 3.0)])
-def test_store_kv_fp8_bit_exact(device, strided, scales):
+def test_store_kv_fp8_bit_exact(device, strided, scales, layout):
     from tinyvllm.kernels.kv_store import store_kv
 
     g = torch.Generator().manual_seed(12)
@@ -54,7 +56,7 @@ def test_store_kv_fp8_bit_exact(device, strided, scales):
     keep = slots >= 0
     ek[slots[keep]] = OK.fp8_quantize(k.contiguous()[keep], scales[0])
     ev[slots[keep]] = OK.fp8_quantize(v.contiguous()[keep], scales[1])
-    cache = _Cache(kc.view(F8).to(device), vc.view(F8).to(device), 16, *scales)
+    cache = _Cache(kc.view(F8).to(device), vc.view(F8).to(device), 16, *scales, layout=layout)
     dq = qkv.to(device)
     if strided:
         dk = dq[:, 16 * d:(16 + hkv) * d].view(tokens, hkv, d)
@@ -100,12 +102,13 @@ def test_qk_norm_rope_store_fp8_bit_exact(device):
     assert torch.equal(vc.cpu().view(torch.uint8), ev)
 
 
-def _decode(case, device, k_scale, v_scale, max_ctx, dtype=torch.bfloat16):
+def _decode(case, device, k_scale, v_scale, max_ctx, dtype=torch.bfloat16,
+            layout="head_major"):
     from tinyvllm.kernels.paged_decode import paged_decode_attention
     from tinyvllm.runtime.contracts import SingleQueryMetadata
 
     cache, kd, vd = _fp8_cache(case["k"].float() * k_scale, case["v"].float() * v_scale,
-                               case["block_size"], device, k_scale, v_scale)
+                               case["block_size"], device, k_scale, v_scale, layout)
     q = case["q"].to(dtype)
     meta = SingleQueryMetadata(*(case[n].to(device) for n in ("rows", "blocks", "offsets",
                                                               "lengths")), max_ctx)
@@ -143,6 +146,14 @@ def test_decode_fp8_cache_fp16_queries(device):
     case = paged_decode_case(seed=5, batch=6, heads=32, kv_heads=8, pool_blocks=1024)
     out, expect = _decode(case, device, 1.0, 1.0, 1024, dtype=torch.float16)
     assert_bf16_close(out.float(), expect.float())
+
+
+def test_decode_fp8_token_major_cache(device):
+    """The reference's contiguous [slots, heads, dim] layout through the same
+    kernel (its 128-byte head rows at a 1 KiB stride)."""
+    case = paged_decode_case(seed=6, batch=8, heads=32, kv_heads=8, pool_blocks=1024)
+    out, expect = _decode(case, device, 0.5, 2.0, 1024, layout="token_major")
+    assert_bf16_close(out, expect)
 
 
 @pytest.mark.parametrize("lengths,heads,kv_heads,max_ctx", [
@@ -218,8 +229,9 @@ def test_decode_fused_fp8_write_matches_unfused(device, lengths, heads, kv_heads
     assert_bf16_close(out_b.cpu(), expect)
 
 
-@pytest.mark.parametrize("bs", [16, 12])
-def test_prefill_fp8_cache_matches_oracle(device, bs):
+@pytest.mark.parametrize("bs,layout", [(16, "head_major"), (12, "head_major"),
+                                       (16, "token_major")])
+def test_prefill_fp8_cache_matches_oracle(device, bs, layout):
     from tinyvllm.kernels.paged_prefill import paged_prefill_attention
     from tinyvllm.runtime.contracts import MultiQueryMetadata
 
@@ -229,7 +241,7 @@ def test_prefill_fp8_cache_matches_oracle(device, bs):
     ks, vs = 0.5, 0.25  # unit-variance K/V stored as 2x and 4x their values
     cache_cpu_k = torch.randn(pool * bs, kv_heads, d, generator=g)
     cache_cpu_v = torch.randn(pool * bs, kv_heads, d, generator=g)
-    cache, kd, vd = _fp8_cache(cache_cpu_k, cache_cpu_v, bs, device, ks, vs)
+    cache, kd, vd = _fp8_cache(cache_cpu_k, cache_cpu_v, bs, device, ks, vs, layout)
     perm = torch.randperm(pool, generator=g).tolist()
     blocks, boff, qoff = [], [0], [0]
     for ctx, ql in items:

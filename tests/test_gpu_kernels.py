@@ -17,11 +17,17 @@ from oracle import pointwise as OP
 pytestmark = pytest.mark.gpu
 
 
-def _Cache(k, v, block_size, k_scale=1.0, v_scale=1.0):
-    """A one-layer PagedKVCache wrapping existing K/V tensors."""
+def _Cache(k, v, block_size, k_scale=1.0, v_scale=1.0, layout="head_major"):
+    """A one-layer PagedKVCache holding the values of the given [slots,
+    kv_heads, dim] K/V, stored head-major (the cache's default: each head's
+    slots contiguous, ``key`` a [slots, heads, dim] view of that storage) or,
+    with ``layout="token_major"``, in the given tensors themselves."""
     from tinyvllm.paged_kv import PagedKVCache
 
+    if layout == "head_major":
+        k, v = (t.transpose(0, 1).contiguous().transpose(0, 1) for t in (k, v))
     cache = PagedKVCache.__new__(PagedKVCache)
+    cache.layout = layout
     cache.key, cache.value = k[None], v[None]
     cache.num_layers, cache.block_size = 1, block_size
     cache.num_slots, cache.num_kv_heads, cache.head_dim = k.shape
@@ -34,9 +40,10 @@ def _Cache(k, v, block_size, k_scale=1.0, v_scale=1.0):
 
 # ------------------------------------------------------------------ store_kv --
 
+@pytest.mark.parametrize("layout", ["head_major", "token_major"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("strided", [False, True])
-def test_store_kv_bit_exact_with_padding(device, dtype, strided):
+def test_store_kv_bit_exact_with_padding(device, dtype, strided, layout):
     from tinyvllm.kernels.kv_store import store_kv
 
     g = torch.Generator().manual_seed(11)
@@ -54,7 +61,7 @@ def test_store_kv_bit_exact_with_padding(device, dtype, strided):
     vc = torch.full((slots_total, hkv, d), -2.5).to(dtype)
     ek, ev = kc.clone(), vc.clone()
     OK.kv_write(ek, ev, slots, k.contiguous(), v.contiguous())
-    cache = _Cache(kc.to(device), vc.to(device), 16)
+    cache = _Cache(kc.to(device), vc.to(device), 16, layout=layout)
     if strided:
         dq = qkv.to(device)
         dk = dq[:, 16 * d:(16 + hkv) * d].view(tokens, hkv, d)
@@ -69,11 +76,12 @@ def test_store_kv_bit_exact_with_padding(device, dtype, strided):
 
 # -------------------------------------------------------------- paged decode --
 
-def _run_decode(case, device, max_context_len=None):
+def _run_decode(case, device, max_context_len=None, layout="head_major"):
     from tinyvllm.kernels.paged_decode import paged_decode_attention
     from tinyvllm.runtime.contracts import SingleQueryMetadata
 
-    cache = _Cache(case["k"].to(device), case["v"].to(device), case["block_size"])
+    cache = _Cache(case["k"].to(device), case["v"].to(device), case["block_size"],
+                   layout=layout)
     meta = SingleQueryMetadata(
         case["rows"].to(device), case["blocks"].to(device), case["offsets"].to(device),
         case["lengths"].to(device), max_context_len,
@@ -89,9 +97,10 @@ def _run_decode(case, device, max_context_len=None):
     return out.cpu(), expect
 
 
-def test_decode_c1_qwen3_0p6b_shapes(device):
+@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+def test_decode_c1_qwen3_0p6b_shapes(device, layout):
     case = paged_decode_case(seed=0, batch=8, heads=16, kv_heads=8)
-    out, expect = _run_decode(case, device, max_context_len=1024)
+    out, expect = _run_decode(case, device, max_context_len=1024, layout=layout)
     assert_bf16_close(out, expect)
 
 
@@ -134,12 +143,13 @@ def test_decode_selected_rows_and_strided_q(device):
     assert_bf16_close(out.cpu(), expect)
 
 
+@pytest.mark.parametrize("layout", ["head_major", "token_major"])
 @pytest.mark.parametrize("head_dim,block_size", [(64, 16), (128, 5), (256, 8)])
-def test_decode_generic_shapes(device, head_dim, block_size):
+def test_decode_generic_shapes(device, head_dim, block_size, layout):
     case = paged_decode_case(seed=head_dim + block_size, batch=3, heads=4, kv_heads=2,
                              head_dim=head_dim, block_size=block_size, pool_blocks=300,
                              max_len=400)
-    out, expect = _run_decode(case, device)
+    out, expect = _run_decode(case, device, layout=layout)
     assert_bf16_close(out, expect)
 
 
@@ -164,11 +174,14 @@ PREFILL_ITEMS = {
 }
 
 
-@pytest.mark.parametrize("heads,kv_heads,items,bs", [
-    (16, 8, "q512", 16), (32, 8, "q512", 16), (32, 8, "q100", 16), (64, 8, "q50", 16),
-    (32, 4, "q100", 8), (16, 16, "q50", 32), (32, 8, "q512", 12), (16, 8, "q100", 2),
-    (64, 8, "q128x8", 16), (64, 8, "q128x8", 12)])
-def test_prefill_chunks_with_history(device, heads, kv_heads, items, bs):
+@pytest.mark.parametrize("heads,kv_heads,items,bs,layout", [
+    (16, 8, "q512", 16, "head_major"), (32, 8, "q512", 16, "head_major"),
+    (32, 8, "q100", 16, "head_major"), (64, 8, "q50", 16, "head_major"),
+    (32, 4, "q100", 8, "head_major"), (16, 16, "q50", 32, "head_major"),
+    (32, 8, "q512", 12, "head_major"), (16, 8, "q100", 2, "head_major"),
+    (64, 8, "q128x8", 16, "head_major"), (64, 8, "q128x8", 12, "head_major"),
+    (32, 8, "q512", 16, "token_major"), (32, 8, "q512", 12, "token_major")])
+def test_prefill_chunks_with_history(device, heads, kv_heads, items, bs, layout):
     from tinyvllm.kernels.paged_prefill import paged_prefill_attention
     from tinyvllm.runtime.contracts import MultiQueryMetadata
 
@@ -188,7 +201,7 @@ def test_prefill_chunks_with_history(device, heads, kv_heads, items, bs):
     meta_cpu = [torch.tensor(x) for x in (qoff, blocks, boff, [c for c, _ in items])]
     expect = torch.zeros_like(q)
     OA.prefill_attention(q, k, v, *meta_cpu, bs, d ** -0.5, expect)
-    cache = _Cache(k.to(device), v.to(device), bs)
+    cache = _Cache(k.to(device), v.to(device), bs, layout=layout)
     meta = MultiQueryMetadata(*(t.to(device) for t in meta_cpu),
                               max_query_len=max(ql for _, ql in items))
     out = torch.zeros(q.shape, dtype=q.dtype, device=device)
@@ -462,7 +475,8 @@ def test_qk_norm_rope_vector_and_scalar_kernels_agree_bitwise(device):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-def test_qk_norm_rope_c2_and_fused_kv_write(device):
+@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+def test_qk_norm_rope_c2_and_fused_kv_write(device, layout):
     from tinyvllm.kernels.pointwise import qk_norm_rope, qk_norm_rope_store
 
     c = _c2_inputs()
@@ -485,8 +499,10 @@ def test_qk_norm_rope_c2_and_fused_kv_write(device):
     # unfused path produces (bit-exact), untouched elsewhere and at slot -1.
     slots = c["slots"].clone()
     slots[5] = -1
-    kc = torch.full((16384, hkv, d), 9.0, dtype=torch.bfloat16, device=device)
-    vc = torch.full((16384, hkv, d), -9.0, dtype=torch.bfloat16, device=device)
+    cache = _Cache(torch.full((16384, hkv, d), 9.0, dtype=torch.bfloat16, device=device),
+                   torch.full((16384, hkv, d), -9.0, dtype=torch.bfloat16, device=device),
+                   16, layout=layout)
+    kc, vc = cache.key[0], cache.value[0]
     fq, fk = qk_norm_rope_store(gq, gk, gv, *args, 1e-6, 1e-6, kc, vc, slots.to(device),
                                 key_out=True)
     assert torch.equal(fq, oq) and torch.equal(fk, ok)
@@ -637,12 +653,14 @@ def test_decode_many_rows_long_context_splits(device):
 
 
 
-@pytest.mark.parametrize("heads,kv_heads,lengths,max_ctx", [
-    (32, 8, [2049, 1, 700, 0, 16, 17], 4096),   # one workgroup per row, padding row
-    (64, 8, [5000, 33, 1], 32768),               # group 8; workgroup-level splits
-    (16, 8, [30000, 2], 32768),                  # the new token in the last workgroup
+@pytest.mark.parametrize("heads,kv_heads,lengths,max_ctx,layout", [
+    (32, 8, [2049, 1, 700, 0, 16, 17], 4096, "head_major"),  # a workgroup per row, padding
+    (64, 8, [5000, 33, 1], 32768, "head_major"),   # group 8; workgroup-level splits
+    (16, 8, [30000, 2], 32768, "head_major"),      # the new token in the last workgroup
+    (32, 8, [2049, 1, 700, 0, 16, 17], 4096, "token_major"),
 ])
-def test_decode_fused_qk_norm_rope_kv_write(device, heads, kv_heads, lengths, max_ctx):
+def test_decode_fused_qk_norm_rope_kv_write(device, heads, kv_heads, lengths, max_ctx,
+                                            layout):
     """Fused decode step == qk_norm_rope_store + paged_decode: the cache after
     the step is bit-identical (rotated K, copied V, slot -1 untouched) and the
     attention output matches the unfused path and the oracle."""
@@ -680,13 +698,13 @@ def test_decode_fused_qk_norm_rope_kv_write(device, heads, kv_heads, lengths, ma
     gslots = G(torch.tensor(slots))
     scale = d ** -0.5
 
-    cache_a = _Cache(G(kc), G(vc), bs)
+    cache_a = _Cache(G(kc), G(vc), bs, layout=layout)
     q_rot, _ = qk_norm_rope_store(q, k, v, G(qw), G(kw), G(cos), G(sin), 1e-6, 1e-6,
                                   cache_a.key[0], cache_a.value[0], gslots)
     out_a = torch.zeros(rows, heads, d, dtype=torch.bfloat16, device=device)
     paged_decode_attention(q_rot, cache_a, 0, meta, out_a, scale=scale)
 
-    cache_b = _Cache(G(kc), G(vc), bs)
+    cache_b = _Cache(G(kc), G(vc), bs, layout=layout)
     out_b = torch.zeros(rows, heads, d, dtype=torch.bfloat16, device=device)
     paged_decode_qk_norm_rope(q, k, v, G(qw), G(kw), G(cos), G(sin), 1e-6, 1e-6,
                               cache_b, 0, meta, gslots, out_b, scale=scale)

@@ -27,7 +27,8 @@ def _call(lib, fn, case, dev, out, workspace=None):
     args = [q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), v.data_ptr(),
             out.data_ptr(), out.stride(0), out.stride(1), rows.data_ptr(),
             blocks.data_ptr(), offsets.data_ptr(), lengths.data_ptr(), rows.numel(),
-            q.shape[1], hkv, d, k.shape[0], case["block_size"], case["max_len"],
+            q.shape[1], hkv, d, k.shape[0], k.stride(0), k.stride(1), case["block_size"],
+            case["max_len"],
             case["scale"]]
     if workspace is not None:
         args += [workspace.data_ptr() if workspace.numel() else None, workspace.numel()]
@@ -83,8 +84,8 @@ def test_noalloc_rejects_geometry_beyond_scratch():
         "need = lib.tvllm_paged_decode_workspace_size(64, 128, 8, 128, 1 << 20, 16)\n"
         "assert need > (8 << 20), need\n"
         "st = lib.tvllm_paged_decode_noalloc(None, 0, 0, None, None, None, 0, 0, None,"
-        " None, None, None, 64, 128, 8, 128, 1 << 24, 16, 1 << 20, 0.1, 0, 0, 1.0,"
-        " 1.0, None)\n"
+        " None, None, None, 64, 128, 8, 128, 1 << 24, 1024, 128, 16, 1 << 20, 0.1, 0, 0,"
+        " 1.0, 1.0, None)\n"
         "assert st == -1, st\n"
         "assert b'static scratch' in lib.tvllm_last_error()\n"
     ) % (str(ROOT / "tiny-vllm_amd"), str(ROOT))

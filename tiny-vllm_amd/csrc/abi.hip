@@ -20,7 +20,7 @@ void clear_error() { g_error[0] = '\0'; }
 
 extern "C" const char* tvllm_last_error(void) { return tvllm::g_error; }
 
-extern "C" int tvllm_abi_version(void) { return 4; }
+extern "C" int tvllm_abi_version(void) { return 5; }
 
 #ifndef TVLLM_SOURCE_HASH
 #define TVLLM_SOURCE_HASH "unknown"

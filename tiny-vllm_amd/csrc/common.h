@@ -49,6 +49,28 @@ inline bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
 
+// Paged KV-cache geometry: the row of (slot, KV head) starts at element
+// slot * slot_stride + head * head_stride and holds head_dim contiguous
+// elements. Rows must not overlap, which holds for the two nestings:
+// token-major (a slot's heads side by side: head_stride >= head_dim,
+// slot_stride >= kv_heads * head_stride) and head-major (a head's slots side
+// by side: slot_stride >= head_dim, head_stride >= num_slots * slot_stride).
+inline bool cache_layout_ok(int64_t num_slots, int64_t kv_heads, int64_t head_dim,
+                            int64_t slot_stride, int64_t head_stride) {
+    if (num_slots <= 0 || kv_heads <= 0 || head_dim <= 0) return false;
+    const bool token_major = head_stride >= head_dim &&
+                             slot_stride / kv_heads >= head_stride;
+    const bool head_major = slot_stride >= head_dim &&
+                            head_stride / num_slots >= slot_stride;
+    return token_major || head_major;
+}
+
+// Elements spanned by the cache (one past its last element).
+inline int64_t cache_extent(int64_t num_slots, int64_t kv_heads, int64_t head_dim,
+                            int64_t slot_stride, int64_t head_stride) {
+    return (num_slots - 1) * slot_stride + (kv_heads - 1) * head_stride + head_dim;
+}
+
 // ------------------------------------------------------------- elements --
 
 template <int DT> struct Elem;

@@ -131,6 +131,7 @@ struct DecodeArgs {
     int64_t qts, qhs;
     const void* k;  // cache rows: 16 units of 8 elements (16 B, or 8 B for FP8)
     const void* v;
+    int64_t css, chs;  // cache slot / head strides (elements, multiples of 8)
     T* out;
     int64_t ots, ohs;
     const int64_t* rows;
@@ -291,8 +292,6 @@ paged_decode_d128(DecodeArgs<T> a) {
     constexpr int D = 128;
     constexpr int ROW16 = D / 8;  // 8-element units per cache row of one head
     using Unit = std::conditional_t<F8, uint2, U16x8>;  // 8 cached elements
-    const Unit* const kc = static_cast<const Unit*>(a.k);
-    const Unit* const vc = static_cast<const Unit*>(a.v);
     constexpr int CH = 16 * NT;   // tokens per iteration
     static_assert(CH <= 64, "one lane resolves one token of an iteration");
     const int lane = threadIdx.x & 63;
@@ -309,6 +308,12 @@ paged_decode_d128(DecodeArgs<T> a) {
     const int split = wave - local_head * a.splits;
     const int kvh = (unit - r * head_groups) * a.heads_per_wg + local_head;
     const int h0 = kvh * a.group;
+    // This wave's KV head rows: slot s at unit s * slot_units past kc / vc
+    // (32-bit offsets: the host checks that every slot's offset fits).
+    const int64_t head_units = int64_t(__builtin_amdgcn_readfirstlane(kvh)) * (a.chs >> 3);
+    const Unit* const kc = static_cast<const Unit*>(a.k) + head_units;
+    const Unit* const vc = static_cast<const Unit*>(a.v) + head_units;
+    const uint64_t slot_units = uint64_t(a.css >> 3);
 
     const int64_t row = a.rows[r];
     const int64_t length = a.lengths[r];
@@ -407,7 +412,7 @@ paged_decode_d128(DecodeArgs<T> a) {
                 id = (rel >> 6) == uint32_t(r) ? other : id;
             }
             const uint64_t slot = uint64_t(id) * ubs + (t - page * ubs);
-            return static_cast<uint32_t>((slot * uint64_t(a.kv_heads) + uint64_t(kvh)) * ROW16);
+            return static_cast<uint32_t>(slot * slot_units);
         };
         Unit kreg[NT][4];  // [tile][k-slice]: token 16*tile + col
         Unit vreg[NT][4];  // [tile][i]:       token 16*tile + 4*quad + i
@@ -531,7 +536,7 @@ paged_decode_d128(DecodeArgs<T> a) {
                 const int64_t slot = new_slot;
                 if (slot >= 0) {
                     constexpr int EB = F8 ? 1 : int(sizeof(T));  // bytes per element
-                    const int64_t off = (slot * a.kv_heads + kvh) * D * EB;
+                    const int64_t off = (slot * a.css + int64_t(kvh) * a.chs) * EB;
                     write_new_kv<T, F8>(new_kv, a.k_eps,
                                         static_cast<char*>(a.kcache) + off,
                                         static_cast<char*>(a.vcache) + off, a.k_inv_scale,
@@ -826,8 +831,8 @@ paged_decode_merge(const float* __restrict__ part_o, const float* __restrict__ p
 template <typename T>
 __global__ void __launch_bounds__(64)
 paged_decode_generic(const T* __restrict__ q, int64_t qts, int64_t qhs,
-                     const T* __restrict__ k, const T* __restrict__ v,
-                     T* __restrict__ out, int64_t ots, int64_t ohs,
+                     const T* __restrict__ k, const T* __restrict__ v, int64_t css,
+                     int64_t chs, T* __restrict__ out, int64_t ots, int64_t ohs,
                      const int64_t* __restrict__ rows,
                      const int64_t* __restrict__ blocks,
                      const int64_t* __restrict__ offsets,
@@ -856,7 +861,7 @@ paged_decode_generic(const T* __restrict__ q, int64_t qts, int64_t qhs,
     for (int64_t t = 0; t < length; ++t) {
         const int64_t page = t / block_size;
         const int64_t slot = blocks[table + page] * block_size + (t - page * block_size);
-        const int64_t base = (slot * kv_heads + kvh) * head_dim;
+        const int64_t base = slot * css + kvh * chs;
         float dot = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -980,13 +985,18 @@ int heads_per_group(int64_t kv_heads, int64_t splits, int64_t waves) {
     return h;
 }
 
+// css / chs: the cache's slot and head strides (elements). 16-byte loads
+// need them in whole 16-byte units (8 elements, 16 for FP8 bytes), and the
+// kernel's 32-bit row offsets need every slot's offset below 2^32 units.
 bool fast_path(int64_t head_dim, int64_t group, const void* q, int64_t qts,
                int64_t qhs, const void* out, int64_t ots, int64_t ohs,
-               const void* k, const void* v, int64_t num_slots, int64_t kv_heads) {
+               const void* k, const void* v, int64_t num_slots, int64_t css, int64_t chs,
+               bool f8) {
+    const int64_t unit = f8 ? 16 : 8;
     return head_dim == 128 && group <= 16 && aligned16(q) && qts % 8 == 0 &&
            qhs % 8 == 0 && aligned16(out) && ots % 8 == 0 && ohs % 8 == 0 &&
-           aligned16(k) && aligned16(v) &&
-           num_slots * kv_heads * (head_dim / 8) <= int64_t(UINT32_MAX);
+           aligned16(k) && aligned16(v) && css % unit == 0 && chs % unit == 0 &&
+           num_slots * (css / 8) <= int64_t(UINT32_MAX);
 }
 
 }  // namespace
@@ -1044,7 +1054,8 @@ int paged_decode_impl(
     int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
     const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
-    int64_t block_size, int64_t max_context_len, float scale, void* workspace,
+    int64_t cache_slot_stride, int64_t cache_head_stride, int64_t block_size,
+    int64_t max_context_len, float scale, void* workspace,
     int64_t workspace_bytes, int dtype, int cache_dtype, float k_scale, float v_scale,
     tvllm_stream_t stream, const FusedIn* fused) {
     TVLLM_CHECK(head_dim > 0 && head_dim <= 256 && num_heads > 0 && num_kv_heads > 0,
@@ -1062,6 +1073,9 @@ int paged_decode_impl(
                 "paged_decode: KV scales must be positive and finite");
     TVLLM_CHECK(f8 || (k_scale == 1.f && v_scale == 1.f),
                 "paged_decode: KV scales apply to an FP8 cache only");
+    TVLLM_CHECK(cache_layout_ok(num_slots, num_kv_heads, head_dim, cache_slot_stride,
+                                cache_head_stride),
+                "paged_decode: cache strides must give non-overlapping head rows");
     if (num_rows == 0) return TVLLM_OK;
     TVLLM_CHECK(q && k_cache && v_cache && out && rows && blocks && offsets && lengths,
                 "paged_decode: null pointer");
@@ -1073,7 +1087,7 @@ int paged_decode_impl(
         using T = typename Elem<DT>::T;
         const bool fast = fast_path(head_dim, group, q, q_token_stride, q_head_stride, out,
                                     out_token_stride, out_head_stride, k_cache, v_cache,
-                                    num_slots, num_kv_heads);
+                                    num_slots, cache_slot_stride, cache_head_stride, f8);
         TVLLM_CHECK(fused == nullptr || fast,
                     "paged_decode_qk_norm_rope: needs head_dim 128, group <= 16 and "
                     "16-byte aligned rows");
@@ -1084,6 +1098,7 @@ int paged_decode_impl(
             paged_decode_generic<T><<<int(num_rows * num_heads), 64, 0, s>>>(
                 static_cast<const T*>(q), q_token_stride, q_head_stride,
                 static_cast<const T*>(k_cache), static_cast<const T*>(v_cache),
+                cache_slot_stride, cache_head_stride,
                 static_cast<T*>(out), out_token_stride, out_head_stride, rows,
                 blocks, offsets, lengths, int(num_heads), int(num_kv_heads),
                 int(head_dim), int(block_size), scale_log2);
@@ -1110,6 +1125,8 @@ int paged_decode_impl(
         args.qhs = q_head_stride;
         args.k = k_cache;
         args.v = v_cache;
+        args.css = cache_slot_stride;
+        args.chs = cache_head_stride;
         args.out = static_cast<T*>(out);
         args.ots = out_token_stride;
         args.ohs = out_head_stride;
@@ -1204,13 +1221,15 @@ extern "C" int tvllm_paged_decode(
     int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
     const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
-    int64_t block_size, int64_t max_context_len, float scale, void* workspace,
+    int64_t cache_slot_stride, int64_t cache_head_stride, int64_t block_size,
+    int64_t max_context_len, float scale, void* workspace,
     int64_t workspace_bytes, int dtype, int cache_dtype, float k_scale, float v_scale,
     tvllm_stream_t stream) {
     return paged_decode_impl(q, q_token_stride, q_head_stride, k_cache, v_cache, out,
                              out_token_stride, out_head_stride, rows, blocks, offsets,
                              lengths, num_rows, num_heads, num_kv_heads, head_dim,
-                             num_slots, block_size, max_context_len, scale, workspace,
+                             num_slots, cache_slot_stride, cache_head_stride, block_size,
+                             max_context_len, scale, workspace,
                              workspace_bytes, dtype, cache_dtype, k_scale, v_scale, stream,
                              nullptr);
 }
@@ -1263,7 +1282,8 @@ extern "C" int tvllm_paged_decode_noalloc(
     int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
     const int64_t* offsets, const int64_t* lengths, int64_t num_rows,
     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t num_slots,
-    int64_t block_size, int64_t max_context_len, float scale, int dtype,
+    int64_t cache_slot_stride, int64_t cache_head_stride, int64_t block_size,
+    int64_t max_context_len, float scale, int dtype,
     int cache_dtype, float k_scale, float v_scale, tvllm_stream_t stream) {
     const int64_t need = tvllm_paged_decode_workspace_size(
         num_rows, num_heads, num_kv_heads, head_dim, max_context_len, block_size);
@@ -1281,7 +1301,8 @@ extern "C" int tvllm_paged_decode_noalloc(
     return paged_decode_impl(q, q_token_stride, q_head_stride, k_cache, v_cache, out,
                              out_token_stride, out_head_stride, rows, blocks, offsets,
                              lengths, num_rows, num_heads, num_kv_heads, head_dim,
-                             num_slots, block_size, max_context_len, scale, ws,
+                             num_slots, cache_slot_stride, cache_head_stride, block_size,
+                             max_context_len, scale, ws,
                              need > 0 ? kScratchBytes : 0, dtype, cache_dtype, k_scale,
                              v_scale, stream, nullptr);
 }
@@ -1294,7 +1315,8 @@ extern "C" int tvllm_paged_decode_qk_norm_rope(
     void* v_cache, void* out, int64_t out_token_stride, int64_t out_head_stride,
     const int64_t* rows, const int64_t* blocks, const int64_t* offsets,
     const int64_t* lengths, int64_t num_rows, int64_t num_heads, int64_t num_kv_heads,
-    int64_t head_dim, int64_t num_slots, int64_t block_size, int64_t max_context_len,
+    int64_t head_dim, int64_t num_slots, int64_t cache_slot_stride,
+    int64_t cache_head_stride, int64_t block_size, int64_t max_context_len,
     float scale, void* workspace, int64_t workspace_bytes, int dtype, int cache_dtype,
     float k_scale, float v_scale, tvllm_stream_t stream) {
     TVLLM_CHECK(head_dim == 128, "paged_decode_qk_norm_rope: head_dim must be 128");
@@ -1307,7 +1329,8 @@ extern "C" int tvllm_paged_decode_qk_norm_rope(
     return paged_decode_impl(q, q_token_stride, q_head_stride, k_cache, v_cache, out,
                              out_token_stride, out_head_stride, rows, blocks, offsets,
                              lengths, num_rows, num_heads, num_kv_heads, head_dim,
-                             num_slots, block_size, max_context_len, scale, workspace,
+                             num_slots, cache_slot_stride, cache_head_stride, block_size,
+                             max_context_len, scale, workspace,
                              workspace_bytes, dtype, cache_dtype, k_scale, v_scale, stream,
                              &f);
 }

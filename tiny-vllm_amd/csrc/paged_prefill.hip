@@ -95,6 +95,7 @@ struct PrefillArgs {
     int64_t qts, qhs;
     const void* k;  // cache rows: T elements, or FP8 E4M3 bytes (F8 kernels)
     const void* v;
+    int64_t css, chs;  // cache slot / head strides (elements)
     T* out;
     int64_t ots, ohs;
     const int64_t* q_offsets;
@@ -224,10 +225,12 @@ paged_prefill_d128(PrefillArgs<T> a) {
             tq = is_v ? (job & 15) : ((job >> 4) & 15);
             piece = is_v ? ((job >> 4) & 15) : (job & 15);
         };
-        // Token positions fit in 32 bits (contexts < 2^31) and slots in 32 bits
-        // (checked on the host); the element offset of a slot is formed in 64 bits.
+        // Token positions fit in 32 bits (contexts < 2^31), slots and the
+        // slot stride in bytes too (checked on the host); the byte offset of a
+        // slot is formed in 64 bits.
         const int end1 = int(kv_end) - 1;
-        const uint32_t slot_elems = uint32_t(a.kv_heads) * D;
+        const uint32_t slot_elems = uint32_t(a.css);
+        const int64_t head_elems = int64_t(kvh) * a.chs;
         // QUAD (power-of-two pages of >= 4 tokens): a job's 4 tokens share a
         // page, so one block id serves all four. A template parameter, not a
         // branch: two load paths in the loop would make the wait-count pass
@@ -266,7 +269,7 @@ paged_prefill_d128(PrefillArgs<T> a) {
                 job_coords(r, is_v, tq, piece);
                 const int t0 = max(tile_base + lead_of(is_v), 0) * BK;
                 const char* src = static_cast<const char*>(is_v ? a.v : a.k) +
-                                  int64_t(kvh * D + piece * 8) * EB;
+                                  (head_elems + piece * 8) * EB;
                 const uint32_t row_bytes = slot_elems * EB;
                 if constexpr (quad_pages) {
                     // The quad's tokens are consecutive slots of one page:
@@ -607,7 +610,8 @@ extern "C" int tvllm_paged_prefill(
     int64_t out_head_stride, const int64_t* q_offsets, const int64_t* blocks,
     const int64_t* block_offsets, const int64_t* context_lens, int64_t num_items,
     int64_t max_query_len, int64_t num_heads, int64_t num_kv_heads,
-    int64_t head_dim, int64_t num_slots, int64_t block_size, float scale,
+    int64_t head_dim, int64_t num_slots, int64_t cache_slot_stride,
+    int64_t cache_head_stride, int64_t block_size, float scale,
     void* workspace, int64_t workspace_bytes,
     int dtype, int cache_dtype, float k_scale, float v_scale, tvllm_stream_t stream) {
     TVLLM_CHECK(head_dim == 128, "paged_prefill: head_dim must be 128");
@@ -623,6 +627,13 @@ extern "C" int tvllm_paged_prefill(
     TVLLM_CHECK(block_size > 0 && num_slots % block_size == 0,
                 "paged_prefill: invalid block geometry");
     TVLLM_CHECK(num_slots <= INT32_MAX, "paged_prefill: at most 2^31-1 cache slots");
+    TVLLM_CHECK(cache_layout_ok(num_slots, num_kv_heads, head_dim, cache_slot_stride,
+                                cache_head_stride),
+                "paged_prefill: cache strides must give non-overlapping head rows");
+    TVLLM_CHECK(cache_slot_stride % 8 == 0 && cache_head_stride % 8 == 0 &&
+                    cache_slot_stride * (f8 ? 1 : 2) <= int64_t(UINT32_MAX),
+                "paged_prefill: cache strides must be whole 8-element units "
+                "(slot stride below 2^32 bytes)");
     TVLLM_CHECK(num_items >= 0 && max_query_len >= 0,
                 "paged_prefill: negative sizes");
     TVLLM_CHECK(scale > 0.f && scale < INFINITY, "paged_prefill: scale must be positive");
@@ -667,6 +678,8 @@ extern "C" int tvllm_paged_prefill(
         args.qhs = q_head_stride;
         args.k = k_cache;
         args.v = v_cache;
+        args.css = cache_slot_stride;
+        args.chs = cache_head_stride;
         args.out = static_cast<T*>(out);
         args.ots = out_token_stride;
         args.ohs = out_head_stride;

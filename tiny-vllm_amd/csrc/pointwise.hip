@@ -356,7 +356,7 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
                     float q_eps, float k_eps, T* __restrict__ q_out,
                     T* __restrict__ k_out, const T* __restrict__ v, int64_t vts,
                     int64_t vhs, void* __restrict__ key_cache,
-                    void* __restrict__ value_cache,
+                    void* __restrict__ value_cache, int64_t css, int64_t chs,
                     const int64_t* __restrict__ slots, float k_inv, float v_inv) {
     const int lane = threadIdx.x & 63;
     const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -409,7 +409,7 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
     } else if (key_cache != nullptr) {
         slot = slots[tok];
         if (slot >= 0) {
-            const int64_t off = (slot * kv_heads + h) * head_dim;
+            const int64_t off = slot * css + h * chs;
             if constexpr (F8) dst8 = static_cast<uint8_t*>(key_cache) + off;
             else dst = static_cast<T*>(key_cache) + off;
         }
@@ -449,7 +449,7 @@ qk_norm_rope_kernel(const T* __restrict__ q, int64_t qts, int64_t qhs,
 
     if (!is_q && key_cache != nullptr && slot >= 0) {
         const T* vsrc = v + tok * vts + h * vhs;
-        const int64_t off = (slot * kv_heads + h) * head_dim;
+        const int64_t off = slot * css + h * chs;
         if constexpr (F8) {
             uint8_t* vdst = static_cast<uint8_t*>(value_cache) + off;
             for (int d = lane; d < head_dim; d += 64)
@@ -479,8 +479,8 @@ qk_norm_rope_d128(const T* __restrict__ q, int64_t qts, int64_t qhs,
                   int64_t tokens, int heads, int kv_heads, float q_eps, float k_eps,
                   T* __restrict__ q_out, T* __restrict__ k_out, const T* __restrict__ v,
                   int64_t vts, int64_t vhs, void* __restrict__ key_cache,
-                  void* __restrict__ value_cache, const int64_t* __restrict__ slots,
-                  float k_inv, float v_inv) {
+                  void* __restrict__ value_cache, int64_t css, int64_t chs,
+                  const int64_t* __restrict__ slots, float k_inv, float v_inv) {
     constexpr int D = 128, H = 64;
     const int j = threadIdx.x & 15;
     const int64_t row = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4);
@@ -552,7 +552,7 @@ qk_norm_rope_d128(const T* __restrict__ q, int64_t qts, int64_t qhs,
         store4(dst + H + 4 * j, o2);
     }
     if (key_cache == nullptr || slot < 0) return;
-    const int64_t off = (slot * kv_heads + h) * D;
+    const int64_t off = slot * css + h * chs;
     const T* vsrc = v + tok * vts + h * vhs + 8 * j;
     const uint2 va = *reinterpret_cast<const uint2*>(vsrc);
     const uint2 vb = *reinterpret_cast<const uint2*>(vsrc + 4);
@@ -697,8 +697,9 @@ extern "C" int tvllm_qk_norm_rope(
     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, float q_eps,
     float k_eps, void* q_out, void* k_out, const void* v, int64_t v_token_stride,
     int64_t v_head_stride, void* key_cache, void* value_cache,
-    const int64_t* slots, int64_t num_slots, int dtype, int cache_dtype, float k_scale,
-    float v_scale, tvllm_stream_t stream) {
+    const int64_t* slots, int64_t num_slots, int64_t cache_slot_stride,
+    int64_t cache_head_stride, int dtype, int cache_dtype, float k_scale, float v_scale,
+    tvllm_stream_t stream) {
     TVLLM_CHECK(tokens >= 0 && num_heads > 0 && num_kv_heads > 0,
                 "qk_norm_rope: Q/K must have positive head counts");
     const bool f8 = cache_dtype == TVLLM_FP8_E4M3;
@@ -717,6 +718,10 @@ extern "C" int tvllm_qk_norm_rope(
                 "qk_norm_rope: fused KV write needs v, value_cache and slots");
     TVLLM_CHECK(fused || k_out != nullptr, "qk_norm_rope: k_out is required");
     TVLLM_CHECK(!fused || tokens <= num_slots, "qk_norm_rope: too many KV rows");
+    TVLLM_CHECK(!fused || cache_layout_ok(num_slots, num_kv_heads, head_dim,
+                                          cache_slot_stride, cache_head_stride),
+                "qk_norm_rope: cache strides must give non-overlapping head rows");
+    const int64_t css = cache_slot_stride, chs = cache_head_stride;
     const int64_t rows = tokens * (num_heads + num_kv_heads);
     if (rows == 0) return TVLLM_OK;
     TVLLM_CHECK(q && k && q_weight && k_weight && cos && sin && q_out,
@@ -728,7 +733,8 @@ extern "C" int tvllm_qk_norm_rope(
                       a8(q_weight) && a8(k_weight) && a8(cos) && a8(sin) && a8(q_out) &&
                       (k_out == nullptr || a8(k_out)) &&
                       (!fused || (v_token_stride % 4 == 0 && v_head_stride % 4 == 0 && a8(v) &&
-                                  a8(key_cache) && a8(value_cache)));
+                                  a8(key_cache) && a8(value_cache) && css % 8 == 0 &&
+                                  chs % 8 == 0));
     return dispatch_half(dtype, [&]<int DT>() {
         using T = typename Elem<DT>::T;
         const int blocks = int((rows + 3) / 4);
@@ -745,7 +751,7 @@ extern "C" int tvllm_qk_norm_rope(
                     static_cast<const T*>(cos), static_cast<const T*>(sin), tokens,
                     int(num_heads), int(num_kv_heads), q_eps, k_eps, static_cast<T*>(q_out),
                     static_cast<T*>(k_out), static_cast<const T*>(v), v_token_stride,
-                    v_head_stride, key_cache, value_cache, slots, k_inv, v_inv);
+                    v_head_stride, key_cache, value_cache, css, chs, slots, k_inv, v_inv);
             };
             if (f8) go128.template operator()<true>();
             else go128.template operator()<false>();
@@ -761,7 +767,7 @@ extern "C" int tvllm_qk_norm_rope(
         int(num_heads), int(num_kv_heads), int(head_dim), q_eps, k_eps,          \
         static_cast<T*>(q_out), static_cast<T*>(k_out),                          \
         static_cast<const T*>(v), v_token_stride, v_head_stride,                 \
-        key_cache, value_cache, slots, k_inv, v_inv)
+        key_cache, value_cache, css, chs, slots, k_inv, v_inv)
             if (half <= 64) TVLLM_QKR(1);
             else if (half <= 128) TVLLM_QKR(2);
             else if (half <= 256) TVLLM_QKR(4);

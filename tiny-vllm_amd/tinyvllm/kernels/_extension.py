@@ -19,7 +19,7 @@ from pathlib import Path
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libtinyvllm_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -31,22 +31,24 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_abi_version": (_INT, []),
     "tvllm_source_hash": (ctypes.c_char_p, []),
     "tvllm_store_kv": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, _P,
-                              _I64, _I64, _I64, _I64, _INT, _INT, _F32, _F32, _P]),
+                              _I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, _F32, _F32,
+                              _P]),
     "tvllm_paged_decode_workspace_size": (_I64, [_I64] * 6),
     "tvllm_paged_decode_split_plan": (_I64, [_I64] * 6),
     "tvllm_paged_decode": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64,
                                   _P, _P, _P, _P, _I64, _I64, _I64, _I64,
-                                  _I64, _I64, _I64, _F32, _P, _I64, _INT, _INT, _F32,
-                                  _F32, _P]),
+                                  _I64, _I64, _I64, _I64, _I64, _F32, _P, _I64, _INT, _INT,
+                                  _F32, _F32, _P]),
     "tvllm_paged_decode_noalloc": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64,
                                           _P, _P, _P, _P, _I64, _I64, _I64, _I64,
-                                          _I64, _I64, _I64, _F32, _INT, _INT, _F32,
-                                          _F32, _P]),
+                                          _I64, _I64, _I64, _I64, _I64, _F32, _INT, _INT,
+                                          _F32, _F32, _P]),
     "tvllm_paged_decode_qk_norm_rope": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64,
                                                _I64, _P, _P, _P, _P, _F32, _F32, _P, _P,
                                                _P, _P, _I64, _I64, _P, _P, _P, _P, _I64,
-                                               _I64, _I64, _I64, _I64, _I64, _I64, _F32,
-                                               _P, _I64, _INT, _INT, _F32, _F32, _P]),
+                                               _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                               _I64, _F32, _P, _I64, _INT, _INT, _F32, _F32,
+                                               _P]),
     "tvllm_rms_norm": (_INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64,
                               _P, _P, _F32, _INT, _P]),
     "tvllm_silu_and_mul": (_INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _INT, _P]),
@@ -54,8 +56,8 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
                                            _P, _P, _F32, _INT, _P]),
     "tvllm_qk_norm_rope": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P,
                                   _P, _I64, _I64, _I64, _I64, _F32, _F32, _P,
-                                  _P, _P, _I64, _I64, _P, _P, _P, _I64, _INT,
-                                  _INT, _F32, _F32, _P]),
+                                  _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64,
+                                  _INT, _INT, _F32, _F32, _P]),
     "tvllm_argmax": (_INT, [_P, _I64, _I64, _I64, _P, _INT, _P]),
     "tvllm_sample_workspace_size": (_I64, [_I64, _I64]),
     "tvllm_sample": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
@@ -64,8 +66,8 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
     "tvllm_apply_table_updates": (_INT, [_P, _I64, _P, _I64, _P]),
     "tvllm_paged_prefill": (_INT, [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _P,
                                    _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
-                                   _I64, _I64, _F32, _P, _I64, _INT, _INT, _F32, _F32,
-                                   _P]),
+                                   _I64, _I64, _I64, _I64, _F32, _P, _I64, _INT, _INT, _F32,
+                                   _F32, _P]),
     "tvllm_paged_prefill_workspace_size": (_I64, [_INT, _INT]),
 }
 

@@ -26,6 +26,8 @@ def store_kv(
     device = require_gpu(key, value, key_cache, value_cache, slots)
     if key.dtype not in (torch.float16, torch.bfloat16):
         raise RuntimeError("KV store requires float16 or bfloat16")
+    if key_cache.stride() != value_cache.stride():
+        raise RuntimeError("K/V caches must share one layout")
     for tensor in (value,) if cache.fp8 else (value, key_cache, value_cache):
         if tensor.dtype != key.dtype:
             raise RuntimeError("KV dtype mismatch")
@@ -45,7 +47,7 @@ def store_kv(
         key.stride(0), key.stride(1), value.stride(0), value.stride(1),
         key_cache.data_ptr(), value_cache.data_ptr(), slots.data_ptr(),
         key.shape[0], key.shape[1], key.shape[2], key_cache.shape[0],
-        dtype_code(key.dtype), *cache_format(cache), stream_of(device),
+        key_cache.stride(0), key_cache.stride(1), dtype_code(key.dtype), *cache_format(cache), stream_of(device),
     ))
 
 

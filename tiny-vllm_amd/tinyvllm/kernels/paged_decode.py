@@ -57,6 +57,8 @@ def paged_decode_attention(
     device = require_gpu(q, k, v, output, rows, blocks, offsets, lengths)
     if q.dim() != 3:
         raise RuntimeError("Q must be a GPU [tokens, heads, dim] tensor")
+    if k.stride() != v.stride():
+        raise RuntimeError("K/V caches must share one layout")
     if q.dtype not in (torch.float16, torch.bfloat16):
         raise RuntimeError("Q must use float16 or bfloat16")
     if (k.dtype != q.dtype and not cache.fp8) or output.dtype != q.dtype:
@@ -85,7 +87,7 @@ def paged_decode_attention(
         k.data_ptr(), v.data_ptr(),
         output.data_ptr(), output.stride(0), output.stride(1),
         rows.data_ptr(), blocks.data_ptr(), offsets.data_ptr(), lengths.data_ptr(),
-        num_rows, heads, cache.num_kv_heads, dim, cache.num_slots,
+        num_rows, heads, cache.num_kv_heads, dim, cache.num_slots, k.stride(0), k.stride(1),
         cache.block_size, max_len, float(scale),
         workspace.data_ptr() if need else None, need,
         dtype_code(q.dtype), *cache_format(cache), stream_of(device),
@@ -130,6 +132,8 @@ def paged_decode_qk_norm_rope(
             t.dtype != q.dtype for t in (k, v, query_weight, key_weight, cos, sin, output)) \
             or (kc.dtype != q.dtype and not cache.fp8):
         raise RuntimeError("Q/K/V, weights, RoPE tables and cache must share a half dtype")
+    if vc.stride() != kc.stride():
+        raise RuntimeError("K/V caches must share one layout")
     if any(t.stride(-1) != 1 for t in (q, k, v, output)) or output.shape != q.shape:
         raise RuntimeError("Q/K/V/output rows must have unit last stride")
     if (query_weight.shape != (128,) or key_weight.shape != (128,)
@@ -164,7 +168,7 @@ def paged_decode_qk_norm_rope(
         output.stride(0), output.stride(1), m.query_rows.data_ptr(),
         m.block_table_ids.data_ptr(), m.block_table_offsets.data_ptr(),
         m.context_lens.data_ptr(), num_rows, heads, cache.num_kv_heads, 128,
-        cache.num_slots, cache.block_size, max_len, float(scale),
+        cache.num_slots, kc.stride(0), kc.stride(1), cache.block_size, max_len, float(scale),
         workspace.data_ptr() if need else None, need, dtype_code(q.dtype),
         *cache_format(cache), stream_of(device),
     ))

@@ -31,6 +31,8 @@ def paged_prefill_attention(
     m = metadata
     device = require_gpu(q, k, v, output, m.query_offsets, m.block_table_ids,
                          m.block_table_offsets, m.context_lens)
+    if k.stride() != v.stride():
+        raise RuntimeError("K/V caches must share one layout")
     if q.dim() != 3 or output.shape != q.shape:
         raise RuntimeError("Q/output must be [tokens, heads, dim] tensors")
     if q.dtype not in (torch.float16, torch.bfloat16) or output.dtype != q.dtype \
@@ -56,7 +58,7 @@ def paged_prefill_attention(
         m.query_offsets.data_ptr(), m.block_table_ids.data_ptr(),
         m.block_table_offsets.data_ptr(), m.context_lens.data_ptr(),
         items, m.max_query_len, q.shape[1], cache.num_kv_heads, q.shape[2],
-        cache.num_slots, cache.block_size, float(scale),
+        cache.num_slots, k.stride(0), k.stride(1), cache.block_size, float(scale),
         None if guard is None else guard.data_ptr(), 0 if guard is None else guard.numel(),
         dtype_code(q.dtype), cache_dtype, k_scale, v_scale, stream_of(device),
     ))

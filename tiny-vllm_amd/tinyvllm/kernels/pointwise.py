@@ -176,7 +176,7 @@ def qk_norm_rope(
             query_weight.data_ptr(), key_weight.data_ptr(), cos.data_ptr(),
             sin.data_ptr(), query.shape[0], query.shape[1], key.shape[1],
             query.shape[2], float(query_eps), float(key_eps),
-            q_out.data_ptr(), k_out.data_ptr(), None, 0, 0, None, None, None, 0,
+            q_out.data_ptr(), k_out.data_ptr(), None, 0, 0, None, None, None, 0, 0, 0,
             dtype_code(query.dtype), dtype_code(query.dtype), 1.0, 1.0, stream_of(device),
         ))
     return q_out, k_out
@@ -214,10 +214,12 @@ def qk_norm_rope_store(
     if value.shape != key.shape or value.dtype != key.dtype or value.stride(2) != 1:
         raise RuntimeError("V must match K's shape and dtype with unit last stride")
     if (key_cache.dim() != 3 or tuple(key_cache.shape[1:]) != tuple(key.shape[1:])
-            or value_cache.shape != key_cache.shape or not key_cache.is_contiguous()
-            or not value_cache.is_contiguous() or value_cache.dtype != key_cache.dtype
+            or value_cache.shape != key_cache.shape
+            or value_cache.stride() != key_cache.stride() or key_cache.stride(2) != 1
+            or value_cache.dtype != key_cache.dtype
             or key_cache.dtype not in (key.dtype, torch.float8_e4m3fn)):
-        raise RuntimeError("KV caches must be contiguous [slots, kv_heads, dim]")
+        raise RuntimeError("KV caches must be [slots, kv_heads, dim] views of one layout "
+                           "with unit last stride")
     if slots.dtype != torch.long or slots.dim() != 1 or not slots.is_contiguous() \
             or slots.numel() != key.shape[0]:
         raise RuntimeError("slots must be contiguous GPU int64 matching token rows")
@@ -233,7 +235,8 @@ def qk_norm_rope_store(
             q_out.data_ptr(), k_out.data_ptr() if k_out is not None else None,
             value.data_ptr(), value.stride(0), value.stride(1),
             key_cache.data_ptr(), value_cache.data_ptr(), slots.data_ptr(),
-            key_cache.shape[0], dtype_code(query.dtype), dtype_code(key_cache.dtype),
+            key_cache.shape[0], key_cache.stride(0), key_cache.stride(1),
+            dtype_code(query.dtype), dtype_code(key_cache.dtype),
             float(k_scale), float(v_scale), stream_of(device),
         ))
     return q_out, k_out

@@ -2,11 +2,25 @@
 
 Layout contract (kept identical to the reference, paged_kv.py:53-65):
 ``key``/``value`` are ``[num_layers, num_blocks * block_size, num_kv_heads,
-head_dim]``; token position p of a request whose block table is ``table``
-lives at slot ``table[p // block_size] * block_size + p % block_size``.
-One slot row of one layer is ``num_kv_heads * head_dim`` contiguous elements
-(2 KiB for Qwen3's 8 x 128 bf16), so a 16-token page of one layer is 32 KiB
-of contiguous HBM.
+head_dim]`` tensors; token position p of a request whose block table is
+``table`` lives at slot ``table[p // block_size] * block_size + p %
+block_size``, and ``key[layer][slot]`` is that token's [kv_heads, head_dim]
+row, indexed exactly as in the reference.
+
+Storage underneath: ``layout="token_major"`` (default) stores that shape
+contiguously, as the reference does: one slot row of one layer is
+``num_kv_heads * head_dim`` elements (2 KiB for Qwen3's 8 x 128 bf16), and a
+16-token page of one KV head is 16 pieces of 256 bytes at a 2 KiB stride.
+``layout="head_major"`` (beyond the reference) stores ``[num_layers,
+num_kv_heads, num_slots, head_dim]`` and makes ``key``/``value`` permuted
+views of it, so that page is 4 KiB of contiguous HBM. Gathered 4 KiB pages
+stream at 6.6-6.7 TB/s on MI355X when at least four waves read each head,
+the 256-byte pieces at 6.3-6.35 TB/s; with two waves per head the pieces
+read faster (5.25 vs 5.05 TB/s), since the heads of a token then arrive
+together. So head-major pays for few rows with long contexts (Qwen3-32B,
+16 rows at 16-32k: 253 -> 238 us per decode call) and costs at many rows
+(Qwen3-8B, 64 rows at 2k: 87.5 -> 90.3 us). The kernels take the views'
+slot and head strides, so they serve either.
 
 Slots and block ids are validated on the CPU before lowering (ModelRunner);
 this class checks shapes/devices only and never synchronises on GPU values.
@@ -25,6 +39,19 @@ from tinyvllm._validation import _check_non_negative_int, _check_positive_int
 
 FP8_DTYPE = torch.float8_e4m3fn
 _MODEL_DTYPES = (torch.float16, torch.bfloat16)
+LAYOUTS = ("head_major", "token_major")
+
+
+def resolve_layout(layout: str, max_rows: int, kv_heads: int) -> str:
+    """``layout``, with "auto" resolved for a cache read by at most
+    ``max_rows`` decode rows at once: head-major below 256 (row, KV head)
+    pairs (few rows, so long contexts split into many waves per head),
+    token-major otherwise."""
+    if layout == "auto":
+        return "head_major" if max_rows * kv_heads < 256 else "token_major"
+    if layout not in LAYOUTS:
+        raise ValueError(f"layout must be 'auto' or one of {LAYOUTS}")
+    return layout
 
 
 class PagedKVCache:
@@ -42,7 +69,10 @@ class PagedKVCache:
         dtype: torch.dtype,
         k_scale: float = 1.0,
         v_scale: float = 1.0,
+        layout: str = "token_major",
     ) -> None:
+        if layout not in LAYOUTS:
+            raise ValueError(f"layout must be one of {LAYOUTS}")
         for name, value in (
             ("num_layers", num_layers),
             ("num_blocks", num_blocks),
@@ -70,9 +100,15 @@ class PagedKVCache:
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
         self.num_slots = num_blocks * block_size
-        shape = (num_layers, self.num_slots, num_kv_heads, head_dim)
-        self.key = torch.empty(shape, device=device, dtype=dtype)
-        self.value = torch.empty_like(self.key)
+        self.layout = layout
+        if layout == "head_major":
+            shape = (num_layers, num_kv_heads, self.num_slots, head_dim)
+            self.key = torch.empty(shape, device=device, dtype=dtype).permute(0, 2, 1, 3)
+            self.value = torch.empty(shape, device=device, dtype=dtype).permute(0, 2, 1, 3)
+        else:
+            shape = (num_layers, self.num_slots, num_kv_heads, head_dim)
+            self.key = torch.empty(shape, device=device, dtype=dtype)
+            self.value = torch.empty_like(self.key)
 
     @staticmethod
     def bytes_per_block(

@@ -15,7 +15,7 @@ from tinyvllm._validation import _check_positive_int
 from tinyvllm.batch import PreparedBatch
 from tinyvllm.kernels.paged_decode import decode_workspace_bytes
 from tinyvllm.kernels.sampling import resolve_tokens, sample
-from tinyvllm.paged_kv import PagedKVCache
+from tinyvllm.paged_kv import PagedKVCache, resolve_layout
 from tinyvllm.runtime.attention import HipAttention, SDPAAttention, check_backend
 from tinyvllm.runtime.contracts import (
     ModelInput, MultiQueryMetadata, PagedKVMetadata, SingleQueryMetadata,
@@ -42,10 +42,17 @@ class ModelRunner:
         kv_cache_dtype: torch.dtype | None = None,
         kv_scales: tuple[float, float] = (1.0, 1.0),
         prefill_graph_tokens: int = 2048,
+        kv_cache_layout: str = "auto",
     ) -> None:
         """``kv_cache_dtype``: None keeps K/V in the model dtype;
         ``torch.float8_e4m3fn`` stores them as FP8 E4M3 with ``kv_scales``
         (k_scale, v_scale) - a layout beyond the reference (hip backend).
+        ``kv_cache_layout``: the cache's storage order (``PagedKVCache``'s
+        ``layout``; both keep the reference's [layers, slots, heads, dim]
+        view); "auto" picks head-major when fewer than 256 (row, KV head)
+        pairs can decode at once (``max_num_seqs * num_kv_heads``: few rows,
+        whose long contexts split into many waves per head), else
+        token-major.
         ``prefill_graph_tokens``: prefill and mixed steps of up to this many
         tokens (and up to 16 items; single-token items of short context only)
         replay captured graphs (0: always eager; beyond the reference, which
@@ -86,6 +93,8 @@ class ModelRunner:
                 block_size=block_size, num_kv_heads=config.num_key_value_heads,
                 head_dim=config.head_dim, device=self.device, dtype=kv_dtype,
                 k_scale=float(kv_scales[0]), v_scale=float(kv_scales[1]),
+                layout=resolve_layout(kv_cache_layout, max_num_seqs,
+                                      config.num_key_value_heads),
             )
             if self.backend == "hip":
                 self.decode_inputs = DecodeInputs(
