@@ -1184,16 +1184,20 @@ int paged_decode_impl(
             paged_decode_d128<T, GP, 2, kMaxWaves, F, F8>                            \
                 <<<int(grid), threads, 0, s>>>(args);                                \
     } while (0)
-            // Groups above 4 carry 64+ accumulator registers per lane: one
-            // 16-token tile per iteration keeps them within 256 VGPRs.
+            // Groups above 4 carry 64+ accumulator registers per lane. A bf16
+            // cache keeps one 16-token tile per iteration there (two fit in
+            // 227 VGPRs but measured slower: Qwen3-32B C5 shape 237.5 ->
+            // 243 us); an FP8 tile is half the bytes, so FP8 takes four
+            // tiles at group 8 (218 VGPRs; C5 shape 168.6 -> 138.7 us: one
+            // tile left a wave with 2 KiB of K in flight) and two at 16.
             if (group <= 1) TVLLM_DEC(1);
             else if (group <= 2) TVLLM_DEC(2);
             else if (group <= 4) TVLLM_DEC(4);
             else if (group <= 8)
-                paged_decode_d128<T, 8, 1, kMaxWaves, F, F8>
+                paged_decode_d128<T, 8, F8 ? 4 : 1, kMaxWaves, F, F8>
                     <<<int(grid), threads, 0, s>>>(args);
             else
-                paged_decode_d128<T, 16, 1, kMaxWaves, F, F8>
+                paged_decode_d128<T, 16, F8 ? 2 : 1, kMaxWaves, F, F8>
                     <<<int(grid), threads, 0, s>>>(args);
         };
         if (fused && f8) launch.template operator()<true, true>();
