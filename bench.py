@@ -929,7 +929,8 @@ def main() -> None:
                         max_model_len=max_model_len, max_num_seqs=args.batch,
                         graph_sizes=(args.batch,),
                         kv_cache_dtype=torch.float8_e4m3fn if fp8 else None,
-                        kv_cache_layout=args.kv_layout)
+                        kv_cache_layout=args.kv_layout,
+                        prefill_graph_tokens=0)  # every timed step is a decode step
     cache = executor.runner.kv_cache
     gen = torch.Generator(device=device).manual_seed(1)
     if fp8:  # N(0, 1) values quantised layer by layer

@@ -83,13 +83,14 @@ class Executor:
                  graph_sizes: tuple[int, ...] | None = None,
                  kv_cache_dtype: torch.dtype | None = None,
                  kv_scales: tuple[float, float] = (1.0, 1.0),
-                 kv_cache_layout: str = "auto") -> None:
+                 kv_cache_layout: str = "auto", prefill_graph_tokens: int = 2048) -> None:
         self.runner = ModelRunner(model, block_size=block_size, num_blocks=num_blocks,
                                   max_model_len=max_model_len, max_num_seqs=max_num_seqs,
                                   attention_backend=attention_backend,
                                   enforce_eager=enforce_eager, graph_sizes=graph_sizes,
                                   kv_cache_dtype=kv_cache_dtype, kv_scales=kv_scales,
-                                  kv_cache_layout=kv_cache_layout)
+                                  kv_cache_layout=kv_cache_layout,
+                                  prefill_graph_tokens=prefill_graph_tokens)
         self.capabilities = ExecutorCapabilities(
             vocab_size=model.config.vocab_size,
             max_model_len=self.runner.max_model_len,
