@@ -199,6 +199,31 @@ int tvllm_paged_decode_qk_norm_rope(
     float scale, void* workspace, int64_t workspace_bytes, int dtype, int cache_dtype,
     float k_scale, float v_scale, tvllm_stream_t stream);
 
+/* tvllm_paged_decode_qk_norm_rope with the raw q/k/v given as four fp32
+ * split-K partials of the qkv projection instead of its rounded output:
+ * parts[s * slice_stride + row * row_stride + col], s < 4, a row holding
+ * the num_heads query heads, then the num_kv_heads key heads, then the
+ * value heads, 128 columns each (the [4, tokens, width] fp32 result of a
+ * batched torch.bmm over four slices of the reduction axis). Each raw
+ * element is ((p0 + p1) + p2) + p3 in fp32, rounded once to dtype - a
+ * single fp32-accumulating GEMM's rounding, up to the order of the sum -
+ * and then normalised, rotated, written and attended exactly as
+ * tvllm_paged_decode_qk_norm_rope does. parts must be 16-byte aligned, both
+ * strides whole multiples of 4 elements.
+ * No reference counterpart: it lets a decode step's qkv projection run as
+ * a split-K batched GEMM (which fills the GPU at decode batch sizes) with
+ * no extra launch to sum the slices. */
+int tvllm_paged_decode_qk_norm_rope_partials(
+    const float* parts, int64_t slice_stride, int64_t row_stride, const void* q_weight,
+    const void* k_weight, const void* cos, const void* sin, float q_eps, float k_eps,
+    const int64_t* slots, void* k_cache, void* v_cache, void* out, int64_t out_token_stride,
+    int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
+    const int64_t* offsets, const int64_t* lengths, int64_t num_rows, int64_t num_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t num_slots, int64_t cache_slot_stride,
+    int64_t cache_head_stride, int64_t block_size, int64_t max_context_len, float scale,
+    void* workspace, int64_t workspace_bytes, int dtype, int cache_dtype, float k_scale,
+    float v_scale, tvllm_stream_t stream);
+
 /* RMSNorm over rows of width `width`, optionally after a residual add:
  *   x = residual ? round(x + residual) : x
  *   out = round(round(x * rsqrt(mean(x^2) + eps)) * weight)

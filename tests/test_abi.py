@@ -62,6 +62,31 @@ def test_argument_errors_surface_without_touching_a_gpu():
         check(status)
 
 
+def test_qkv_partials_entry_point_contract():
+    """The split-K qkv decode entry point refuses rows too narrow for the
+    q/k/v heads and strides that are not whole float4 units."""
+    from tinyvllm.kernels._extension import check, load_kernels
+
+    lib = load_kernels()
+    # parts, slice/row strides, weights, cos, sin, eps x2, slots, caches, out +
+    # strides, rows/blocks/offsets/lengths, 0 rows of 32 Q / 8 KV heads, ...
+    base = [None, 0, 0, None, None, None, None, 1e-6, 1e-6, None, None, None, None, 0, 0,
+            None, None, None, None, 0, 32, 8, 128, 64, 1024, 128, 16, 64, 0.1, None, 0, 0,
+            0, 1.0, 1.0, None]
+    assert len(base) == 36
+    narrow = dict(enumerate(base))
+    narrow[2] = 47 * 128  # a row needs (32 + 2 * 8) * 128 columns
+    with pytest.raises(RuntimeError, match="q, k and v heads"):
+        check(lib.tvllm_paged_decode_qk_norm_rope_partials(*narrow.values()))
+    odd = dict(enumerate(base))
+    odd[2], odd[1] = 48 * 128, 6
+    with pytest.raises(RuntimeError, match="float4"):
+        check(lib.tvllm_paged_decode_qk_norm_rope_partials(*odd.values()))
+    ok = dict(enumerate(base))
+    ok[2], ok[1] = 48 * 128, 48 * 128 * 3
+    assert lib.tvllm_paged_decode_qk_norm_rope_partials(*ok.values()) == 0  # no rows
+
+
 def test_cache_layout_contract():
     """Both cache nestings are accepted (token-major [slots, heads, dim] and
     head-major [heads, slots, dim]); strides whose head rows would overlap

@@ -806,3 +806,85 @@ def test_decode_split_merge_reuses_its_workspace(device):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(graph_out.cpu(), outs[0])
+
+
+@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("heads,kv_heads,lengths,max_ctx", [
+    (32, 8, [2049, 1, 700, 0, 16, 17], 4096),   # group 4, a padding row
+    (16, 8, [300, 77, 1], 1024),                 # group 2
+    (64, 8, [5000, 33], 32768),                  # group 8, workgroup-level splits
+])
+def test_decode_fused_from_qkv_partials(device, heads, kv_heads, lengths, max_ctx, layout):
+    """The fused decode kernel fed the qkv projection as four fp32 split-K
+    partials equals the same kernel fed their in-order sum rounded to bf16:
+    the cache bits written and the attention output are identical."""
+    from tinyvllm.kernels.paged_decode import (paged_decode_qk_norm_rope,
+                                               paged_decode_qk_norm_rope_partials)
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    g = torch.Generator().manual_seed(sum(lengths) % 997 + heads)
+    bs, d = 16, 128
+    rows = len(lengths)
+    pages = [max(1, -(-n // bs)) for n in lengths]
+    pool = sum(pages) + 4
+    perm = torch.randperm(pool, generator=g)
+    blocks, offsets = [], [0]
+    for p in pages:
+        blocks += perm[offsets[-1]:offsets[-1] + p].tolist()
+        offsets.append(offsets[-1] + p)
+    slots = [blocks[offsets[r] + (n - 1) // bs] * bs + (n - 1) % bs if n > 0 else -1
+             for r, n in enumerate(lengths)]
+    kc = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(pool * bs, kv_heads, d, generator=g).to(torch.bfloat16)
+    width = (heads + 2 * kv_heads) * d
+    parts = torch.randn(4, rows, width, generator=g) * 0.5
+    summed = (((parts[0] + parts[1]) + parts[2]) + parts[3]).to(torch.bfloat16)
+    qw = (1 + 0.05 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.05 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    pos = torch.tensor([max(n - 1, 0) for n in lengths])
+    cos, sin = OP.rope_tables(pos, d, 1e6, torch.bfloat16)
+    G = lambda t: t.to(device)  # noqa: E731
+    meta = SingleQueryMetadata(G(torch.arange(rows)), G(torch.tensor(blocks)),
+                               G(torch.tensor(offsets)), G(torch.tensor(lengths)), max_ctx)
+    gslots = G(torch.tensor(slots))
+    args = (G(qw), G(kw), G(cos), G(sin), 1e-6, 1e-6)
+    gs = G(summed)
+    q = gs[:, :heads * d].view(rows, heads, d)
+    k = gs[:, heads * d:(heads + kv_heads) * d].view(rows, kv_heads, d)
+    v = gs[:, (heads + kv_heads) * d:].view(rows, kv_heads, d)
+    cache_a = _Cache(G(kc), G(vc), bs, layout=layout)
+    out_a = torch.zeros(rows, heads, d, dtype=torch.bfloat16, device=device)
+    paged_decode_qk_norm_rope(q, k, v, *args, cache_a, 0, meta, gslots, out_a, scale=d ** -0.5)
+    cache_b = _Cache(G(kc), G(vc), bs, layout=layout)
+    out_b = torch.full((rows, heads, d), 5.0, dtype=torch.bfloat16, device=device)
+    paged_decode_qk_norm_rope_partials(G(parts), heads, *args, cache_b, 0, meta, gslots, out_b,
+                                       scale=d ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(cache_a.key[0].cpu(), cache_b.key[0].cpu())
+    assert torch.equal(cache_a.value[0].cpu(), cache_b.value[0].cpu())
+    assert torch.equal(out_a.cpu(), out_b.cpu())
+
+
+def test_qkv_decode_partials_rule_and_values(device):
+    """PackedLinear.decode_partials: four fp32 slices whose sum is the
+    projection (within fp32 rounding), only at decode batch sizes."""
+    from tinyvllm.layers import PackedLinear
+
+    torch.manual_seed(0)
+    small = PackedLinear(1024, (2048, 1024, 1024), device=device, dtype=torch.bfloat16)
+    wide = PackedLinear(4096, (4096, 1024, 1024), device=device, dtype=torch.bfloat16)
+    x = torch.randn(32, 1024, device=device, dtype=torch.bfloat16)
+    parts = small.decode_partials(x)
+    assert parts.shape == (4, 32, 4096) and parts.dtype == torch.float32
+    ref = x.float() @ small.weight.float().t()
+    assert (parts.sum(0) - ref).abs().max().item() < 1e-3
+    assert small.decode_partials(torch.randn(65, 1024, device=device,
+                                             dtype=torch.bfloat16)) is None
+    assert small.decode_partials(x[:16]) is None                 # 16 rows: one GEMM
+    assert wide.decode_partials(torch.randn(64, 4096, device=device,
+                                            dtype=torch.bfloat16)) is None
+    wider = PackedLinear(5120, (8192, 1024, 1024), device=device, dtype=torch.bfloat16)
+    assert wider.decode_partials(torch.randn(64, 5120, device=device,
+                                             dtype=torch.bfloat16)).shape == (4, 64, 10240)
+    assert wider.decode_partials(torch.randn(32, 5120, device=device,
+                                             dtype=torch.bfloat16)) is None

@@ -164,7 +164,14 @@ struct DecodeArgs {
     void* kcache;       // writable views of k / v
     void* vcache;
     const int64_t* slots;
+    // Split-K qkv (PARTS kernels): the raw projections as kQkvParts fp32
+    // slices of the reduction, [slice][row][q heads | k heads | v heads]
+    // x 128, slice stride pss and row stride pts (elements).
+    const float* parts;
+    int64_t pss, pts;
 };
+
+constexpr int kQkvParts = 4;
 
 constexpr int kMaxWaves = 8;  // 2 resident waves per SIMD at <= 256 VGPRs
 constexpr int64_t kMaxSplits = 64;
@@ -245,6 +252,32 @@ __device__ __forceinline__ NewKV<T> load_new_kv(const T* __restrict__ k, const T
                     v[lane], v[lane + 64]};
 }
 
+// The same inputs from split-K partials: each raw element is the fp32 sum of
+// its kQkvParts slices in slice order, rounded once to T (what a single GEMM
+// with fp32 accumulation stores, up to the order of the sum).
+template <typename T>
+__device__ __forceinline__ float sum_parts(const float* __restrict__ p, int64_t pss) {
+    float x[kQkvParts];
+#pragma unroll
+    for (int s = 0; s < kQkvParts; ++s) x[s] = p[s * pss];
+    float t = x[0];
+#pragma unroll
+    for (int s = 1; s < kQkvParts; ++s) t += x[s];
+    return t;
+}
+
+template <typename T>
+__device__ __forceinline__ NewKV<T> load_new_kv_parts(const float* __restrict__ k,
+                                                   const float* __restrict__ v, int64_t pss,
+                                                   const T* __restrict__ w,
+                                                   const T* __restrict__ cs,
+                                                   const T* __restrict__ sn, int lane) {
+    return NewKV<T>{rnd<T>(sum_parts<T>(k + lane, pss)), rnd<T>(sum_parts<T>(k + lane + 64, pss)),
+                    to_f<T>(w[lane]), to_f<T>(w[lane + 64]), to_f<T>(cs[lane]),
+                    to_f<T>(sn[lane]), static_cast<T>(sum_parts<T>(v + lane, pss)),
+                    static_cast<T>(sum_parts<T>(v + lane + 64, pss))};
+}
+
 // New K row: normalised and rotated exactly as the standalone kernel does
 // (lane l owns the pair (l, l + 64), one wave-wide sum of squares), written
 // with the V row into the cache slot.
@@ -286,9 +319,10 @@ __device__ __forceinline__ void write_new_kv(const NewKV<T>& in, float eps,
 // F8: the cache holds FP8 E4M3 rows (8-byte units; K widened exactly to T
 // for the MFMA, V to f32 for P.V, the scales folded into the softmax scale
 // and the final normalisation).
-template <typename T, int GP, int NT, int MAXW, bool FUSED, bool F8>
+template <typename T, int GP, int NT, int MAXW, bool FUSED, bool F8, bool PARTS>
 __global__ void __launch_bounds__(64 * MAXW)
 paged_decode_d128(DecodeArgs<T> a) {
+    static_assert(FUSED || !PARTS, "partial sums feed the fused prologue only");
     constexpr int D = 128;
     constexpr int ROW16 = D / 8;  // 8-element units per cache row of one head
     using Unit = std::conditional_t<F8, uint2, U16x8>;  // 8 cached elements
@@ -359,17 +393,49 @@ paged_decode_d128(DecodeArgs<T> a) {
         // of its own at short contexts.
         const int64_t new_slot = FUSED ? a.slots[row] : -1;
         NewKV<T> new_kv{};
-        if constexpr (FUSED)
+        if constexpr (PARTS) {
+            const float* prow = a.parts + row * a.pts;
+            new_kv = load_new_kv_parts<T>(prow + (a.heads + kvh) * D,
+                                          prow + (a.heads + a.kv_heads + kvh) * D, a.pss, a.kw,
+                                          a.cos_t + row * 64, a.sin_t + row * 64, lane);
+        } else if constexpr (FUSED) {
             new_kv = load_new_kv<T>(a.kraw + row * a.krts + kvh * a.krhs,
                                     a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
                                     a.cos_t + row * 64, a.sin_t + row * 64, lane);
+        }
         // B operand: query head g = col (zero beyond the group), dims c*32 + quad*8.
         U16x8 qb[4];
         {
             const bool has = col < a.group;
-            const T* qrow = a.q + row * a.qts + (h0 + (has ? col : 0)) * a.qhs + quad * 8;
+            const int hq = h0 + (has ? col : 0);
+            if constexpr (PARTS) {
+                // Each 8-element piece: two 16-byte loads per slice, summed
+                // in slice order and rounded once.
+                const float* qp = a.parts + row * a.pts + hq * D + quad * 8;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) qb[c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
+                for (int c = 0; c < 4; ++c) {
+                    float4 lo[kQkvParts], hi[kQkvParts];
+#pragma unroll
+                    for (int s = 0; s < kQkvParts; ++s) {
+                        lo[s] = *reinterpret_cast<const float4*>(qp + s * a.pss + c * 32);
+                        hi[s] = *reinterpret_cast<const float4*>(qp + s * a.pss + c * 32 + 4);
+                    }
+                    float4 l = lo[0], h = hi[0];
+#pragma unroll
+                    for (int s = 1; s < kQkvParts; ++s) {
+                        l.x += lo[s].x; l.y += lo[s].y; l.z += lo[s].z; l.w += lo[s].w;
+                        h.x += hi[s].x; h.y += hi[s].y; h.z += hi[s].z; h.w += hi[s].w;
+                    }
+                    qb[c].w[0] = pack2<T>(l.x, l.y);
+                    qb[c].w[1] = pack2<T>(l.z, l.w);
+                    qb[c].w[2] = pack2<T>(h.x, h.y);
+                    qb[c].w[3] = pack2<T>(h.z, h.w);
+                }
+            } else {
+                const T* qrow = a.q + row * a.qts + hq * a.qhs + quad * 8;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) qb[c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
+            }
 #pragma unroll
             for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -1046,6 +1112,8 @@ struct FusedIn {
     const void* sin;
     float q_eps, k_eps;
     const int64_t* slots;
+    const float* parts;  // split-K qkv partials (then k, v are unused)
+    int64_t pss, pts;
 };
 
 int paged_decode_impl(
@@ -1152,6 +1220,7 @@ int paged_decode_impl(
         args.kraw = nullptr;
         args.vraw = nullptr;
         args.slots = nullptr;
+        args.parts = nullptr;
         if (fused) {
             args.kraw = static_cast<const T*>(fused->k);
             args.krts = fused->kts;
@@ -1168,6 +1237,9 @@ int paged_decode_impl(
             args.kcache = const_cast<void*>(k_cache);
             args.vcache = const_cast<void*>(v_cache);
             args.slots = fused->slots;
+            args.parts = fused->parts;
+            args.pss = fused->pss;
+            args.pts = fused->pts;
         }
 
         // Four tiles per iteration (64 tokens, twice the bytes in flight)
@@ -1175,13 +1247,13 @@ int paged_decode_impl(
         // elements; bf16 at the 8B bs64 shape measured 87.6 -> 92.5 us with
         // them, FP8 53.3 -> 49.5 us.
         const bool tiles4 = tuning().tiles ? tuning().tiles == 4 : f8;
-        auto launch = [&]<bool F, bool F8>() {
+        auto launch = [&]<bool F, bool F8, bool P>() {
 #define TVLLM_DEC(GP)                                                                \
     do {                                                                             \
         if (tiles4 && threads <= 256)                                                \
-            paged_decode_d128<T, GP, 4, 4, F, F8><<<int(grid), threads, 0, s>>>(args); \
+            paged_decode_d128<T, GP, 4, 4, F, F8, P><<<int(grid), threads, 0, s>>>(args); \
         else                                                                         \
-            paged_decode_d128<T, GP, 2, kMaxWaves, F, F8>                            \
+            paged_decode_d128<T, GP, 2, kMaxWaves, F, F8, P>                         \
                 <<<int(grid), threads, 0, s>>>(args);                                \
     } while (0)
             // Groups above 4 carry 64+ accumulator registers per lane. A bf16
@@ -1194,16 +1266,19 @@ int paged_decode_impl(
             else if (group <= 2) TVLLM_DEC(2);
             else if (group <= 4) TVLLM_DEC(4);
             else if (group <= 8)
-                paged_decode_d128<T, 8, F8 ? 4 : 1, kMaxWaves, F, F8>
+                paged_decode_d128<T, 8, F8 ? 4 : 1, kMaxWaves, F, F8, P>
                     <<<int(grid), threads, 0, s>>>(args);
             else
-                paged_decode_d128<T, 16, F8 ? 2 : 1, kMaxWaves, F, F8>
+                paged_decode_d128<T, 16, F8 ? 2 : 1, kMaxWaves, F, F8, P>
                     <<<int(grid), threads, 0, s>>>(args);
         };
-        if (fused && f8) launch.template operator()<true, true>();
-        else if (fused) launch.template operator()<true, false>();
-        else if (f8) launch.template operator()<false, true>();
-        else launch.template operator()<false, false>();
+        const bool parts = fused && fused->parts;
+        if (parts && f8) launch.template operator()<true, true, true>();
+        else if (parts) launch.template operator()<true, false, true>();
+        else if (fused && f8) launch.template operator()<true, true, false>();
+        else if (fused) launch.template operator()<true, false, false>();
+        else if (f8) launch.template operator()<false, true, false>();
+        else launch.template operator()<false, false, false>();
 #undef TVLLM_DEC
         const int st = launch_status("paged_decode");
         if (st != TVLLM_OK || plan.grid <= 1) return st;
@@ -1329,7 +1404,7 @@ extern "C" int tvllm_paged_decode_qk_norm_rope(
     TVLLM_CHECK(aligned16(q_weight) && aligned16(cos) && aligned16(sin),
                 "paged_decode_qk_norm_rope: weights and RoPE tables must be 16-byte aligned");
     const FusedIn f{k, k_token_stride, k_head_stride, v, v_token_stride, v_head_stride,
-                    q_weight, k_weight, cos, sin, q_eps, k_eps, slots};
+                    q_weight, k_weight, cos, sin, q_eps, k_eps, slots, nullptr, 0, 0};
     return paged_decode_impl(q, q_token_stride, q_head_stride, k_cache, v_cache, out,
                              out_token_stride, out_head_stride, rows, blocks, offsets,
                              lengths, num_rows, num_heads, num_kv_heads, head_dim,
@@ -1337,4 +1412,36 @@ extern "C" int tvllm_paged_decode_qk_norm_rope(
                              max_context_len, scale, workspace,
                              workspace_bytes, dtype, cache_dtype, k_scale, v_scale, stream,
                              &f);
+}
+
+extern "C" int tvllm_paged_decode_qk_norm_rope_partials(
+    const float* parts, int64_t slice_stride, int64_t row_stride, const void* q_weight,
+    const void* k_weight, const void* cos, const void* sin, float q_eps, float k_eps,
+    const int64_t* slots, void* k_cache, void* v_cache, void* out, int64_t out_token_stride,
+    int64_t out_head_stride, const int64_t* rows, const int64_t* blocks,
+    const int64_t* offsets, const int64_t* lengths, int64_t num_rows, int64_t num_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t num_slots, int64_t cache_slot_stride,
+    int64_t cache_head_stride, int64_t block_size, int64_t max_context_len, float scale,
+    void* workspace, int64_t workspace_bytes, int dtype, int cache_dtype, float k_scale,
+    float v_scale, tvllm_stream_t stream) {
+    TVLLM_CHECK(head_dim == 128,
+                "paged_decode_qk_norm_rope_partials: head_dim must be 128");
+    TVLLM_CHECK(num_heads > 0 && num_kv_heads > 0 &&
+                    row_stride >= (num_heads + 2 * num_kv_heads) * head_dim,
+                "paged_decode_qk_norm_rope_partials: a row holds q, k and v heads");
+    TVLLM_CHECK(slice_stride >= 0 && row_stride % 4 == 0 && slice_stride % 4 == 0,
+                "paged_decode_qk_norm_rope_partials: strides must be whole float4 units");
+    TVLLM_CHECK(num_rows == 0 || (parts && q_weight && k_weight && cos && sin && slots),
+                "paged_decode_qk_norm_rope_partials: null pointer");
+    TVLLM_CHECK(aligned16(parts) && aligned16(q_weight) && aligned16(cos) && aligned16(sin),
+                "paged_decode_qk_norm_rope_partials: partials, weights and RoPE tables must "
+                "be 16-byte aligned");
+    const FusedIn f{nullptr, 0, 0, nullptr, 0, 0, q_weight, k_weight, cos, sin,
+                    q_eps, k_eps, slots, parts, slice_stride, row_stride};
+    // The query pointer only passes the host checks (the kernel reads parts).
+    return paged_decode_impl(parts, 0, 0, k_cache, v_cache, out, out_token_stride,
+                             out_head_stride, rows, blocks, offsets, lengths, num_rows,
+                             num_heads, num_kv_heads, head_dim, num_slots, cache_slot_stride,
+                             cache_head_stride, block_size, max_context_len, scale, workspace,
+                             workspace_bytes, dtype, cache_dtype, k_scale, v_scale, stream, &f);
 }

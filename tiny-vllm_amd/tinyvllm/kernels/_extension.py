@@ -49,6 +49,10 @@ _SIGNATURES: dict[str, tuple[type, list[type]]] = {
                                                _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                                _I64, _F32, _P, _I64, _INT, _INT, _F32, _F32,
                                                _P]),
+    "tvllm_paged_decode_qk_norm_rope_partials": (
+        _INT, [_P, _I64, _I64, _P, _P, _P, _P, _F32, _F32, _P, _P, _P, _P, _I64, _I64, _P,
+               _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P,
+               _I64, _INT, _INT, _F32, _F32, _P]),
     "tvllm_rms_norm": (_INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64,
                               _P, _P, _F32, _INT, _P]),
     "tvllm_silu_and_mul": (_INT, [_P, _I64, _I64, _I64, _I64, _I64, _P, _INT, _P]),

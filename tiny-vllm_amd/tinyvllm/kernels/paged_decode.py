@@ -172,3 +172,86 @@ def paged_decode_qk_norm_rope(
         workspace.data_ptr() if need else None, need, dtype_code(q.dtype),
         *cache_format(cache), stream_of(device),
     ))
+
+
+QKV_PARTS = 4  # slices of the split-K qkv projection the fused kernel sums
+
+
+def paged_decode_qk_norm_rope_partials(
+    parts: torch.Tensor,
+    num_heads: int,
+    query_weight: torch.Tensor,
+    key_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    query_eps: float,
+    key_eps: float,
+    cache: PagedKVCache,
+    layer_idx: int,
+    metadata: SingleQueryMetadata,
+    slots: torch.Tensor,
+    output: torch.Tensor,
+    *,
+    scale: float,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """``paged_decode_qk_norm_rope`` fed by the qkv projection's split-K
+    partials (no reference counterpart): ``parts`` is the fp32 [4, tokens,
+    (heads + 2 * kv_heads) * 128] result of a batched GEMM over four slices
+    of the reduction, and each raw Q/K/V element is the in-order fp32 sum of
+    its slices rounded once to the model dtype, summed inside the kernel's
+    prologue (no launch of its own)."""
+    lib = load_kernels()
+    kc, vc = cache.key[layer_idx], cache.value[layer_idx]
+    m = metadata
+    device = require_gpu(parts, query_weight, key_weight, cos, sin, slots, kc, output,
+                         m.query_rows, m.block_table_ids, m.block_table_offsets,
+                         m.context_lens)
+    width = (num_heads + 2 * cache.num_kv_heads) * 128
+    if (parts.dtype != torch.float32 or parts.dim() != 3 or parts.shape[0] != QKV_PARTS
+            or parts.shape[2] != width or parts.stride(2) != 1):
+        raise RuntimeError(f"parts must be float32 [{QKV_PARTS}, tokens, {width}] with unit "
+                           "last stride")
+    dtype = query_weight.dtype
+    if dtype not in (torch.float16, torch.bfloat16) or any(
+            t.dtype != dtype for t in (key_weight, cos, sin, output)) \
+            or (kc.dtype != dtype and not cache.fp8):
+        raise RuntimeError("weights, RoPE tables, output and cache must share a half dtype")
+    if vc.stride() != kc.stride():
+        raise RuntimeError("K/V caches must share one layout")
+    tokens = parts.shape[1]
+    if output.shape != (tokens, num_heads, 128) or output.stride(-1) != 1:
+        raise RuntimeError("output must be [tokens, heads, 128] with unit last stride")
+    if (query_weight.shape != (128,) or key_weight.shape != (128,)
+            or not query_weight.is_contiguous() or not key_weight.is_contiguous()):
+        raise RuntimeError("norm weights must be contiguous [128]")
+    for table in (cos, sin):
+        if table.numel() != tokens * 64 or not table.is_contiguous():
+            raise RuntimeError("RoPE tables must be contiguous [tokens, 1, 64]")
+    if (slots.dtype != torch.long or slots.dim() != 1 or not slots.is_contiguous()
+            or slots.numel() != tokens):
+        raise RuntimeError("slots must be contiguous int64 [tokens]")
+    for tensor in (m.query_rows, m.block_table_ids, m.block_table_offsets, m.context_lens):
+        if tensor.dtype != torch.long or tensor.dim() != 1 or not tensor.is_contiguous():
+            raise RuntimeError("metadata must be contiguous GPU int64 vectors")
+    num_rows = m.query_rows.numel()
+    if m.context_lens.numel() != num_rows or m.block_table_offsets.numel() != num_rows + 1:
+        raise RuntimeError("metadata lengths must align")
+    if num_rows == 0:
+        return
+    max_len = m.max_context_len or cache.num_slots
+    need = int(lib.tvllm_paged_decode_workspace_size(
+        num_rows, num_heads, cache.num_kv_heads, 128, max_len, cache.block_size))
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    check(lib.tvllm_paged_decode_qk_norm_rope_partials(
+        parts.data_ptr(), parts.stride(0), parts.stride(1), query_weight.data_ptr(),
+        key_weight.data_ptr(), cos.data_ptr(), sin.data_ptr(), float(query_eps),
+        float(key_eps), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), output.data_ptr(),
+        output.stride(0), output.stride(1), m.query_rows.data_ptr(),
+        m.block_table_ids.data_ptr(), m.block_table_offsets.data_ptr(),
+        m.context_lens.data_ptr(), num_rows, num_heads, cache.num_kv_heads, 128,
+        cache.num_slots, kc.stride(0), kc.stride(1), cache.block_size, max_len, float(scale),
+        workspace.data_ptr() if need else None, need, dtype_code(dtype),
+        *cache_format(cache), stream_of(device),
+    ))

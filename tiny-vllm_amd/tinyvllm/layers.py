@@ -59,6 +59,32 @@ class PackedLinear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return F.linear(x, self.weight)
 
+    def decode_partials(self, x: torch.Tensor, splits: int = 4) -> torch.Tensor | None:
+        """fp32 [splits, rows, out] partial products over ``splits`` slices of
+        the reduction axis (one batched torch.bmm), or None where one GEMM
+        is faster end to end. For a consumer that sums them itself (the fused
+        decode kernel sums the qkv projection's four slices in its prologue,
+        which costs it a few more loads per lane). hipBLASLt's single GEMM
+        leaves most CUs idle at decode batch sizes; measured on MI355X in
+        graph replay (bf16 qkv, us, F.linear -> four slices): 1024 -> 4096
+        (0.6B) 64 rows 11.5 -> 7.3, 32 rows 11.1 -> 6.5, 16 rows 7.4 -> 6.7,
+        1 row 7.4 -> 5.5; 4096 -> 6144 (8B) 64 rows 17.8 -> 15.6, 16-32 rows
+        and 1 row no gain; 5120 -> 10240 (32B) 64 rows 35.6 -> 25.3, 1-32
+        rows slower. End to end, gains under ~3 us per layer were taken back
+        by the decode kernel's prologue (0.6B at 1 and 16 rows: TPOT 1.40 ->
+        1.41 and 1.55 -> 1.60 ms; 8B at 64 rows: no change), so only the
+        0.6B width at 32-64 rows (C3: 14.9k -> 15.4k tok/s) and widths of
+        5120 and more at 48-64 rows take the split."""
+        rows, k = x.shape if x.dim() == 2 else (0, 0)
+        if (not x.is_cuda or x.dim() != 2 or not x.is_contiguous() or rows > 64
+                or k % (8 * splits)):
+            return None
+        if not ((k <= 2048 and rows >= 32) or (k >= 5120 and rows >= 48)):
+            return None
+        xs = x.view(rows, splits, k // splits).transpose(0, 1)
+        ws = self.weight.view(self.weight.shape[0], splits, k // splits).permute(1, 2, 0)
+        return torch.bmm(xs, ws, out_dtype=torch.float32)
+
     def reset_parameters(self) -> None:
         if self.weight.device.type == "meta":
             return

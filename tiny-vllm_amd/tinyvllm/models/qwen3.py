@@ -151,11 +151,21 @@ class Qwen3Attention(nn.Module):
         tokens = hidden_states.shape[0]
         q_size = self.num_heads * self.head_dim
         kv_size = self.num_kv_heads * self.head_dim
+        cos, sin = position_embeddings
+        # Decode-only steps on a backend that takes the qkv projection as
+        # split-K partials: the fused decode kernel sums them itself.
+        from_partials = getattr(attention, "attend_qkv_partials", None)
+        if from_partials is not None and attention.takes_qkv_partials:
+            parts = self.qkv_proj.decode_partials(hidden_states)
+            if parts is not None:
+                out = from_partials(layer_idx, parts, self.num_heads, self.q_norm.weight,
+                                    self.k_norm.weight, cos, sin, self.q_norm.eps,
+                                    self.k_norm.eps, scale=self.scale)
+                return self.o_proj(out.reshape(tokens, q_size))
         qkv = self.qkv_proj(hidden_states)
         q = qkv[:, :q_size].view(tokens, self.num_heads, self.head_dim)
         k = qkv[:, q_size:q_size + kv_size].view(tokens, self.num_kv_heads, self.head_dim)
         v = qkv[:, q_size + kv_size:].view(tokens, self.num_kv_heads, self.head_dim)
-        cos, sin = position_embeddings
         prepare = getattr(attention, "prepare_qkv", None)
         if prepare is not None:
             q, k, v = prepare(layer_idx, q, k, v, self.q_norm.weight, self.k_norm.weight,

@@ -18,7 +18,11 @@ import torch
 import torch.nn.functional as F
 
 from tinyvllm.kernels.kv_store import store_kv
-from tinyvllm.kernels.paged_decode import paged_decode_attention, paged_decode_qk_norm_rope
+from tinyvllm.kernels.paged_decode import (
+    paged_decode_attention,
+    paged_decode_qk_norm_rope,
+    paged_decode_qk_norm_rope_partials,
+)
 from tinyvllm.kernels.paged_prefill import paged_prefill_attention
 from tinyvllm.kernels.pointwise import qk_norm_rope, qk_norm_rope_store
 from tinyvllm.paged_kv import PagedKVCache
@@ -37,6 +41,24 @@ class HipAttention:
         self.decode_workspace = decode_workspace
         self._written_layer = -1
         self._fused = None
+
+    @property
+    def takes_qkv_partials(self) -> bool:
+        """Decode-only steps: the fused decode kernel can take the qkv
+        projection as split-K partials (``attend_qkv_partials``)."""
+        return self.kv.prefill is None and self.kv.decode is not None
+
+    def attend_qkv_partials(self, layer_idx, parts, num_heads, q_weight, k_weight, cos, sin,
+                            q_eps, k_eps, *, scale):
+        """QK-norm + RoPE + KV write + paged decode of a decode-only step from
+        the qkv projection's fp32 split-K partials [4, tokens, width]."""
+        output = torch.empty((parts.shape[1], num_heads, 128), dtype=q_weight.dtype,
+                             device=parts.device)
+        paged_decode_qk_norm_rope_partials(parts, num_heads, q_weight, k_weight, cos, sin,
+                                           q_eps, k_eps, self.cache, layer_idx,
+                                           self.kv.decode, self.kv.slot_mapping, output,
+                                           scale=scale, workspace=self.decode_workspace)
+        return output
 
     def prepare_qkv(self, layer_idx, q, k, v, q_weight, k_weight, cos, sin, q_eps, k_eps):
         """Decode-only steps: keep the raw Q/K/V for the fused decode kernel
