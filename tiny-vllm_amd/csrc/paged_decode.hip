@@ -405,13 +405,21 @@ paged_decode_d128(DecodeArgs<T> a) {
         }
         // B operand: query head g = col (zero beyond the group), dims c*32 + quad*8.
         U16x8 qb[4];
-        {
+        // The query's B operand (the partial sums, PARTS, are loaded after
+        // the block ids so that the sums' wait does not hold those back).
+        auto load_q = [&]() {
             const bool has = col < a.group;
             const int hq = h0 + (has ? col : 0);
             if constexpr (PARTS) {
                 // Each 8-element piece: two 16-byte loads per slice, summed
-                // in slice order and rounded once.
+                // in slice order and rounded once. Only the lanes of real
+                // query heads load (exec-masked): 512 bytes per lane (4
+                // slices x 8 pieces of 16 bytes) would otherwise go out from
+                // every column.
                 const float* qp = a.parts + row * a.pts + hq * D + quad * 8;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) qb[c] = U16x8{};
+                if (has)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     float4 lo[kQkvParts], hi[kQkvParts];
@@ -440,7 +448,8 @@ paged_decode_d128(DecodeArgs<T> a) {
             for (int c = 0; c < 4; ++c)
 #pragma unroll
                 for (int w = 0; w < 4; ++w) qb[c].w[w] = has ? qb[c].w[w] : 0u;
-        }
+        };
+        if constexpr (!PARTS) load_q();
         // The wave's range is walked in groups of 64 * IDR pages. Lane p
         // holds the block ids of pages p, p + 64, ... of the group in
         // registers (fetched once per group; only the low word: ids < 2^32,
@@ -590,6 +599,7 @@ paged_decode_d128(DecodeArgs<T> a) {
         // last chunk of a group loads clamped (cached) rows instead of
         // branching, so the loop's wait counts never cover a skipped path.
         load_group();
+        if constexpr (PARTS) load_q();
         if constexpr (FUSED) {
             // Keep the new row's loads here, in flight with the query and the
             // block ids (the compiler would sink them into the writer's branch).
