@@ -224,3 +224,44 @@ def test_prefill_graphs_match_eager_prefill(device, monkeypatch):
     for lg, te, tg in zip(results[True][0], results[True][1], results[False][1]):
         for row, (x, y) in enumerate(zip(te, tg)):
             assert x == y or abs(lg[row, x] - lg[row, y]).item() < 0.15, (row, x, y)
+
+
+@pytest.mark.parametrize("kv_dtype", [None, torch.float8_e4m3fn])
+def test_cache_layouts_give_bit_identical_runs(device, kv_dtype):
+    """The kernels address K/V through the cache's slot and head strides and
+    do the same arithmetic in either storage order, so a whole run (chunked
+    prefill through the prefill graphs, then graph-replayed decode steps)
+    gives bit-identical logits and tokens on a token-major and a head-major
+    cache."""
+    from tinyvllm.executor import Executor
+
+    weights = OM.random_weights(CFG, seed=9, dtype=torch.bfloat16, std=0.2)
+    model = _our_model(weights, device)
+    g = torch.Generator().manual_seed(10)
+    prompts = [torch.randint(0, CFG.vocab_size, (n,), generator=g).tolist()
+               for n in (37, 5, 80, 130)]
+    steps = ([(0, 37, True), (1, 5, True)], [(2, 80, True), (3, 64, False)],
+             [(3, 66, True)]) + tuple([(s, 1, True) for s in range(4)] for _ in range(6))
+    runs = {}
+    for layout in ("token_major", "head_major"):
+        executor = Executor(model, block_size=16, num_blocks=64, max_model_len=512,
+                            max_num_seqs=4, kv_cache_dtype=kv_dtype,
+                            kv_scales=(0.5, 0.5) if kv_dtype else (1.0, 1.0),
+                            kv_cache_layout=layout)
+        assert executor.runner.kv_cache.layout == layout
+        mb = ManualBatches(prompts, block_size=16, num_blocks=64)
+        logits, tokens = [], []
+        for items in steps:
+            batch = mb.step(items)
+            out = executor.runner.run_and_sample(batch, [0] * batch.num_samples)
+            if out is None:
+                mb.commit(items, [])
+                continue
+            logits.append(out[0].cpu())
+            tokens.append(out[1].cpu().tolist())
+            mb.commit(items, tokens[-1])
+        runs[layout] = (logits, tokens)
+        executor.clear()
+    assert runs["token_major"][1] == runs["head_major"][1]
+    for a, b in zip(runs["token_major"][0], runs["head_major"][0]):
+        assert torch.equal(a, b)
