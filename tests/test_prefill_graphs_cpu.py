@@ -52,3 +52,24 @@ def test_item_and_table_limits():
     # block tables beyond the packed capacity
     assert _inputs(max_items=1, pitch_pages=2).buckets_for(_batch(p, [(0, 40, True)])) is None
     assert _inputs(max_items=1, pitch_pages=3).buckets_for(_batch(p, [(0, 40, True)])) == (64, 1)
+
+
+def test_graph_token_ceiling_follows_the_model_size():
+    """Prefill graphs cover steps whose dense GEMMs the host launches would
+    otherwise outrun: up to 2048 tokens at 0.6B, 512 at 8B, 128 at 32B."""
+    import torch
+
+    from tinyvllm.models.qwen3 import Qwen3Config, Qwen3ForCausalLM
+    from tinyvllm.runtime.runner import default_prefill_graph_tokens
+
+    shapes = {  # hidden, intermediate, layers, q heads, kv heads
+        2048: (1024, 3072, 28, 16, 8), 512: (4096, 12288, 36, 32, 8),
+        128: (5120, 25600, 64, 64, 8)}
+    for expected, (hidden, inter, layers, hq, hkv) in shapes.items():
+        cfg = Qwen3Config.from_dict(dict(
+            model_type="qwen3", vocab_size=151936, hidden_size=hidden,
+            intermediate_size=inter, num_hidden_layers=layers, num_attention_heads=hq,
+            num_key_value_heads=hkv, head_dim=128, max_position_embeddings=40960,
+            rope_theta=1e6, tie_word_embeddings=False))
+        model = Qwen3ForCausalLM(cfg, device="meta", dtype=torch.bfloat16)
+        assert default_prefill_graph_tokens(model) == expected

@@ -83,7 +83,8 @@ class Executor:
                  graph_sizes: tuple[int, ...] | None = None,
                  kv_cache_dtype: torch.dtype | None = None,
                  kv_scales: tuple[float, float] = (1.0, 1.0),
-                 kv_cache_layout: str = "auto", prefill_graph_tokens: int = 2048) -> None:
+                 kv_cache_layout: str = "auto",
+                 prefill_graph_tokens: int | None = None) -> None:
         self.runner = ModelRunner(model, block_size=block_size, num_blocks=num_blocks,
                                   max_model_len=max_model_len, max_num_seqs=max_num_seqs,
                                   attention_backend=attention_backend,

@@ -22,7 +22,12 @@ from tinyvllm.runtime.contracts import (
 )
 from tinyvllm.runtime.graphs import DecodeGraphs
 from tinyvllm.runtime.inputs import DecodeInputs
-from tinyvllm.runtime.prefill_graphs import ITEM_BUCKETS, PrefillGraphs, PrefillInputs
+from tinyvllm.runtime.prefill_graphs import (
+    ITEM_BUCKETS,
+    TOKEN_BUCKETS,
+    PrefillGraphs,
+    PrefillInputs,
+)
 
 
 class ModelRunner:
@@ -41,7 +46,7 @@ class ModelRunner:
         graph_sizes: tuple[int, ...] | None = None,
         kv_cache_dtype: torch.dtype | None = None,
         kv_scales: tuple[float, float] = (1.0, 1.0),
-        prefill_graph_tokens: int = 2048,
+        prefill_graph_tokens: int | None = None,
         kv_cache_layout: str = "auto",
     ) -> None:
         """``kv_cache_dtype``: None keeps K/V in the model dtype;
@@ -55,8 +60,11 @@ class ModelRunner:
         token-major.
         ``prefill_graph_tokens``: prefill and mixed steps of up to this many
         tokens (and up to 16 items; single-token items of short context only)
-        replay captured graphs (0: always eager; beyond the reference, which
-        runs these steps eagerly)."""
+        replay captured graphs (0: always eager; None: sized from the model,
+        ``default_prefill_graph_tokens``; beyond the reference, which runs
+        these steps eagerly)."""
+        if prefill_graph_tokens is None:
+            prefill_graph_tokens = default_prefill_graph_tokens(model)
         if type(prefill_graph_tokens) is not int or prefill_graph_tokens < 0:
             raise ValueError("prefill_graph_tokens must be a non-negative int")
         if type(enforce_eager) is not bool:
@@ -372,6 +380,23 @@ class ModelRunner:
             self.decode_workspace = None
             self.kv_cache = None
             self.model = None
+
+
+# GEMM work of an eager prefill step whose launches the host can no longer
+# outrun (~6 ms of dense-layer GEMMs on MI355X, about the host's launch time
+# for a 28-64-layer eager step): bigger steps gain nothing from a graph.
+_GRAPH_STEP_FLOP = 8e12
+
+
+def default_prefill_graph_tokens(model: nn.Module) -> int:
+    """The largest prefill-graph token bucket whose dense-layer GEMMs (2 flop
+    per weight per token) stay within ``_GRAPH_STEP_FLOP``, at least the
+    smallest bucket: 2048 for Qwen3-0.6B, 512 for 8B, 128 for 32B."""
+    layers = getattr(getattr(model, "model", None), "layers", None)
+    weights = sum(p.numel() for p in (layers.parameters() if layers is not None
+                                      else model.parameters()))
+    fitting = [b for b in TOKEN_BUCKETS if 2 * weights * b <= _GRAPH_STEP_FLOP]
+    return max(fitting) if fitting else min(TOKEN_BUCKETS)
 
 
 def sample_rows(logits: torch.Tensor, params, counters) -> torch.Tensor:
