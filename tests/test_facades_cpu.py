@@ -200,6 +200,9 @@ def test_engine_config_validation(tmp_path):
     assert cfg.kv_cache_dtype == "auto" and (cfg.kv_k_scale, cfg.kv_v_scale) == (1.0, 1.0)
     fp8 = EngineConfig(model=tmp_path, kv_cache_dtype="fp8_e4m3", kv_k_scale=0.5)
     assert fp8.kv_cache_dtype == "fp8_e4m3" and fp8.kv_k_scale == 0.5
+    assert cfg.kv_cache_layout == "auto" and cfg.prefill_graph_tokens is None
+    tuned = EngineConfig(model=tmp_path, kv_cache_layout="head_major", prefill_graph_tokens=0)
+    assert tuned.kv_cache_layout == "head_major" and tuned.prefill_graph_tokens == 0
     bad = [dict(model=tmp_path / "missing"), dict(model=tmp_path, dtype="float32"),
            dict(model=tmp_path, attention_backend="triton"),
            dict(model=tmp_path, gpu_memory_utilization=1.0),
@@ -209,7 +212,10 @@ def test_engine_config_validation(tmp_path):
            dict(model=tmp_path, kv_cache_dtype="int8"),
            dict(model=tmp_path, kv_k_scale=2.0),  # scales need the FP8 layout
            dict(model=tmp_path, kv_cache_dtype="fp8_e4m3", kv_v_scale=0.0),
-           dict(model=tmp_path, kv_cache_dtype="fp8_e4m3", kv_k_scale=float("inf"))]
+           dict(model=tmp_path, kv_cache_dtype="fp8_e4m3", kv_k_scale=float("inf")),
+           dict(model=tmp_path, kv_cache_layout="slot_major"),
+           dict(model=tmp_path, prefill_graph_tokens=-1),
+           dict(model=tmp_path, prefill_graph_tokens=512.0)]
     for kw in bad:
         with pytest.raises((ValueError, TypeError)):
             EngineConfig(**kw)

@@ -46,7 +46,8 @@ def build_engine(model, *, max_model_len: int, max_num_seqs: int = 64,
                  enable_prefix_caching: bool = True, eos_token_ids=None,
                  graph_sizes=None, clock=None, kv_cache_dtype: torch.dtype | None = None,
                  kv_scales: tuple[float, float] = (1.0, 1.0),
-                 pipelined: bool | None = None) -> "Engine":
+                 pipelined: bool | None = None, kv_cache_layout: str = "auto",
+                 prefill_graph_tokens: int | None = None) -> "Engine":
     """Engine around an already built model (random-init benchmarks, tests).
     ``pipelined=False`` runs one step at a time (the reference's loop)."""
     from tinyvllm.engine import Engine
@@ -57,7 +58,8 @@ def build_engine(model, *, max_model_len: int, max_num_seqs: int = 64,
                         max_model_len=max_model_len, max_num_seqs=max_num_seqs,
                         attention_backend=attention_backend, enforce_eager=enforce_eager,
                         graph_sizes=graph_sizes, kv_cache_dtype=kv_cache_dtype,
-                        kv_scales=kv_scales)
+                        kv_scales=kv_scales, kv_cache_layout=kv_cache_layout,
+                        prefill_graph_tokens=prefill_graph_tokens)
     scheduler = Scheduler(
         max_active_requests=max_num_seqs, max_step_requests=max_num_seqs,
         max_scheduled_tokens=max_num_batched_tokens, prefill_chunk_size=prefill_chunk_size,
@@ -111,7 +113,9 @@ def create_engine(config: EngineConfig) -> "Engine":
         attention_backend=config.attention_backend, enforce_eager=config.enforce_eager,
         enable_prefix_caching=config.enable_prefix_caching,
         eos_token_ids=model_config.eos_token_id, kv_cache_dtype=kv_dtype,
-        kv_scales=(config.kv_k_scale, config.kv_v_scale))
+        kv_scales=(config.kv_k_scale, config.kv_v_scale),
+        kv_cache_layout=config.kv_cache_layout,
+        prefill_graph_tokens=config.prefill_graph_tokens)
     logger.info("engine ready in %.1fs: %d KV blocks of %d tokens",
                 time.perf_counter() - started, blocks, config.kv_block_size)
     return engine

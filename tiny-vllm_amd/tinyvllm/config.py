@@ -11,6 +11,7 @@ from tinyvllm._validation import _check_non_negative_int, _check_positive_int
 DType = Literal["bfloat16", "float16"]
 BACKENDS = ("hip", "reference", "cuda")
 KV_CACHE_DTYPES = ("auto", "fp8_e4m3")
+KV_CACHE_LAYOUTS = ("auto", "token_major", "head_major")
 
 
 @dataclass(frozen=True, slots=True)
@@ -20,7 +21,12 @@ class EngineConfig:
     "cuda", the reference's name for its native backend, maps to "hip".
     Beyond the reference: ``kv_cache_dtype`` "auto" stores K/V in the model
     dtype, "fp8_e4m3" in OCP FP8 E4M3 (one byte per element) with the scales
-    ``kv_k_scale``/``kv_v_scale`` (stored = x / scale, saturated to +-448)."""
+    ``kv_k_scale``/``kv_v_scale`` (stored = x / scale, saturated to +-448);
+    ``kv_cache_layout`` the storage order behind the reference's [slots,
+    heads, dim] cache view ("auto": head-major for fewer than 256 (request,
+    KV head) pairs, token-major otherwise); ``prefill_graph_tokens`` the
+    largest prefill/mixed step replayed from a captured graph (None: sized
+    from the model, 0: prefill always eager)."""
 
     model: Path
     dtype: DType = "bfloat16"
@@ -39,6 +45,8 @@ class EngineConfig:
     kv_cache_dtype: str = "auto"
     kv_k_scale: float = 1.0
     kv_v_scale: float = 1.0
+    kv_cache_layout: str = "auto"
+    prefill_graph_tokens: int | None = None
 
     def __post_init__(self) -> None:
         model = Path(self.model).expanduser().resolve()
@@ -58,6 +66,11 @@ class EngineConfig:
         if self.kv_cache_dtype == "auto" and (self.kv_k_scale != 1.0
                                               or self.kv_v_scale != 1.0):
             raise ValueError("KV scales apply to kv_cache_dtype fp8_e4m3 only")
+        if self.kv_cache_layout not in KV_CACHE_LAYOUTS:
+            raise ValueError(f"unsupported kv_cache_layout: {self.kv_cache_layout}")
+        graph_tokens = self.prefill_graph_tokens
+        if graph_tokens is not None and (type(graph_tokens) is not int or graph_tokens < 0):
+            raise ValueError("prefill_graph_tokens must be None or a non-negative int")
         for name in ("enforce_eager", "enable_prefix_caching"):
             if type(getattr(self, name)) is not bool:
                 raise TypeError(f"{name} must be bool")
