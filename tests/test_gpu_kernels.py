@@ -808,13 +808,15 @@ def test_decode_split_merge_reuses_its_workspace(device):
         assert torch.equal(graph_out.cpu(), outs[0])
 
 
-@pytest.mark.parametrize("layout", ["head_major", "token_major"])
+@pytest.mark.parametrize("layout,fp8", [("head_major", False), ("token_major", False),
+                                       ("token_major", True)])
 @pytest.mark.parametrize("heads,kv_heads,lengths,max_ctx", [
     (32, 8, [2049, 1, 700, 0, 16, 17], 4096),   # group 4, a padding row
     (16, 8, [300, 77, 1], 1024),                 # group 2
     (64, 8, [5000, 33], 32768),                  # group 8, workgroup-level splits
 ])
-def test_decode_fused_from_qkv_partials(device, heads, kv_heads, lengths, max_ctx, layout):
+def test_decode_fused_from_qkv_partials(device, heads, kv_heads, lengths, max_ctx, layout,
+                                        fp8):
     """The fused decode kernel fed the qkv projection as four fp32 split-K
     partials equals the same kernel fed their in-order sum rounded to bf16:
     the cache bits written and the attention output are identical."""
@@ -852,16 +854,21 @@ def test_decode_fused_from_qkv_partials(device, heads, kv_heads, lengths, max_ct
     q = gs[:, :heads * d].view(rows, heads, d)
     k = gs[:, heads * d:(heads + kv_heads) * d].view(rows, kv_heads, d)
     v = gs[:, (heads + kv_heads) * d:].view(rows, kv_heads, d)
-    cache_a = _Cache(G(kc), G(vc), bs, layout=layout)
+    if fp8:  # an FP8 E4M3 cache (scales 0.5 / 2): the same quantised writes
+        kc, vc = (OK.fp8_quantize(t.float(), sc).view(torch.float8_e4m3fn)
+                  for t, sc in ((kc, 0.5), (vc, 2.0)))
+    scales = (0.5, 2.0) if fp8 else (1.0, 1.0)
+    cache_a = _Cache(G(kc), G(vc), bs, *scales, layout=layout)
     out_a = torch.zeros(rows, heads, d, dtype=torch.bfloat16, device=device)
     paged_decode_qk_norm_rope(q, k, v, *args, cache_a, 0, meta, gslots, out_a, scale=d ** -0.5)
-    cache_b = _Cache(G(kc), G(vc), bs, layout=layout)
+    cache_b = _Cache(G(kc), G(vc), bs, *scales, layout=layout)
     out_b = torch.full((rows, heads, d), 5.0, dtype=torch.bfloat16, device=device)
     paged_decode_qk_norm_rope_partials(G(parts), heads, *args, cache_b, 0, meta, gslots, out_b,
                                        scale=d ** -0.5)
     torch.cuda.synchronize()
-    assert torch.equal(cache_a.key[0].cpu(), cache_b.key[0].cpu())
-    assert torch.equal(cache_a.value[0].cpu(), cache_b.value[0].cpu())
+    bits = torch.uint8 if fp8 else torch.int16
+    assert torch.equal(cache_a.key[0].cpu().view(bits), cache_b.key[0].cpu().view(bits))
+    assert torch.equal(cache_a.value[0].cpu().view(bits), cache_b.value[0].cpu().view(bits))
     assert torch.equal(out_a.cpu(), out_b.cpu())
 
 
