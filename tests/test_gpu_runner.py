@@ -166,7 +166,8 @@ def test_token_sources_are_validated(device):
         executor.execute(dataclasses.replace(batch, input_token_sources=(-1,)))
 
 
-def test_prefill_graphs_match_eager_prefill(device, monkeypatch):
+@pytest.mark.parametrize("kv_dtype", [None, torch.float8_e4m3fn])
+def test_prefill_graphs_match_eager_prefill(device, monkeypatch, kv_dtype):
     """Prefill and mixed steps replayed from the captured bucket graphs
     (padded tokens write no KV, padded items are empty, single-token items
     go through the prefill kernel) give the eager path's logits within bf16
@@ -197,7 +198,8 @@ def test_prefill_graphs_match_eager_prefill(device, monkeypatch):
     forced = None  # the graph run commits the eager run's tokens (teacher forcing)
     for eager in (True, False):
         executor = Executor(model, block_size=16, num_blocks=480, max_model_len=1024,
-                            max_num_seqs=12, enforce_eager=eager)
+                            max_num_seqs=12, enforce_eager=eager, kv_cache_dtype=kv_dtype,
+                            kv_scales=(0.5, 0.5) if kv_dtype else (1.0, 1.0))
         mb = ManualBatches(prompts, block_size=16, num_blocks=480)
         logits, tokens = [], []
         for step, items in enumerate(steps):
