@@ -57,6 +57,9 @@ def test_noalloc_decode_matches_workspace_entry_point(device):
         print(f"noalloc case seed={seed} rows={batch} heads={heads}/{kv_heads} "
               f"lengths={lengths}", flush=True)
         c = _case(seed, batch, heads, kv_heads, lengths, device)
+        if seed == 2:  # a head-major cache: each KV head's slots contiguous
+            for name in ("k_d", "v_d"):
+                c[name] = c[name].transpose(0, 1).contiguous().transpose(0, 1)
         need = lib.tvllm_paged_decode_workspace_size(
             batch, heads, kv_heads, 128, c["max_len"], 16)
         assert need > 0  # the case exercises the split-K partials
