@@ -155,7 +155,7 @@ int tvllm_paged_decode(const void* q, int64_t q_token_stride,
  * split-K partials go to a static 8 MiB device array per GPU (held until
  * the process ends); a geometry whose tvllm_paged_decode_workspace_size
  * exceeds 8 MiB is rejected with TVLLM_EINVAL (the default split plan needs
- * at most ~4.3 MB). Allocates nothing. Calls that
+ * at most ~6 MB). Allocates nothing. Calls that
  * overlap on one GPU (different streams) share that array and race; calls
  * ordered on one stream are safe. The first call on a device looks up the
  * array's address (hipGetSymbolAddress): make it outside graph capture. */

@@ -174,7 +174,11 @@ struct DecodeArgs {
 constexpr int kQkvParts = 4;
 
 constexpr int kMaxWaves = 8;  // 2 resident waves per SIMD at <= 256 VGPRs
-constexpr int64_t kMaxSplits = 64;
+// Page ranges per (row, KV head): a single row of 8 KV heads needs 128-256
+// to put a wave on every SIMD (1 row x 32k tokens, 8B heads: 58.4 us with
+// 64, 36.8 us with 256); the workgroup-level splits stay <= 64 (the merge
+// kernel holds one per lane) because a workgroup takes at least four ranges.
+constexpr int64_t kMaxSplits = 256;
 
 __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);  // v_exp_f32; inputs here are <= 0
@@ -1331,8 +1335,10 @@ extern "C" int tvllm_paged_decode(
 namespace tvllm {
 namespace {
 
-// The split planner asks for at most ~4.3 MB (fewer than 512 split (row, KV
-// head) units x group 16 x 520 bytes); 8 MiB leaves room for other plans.
+// The split planner asks for at most ~6 MB (520 bytes per (row, query head,
+// workgroup split); its largest plan, 63 rows x 64 query heads x 3
+// workgroup splits at group 16, is 12,096 of them); 8 MiB leaves room for
+// other plans.
 constexpr int64_t kScratchBytes = int64_t(8) << 20;
 constexpr int kMaxDevices = 64;
 
