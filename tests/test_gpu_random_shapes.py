@@ -1,0 +1,156 @@
+"""Paged decode and chunked prefill against the oracle over seeded random
+configurations: GQA groups 1-16, head dims 64/128/256, page sizes 1-32
+(powers of two and not), bf16 / fp16 queries, bf16 / fp16 / FP8 E4M3
+caches, both storage layouts, ragged lengths with empty rows, query rows
+picked out of a larger token axis and max_context_len hints above the
+longest row. Each configuration comes from its own seed and is printed in
+the test id; the bar is the one every attention test uses (max abs 2e-2,
+mean relative 1e-3), with empty rows exactly zero."""
+import math
+import random
+
+import pytest
+import torch
+
+from helpers import assert_bf16_close
+from oracle import attention as OA
+from test_gpu_fp8 import _fp8_cache
+from test_gpu_kernels import _Cache
+
+pytestmark = pytest.mark.gpu
+
+DECODE_CASES = 28
+PREFILL_CASES = 16
+
+
+def _decode_config(seed: int) -> dict:
+    r = random.Random(1000 + seed)
+    kv_heads = r.choice([1, 2, 4, 8])
+    group = r.choice([1, 2, 3, 4, 5, 8, 16])
+    head_dim = r.choice([128, 128, 128, 64, 256])
+    cache = r.choice(["same", "same", "fp8"]) if head_dim == 128 else "same"
+    block_size = r.choice([16, 16, 16, 1, 2, 5, 8, 32])
+    longest = r.choice([1, 17, 300, 2500, 6000])
+    batch = r.randint(1, 12 if longest <= 2500 else 5)
+    lengths = [r.randint(0, longest) for _ in range(batch)]
+    lengths[r.randrange(batch)] = longest
+    if batch > 2 and r.random() < 0.5:
+        lengths[r.randrange(batch)] = 0
+    return dict(kv_heads=kv_heads, heads=kv_heads * group, head_dim=head_dim, cache=cache,
+                block_size=block_size, lengths=lengths,
+                dtype=r.choice([torch.bfloat16, torch.float16]),
+                layout=r.choice(["head_major", "token_major"]),
+                hint=r.choice([None, longest, 2 * longest + 31]),
+                extra_rows=r.randint(0, 5), scales=r.choice([(1.0, 1.0), (0.5, 2.0)]))
+
+
+def _decode_id(seed: int) -> str:
+    c = _decode_config(seed)
+    return (f"s{seed}-h{c['heads']}kv{c['kv_heads']}-d{c['head_dim']}-bs{c['block_size']}-"
+            f"{str(c['dtype'])[6:]}-{c['cache']}-{c['layout']}-L{max(c['lengths'])}x"
+            f"{len(c['lengths'])}")
+
+
+def _tables(g, lengths, block_size):
+    pages = [math.ceil(n / block_size) for n in lengths]
+    pool = sum(pages) + 3
+    perm = torch.randperm(pool, generator=g)
+    blocks, offsets = [], [0]
+    for p in pages:
+        blocks += perm[offsets[-1]:offsets[-1] + p].tolist()
+        offsets.append(offsets[-1] + p)
+    return pool, torch.tensor(blocks, dtype=torch.long), torch.tensor(offsets, dtype=torch.long)
+
+
+@pytest.mark.parametrize("seed", range(DECODE_CASES), ids=_decode_id)
+def test_decode_random_configuration(device, seed):
+    from tinyvllm.kernels.paged_decode import paged_decode_attention
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    c = _decode_config(seed)
+    g = torch.Generator().manual_seed(seed)
+    bs, d, dt = c["block_size"], c["head_dim"], c["dtype"]
+    batch = len(c["lengths"])
+    pool, blocks, offsets = _tables(g, c["lengths"], bs)
+    k = torch.randn(pool * bs, c["kv_heads"], d, generator=g)
+    v = torch.randn(pool * bs, c["kv_heads"], d, generator=g)
+    tokens = batch + c["extra_rows"]
+    q = torch.randn(tokens, c["heads"], d, generator=g).to(dt)
+    rows = torch.randperm(tokens, generator=g)[:batch]
+    lengths = torch.tensor(c["lengths"], dtype=torch.long)
+    if c["cache"] == "fp8":
+        ks, vs = c["scales"]
+        cache, kd, vd = _fp8_cache(k * ks, v * vs, bs, device, ks, vs, c["layout"])
+    else:
+        kd, vd = k.to(dt), v.to(dt)
+        cache = _Cache(kd.to(device), vd.to(device), bs, layout=c["layout"])
+    meta = SingleQueryMetadata(rows.to(device), blocks.to(device), offsets.to(device),
+                               lengths.to(device), c["hint"])
+    scale = d ** -0.5
+    out = torch.full(q.shape, 7.0, dtype=dt, device=device)
+    paged_decode_attention(q.to(device), cache, 0, meta, out, scale=scale)
+    torch.cuda.synchronize()
+    expect = torch.full(q.shape, 7.0, dtype=dt)
+    OA.decode_attention(q, kd, vd, rows, blocks, offsets, lengths, bs, scale, expect)
+    out = out.cpu()
+    for i, n in enumerate(c["lengths"]):
+        if n == 0:
+            assert (out[rows[i]] == 0).all(), f"empty row {i} not zero"
+    untouched = torch.ones(tokens, dtype=torch.bool)
+    untouched[rows] = False
+    assert (out[untouched] == 7.0).all(), "rows outside query_rows were written"
+    assert_bf16_close(out, expect)
+
+
+def _prefill_config(seed: int) -> dict:
+    r = random.Random(2000 + seed)
+    kv_heads = r.choice([1, 2, 4, 8])
+    group = r.choice([1, 2, 4, 8])
+    items = []
+    for _ in range(r.randint(1, 6)):
+        q_len = r.choice([1, r.randint(2, 40), r.randint(41, 300), 512])
+        history = r.choice([0, 0, r.randint(1, 200), r.randint(200, 3000)])
+        items.append((history + q_len, q_len))
+    return dict(kv_heads=kv_heads, heads=kv_heads * group, items=items,
+                block_size=r.choice([16, 16, 1, 4, 5, 8, 12, 32]),
+                cache=r.choice(["bf16", "bf16", "fp16", "fp8"]),
+                layout=r.choice(["head_major", "token_major"]))
+
+
+def _prefill_id(seed: int) -> str:
+    c = _prefill_config(seed)
+    return (f"s{seed}-h{c['heads']}kv{c['kv_heads']}-bs{c['block_size']}-{c['cache']}-"
+            f"{c['layout']}-{len(c['items'])}items-q{sum(q for _, q in c['items'])}")
+
+
+@pytest.mark.parametrize("seed", range(PREFILL_CASES), ids=_prefill_id)
+def test_prefill_random_configuration(device, seed):
+    from tinyvllm.kernels.paged_prefill import paged_prefill_attention
+    from tinyvllm.runtime.contracts import MultiQueryMetadata
+
+    c = _prefill_config(seed)
+    g = torch.Generator().manual_seed(seed)
+    bs, d = c["block_size"], 128
+    contexts = [ctx for ctx, _ in c["items"]]
+    pool, blocks, boffsets = _tables(g, contexts, bs)
+    k = torch.randn(pool * bs, c["kv_heads"], d, generator=g)
+    v = torch.randn(pool * bs, c["kv_heads"], d, generator=g)
+    dt = torch.float16 if c["cache"] == "fp16" else torch.bfloat16
+    q_offsets = torch.tensor([0] + [sum(q for _, q in c["items"][:i + 1])
+                                    for i in range(len(c["items"]))], dtype=torch.long)
+    q = torch.randn(int(q_offsets[-1]), c["heads"], d, generator=g).to(dt)
+    if c["cache"] == "fp8":
+        cache, kd, vd = _fp8_cache(k * 0.5, v, bs, device, 0.5, 1.0, c["layout"])
+    else:
+        kd, vd = k.to(dt), v.to(dt)
+        cache = _Cache(kd.to(device), vd.to(device), bs, layout=c["layout"])
+    context = torch.tensor(contexts, dtype=torch.long)
+    meta = MultiQueryMetadata(q_offsets.to(device), blocks.to(device), boffsets.to(device),
+                              context.to(device), max_query_len=max(q for _, q in c["items"]))
+    out = torch.zeros(q.shape, dtype=dt, device=device)
+    paged_prefill_attention(q.to(device), cache, 0, meta, out, scale=d ** -0.5)
+    torch.cuda.synchronize()
+    expect = torch.zeros_like(q)
+    OA.prefill_attention(q, kd, vd, q_offsets, blocks, boffsets, context, bs, d ** -0.5,
+                         expect)
+    assert_bf16_close(out.cpu(), expect)
