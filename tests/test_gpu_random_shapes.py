@@ -3,7 +3,8 @@ configurations: GQA groups 1-16, head dims 64/128/256, page sizes 1-32
 (powers of two and not), bf16 / fp16 queries, bf16 / fp16 / FP8 E4M3
 caches, both storage layouts, ragged lengths with empty rows, query rows
 picked out of a larger token axis and max_context_len hints above the
-longest row. Each configuration comes from its own seed and is printed in
+longest row; and the fused decode step (QK-norm, RoPE, KV write and
+attention in one launch) over the same kind of draw. Each configuration comes from its own seed and is printed in
 the test id; the bar is the one every attention test uses (max abs 2e-2,
 mean relative 1e-3), with empty rows exactly zero."""
 import math
@@ -154,3 +155,99 @@ def test_prefill_random_configuration(device, seed):
     OA.prefill_attention(q, kd, vd, q_offsets, blocks, boffsets, context, bs, d ** -0.5,
                          expect)
     assert_bf16_close(out.cpu(), expect)
+
+
+FUSED_CASES = 12
+
+
+def _fused_config(seed: int) -> dict:
+    r = random.Random(3000 + seed)
+    kv_heads = r.choice([1, 2, 4, 8])
+    longest = r.choice([1, 40, 900, 3000, 12000])
+    batch = r.randint(1, 10 if longest <= 3000 else 3)
+    lengths = [r.randint(0, longest) for _ in range(batch)]
+    lengths[r.randrange(batch)] = longest
+    return dict(kv_heads=kv_heads, heads=kv_heads * r.choice([1, 2, 4, 5, 8, 16]),
+                lengths=lengths, block_size=r.choice([16, 16, 8, 32, 5]),
+                fp8=r.random() < 0.3, layout=r.choice(["head_major", "token_major"]),
+                hint=r.choice([None, longest, 4 * longest + 7]))
+
+
+def _fused_id(seed: int) -> str:
+    c = _fused_config(seed)
+    return (f"s{seed}-h{c['heads']}kv{c['kv_heads']}-bs{c['block_size']}-"
+            f"{'fp8' if c['fp8'] else 'bf16'}-{c['layout']}-L{max(c['lengths'])}x"
+            f"{len(c['lengths'])}")
+
+
+@pytest.mark.parametrize("seed", range(FUSED_CASES), ids=_fused_id)
+def test_fused_decode_step_random_configuration(device, seed):
+    """The fused decode step (QK-norm + RoPE + the new token's K/V write +
+    attention) against the unfused kernels (cache bytes bit-identical) and
+    the oracle of the whole step (attention output at the bar)."""
+    from oracle import paged_kv as OK
+    from oracle import pointwise as OP
+    from tinyvllm.kernels.paged_decode import paged_decode_qk_norm_rope
+    from tinyvllm.kernels.pointwise import qk_norm_rope_store
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    c = _fused_config(seed)
+    g = torch.Generator().manual_seed(seed)
+    bs, d, heads, hkv = c["block_size"], 128, c["heads"], c["kv_heads"]
+    lengths = c["lengths"]
+    rows = len(lengths)
+    pool, blocks, offsets = _tables(g, [max(n, 1) for n in lengths], bs)
+    slots = [int(blocks[offsets[r] + (n - 1) // bs]) * bs + (n - 1) % bs if n > 0 else -1
+             for r, n in enumerate(lengths)]
+    ks, vs = (0.5, 0.25) if c["fp8"] else (1.0, 1.0)
+    k_init = torch.randn(pool * bs, hkv, d, generator=g) * ks
+    v_init = torch.randn(pool * bs, hkv, d, generator=g) * vs
+    qkv = torch.randn(rows, (heads + 2 * hkv) * d, generator=g).to(torch.bfloat16)
+    qw = (1 + 0.05 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.05 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    cos, sin = OP.rope_tables(torch.tensor([max(n - 1, 0) for n in lengths]), d, 1e6,
+                              torch.bfloat16)
+
+    def cache():
+        if c["fp8"]:
+            return _fp8_cache(k_init, v_init, bs, device, ks, vs, c["layout"])[0]
+        return _Cache(k_init.to(torch.bfloat16).to(device), v_init.to(torch.bfloat16).to(device),
+                      bs, layout=c["layout"])
+
+    G = lambda t: t.to(device)  # noqa: E731
+    gqkv = G(qkv)
+    q = gqkv[:, :heads * d].view(rows, heads, d)
+    k = gqkv[:, heads * d:(heads + hkv) * d].view(rows, hkv, d)
+    v = gqkv[:, (heads + hkv) * d:].view(rows, hkv, d)
+    gslots = G(torch.tensor(slots))
+    meta = SingleQueryMetadata(G(torch.arange(rows)), G(blocks), G(offsets),
+                               G(torch.tensor(lengths)), c["hint"])
+    cache_a = cache()
+    qk_norm_rope_store(q, k, v, G(qw), G(kw), G(cos), G(sin), 1e-6, 1e-6,
+                       cache_a.key[0], cache_a.value[0], gslots, k_scale=ks, v_scale=vs)
+    cache_b = cache()
+    out = torch.full((rows, heads, d), 7.0, dtype=torch.bfloat16, device=device)
+    paged_decode_qk_norm_rope(q, k, v, G(qw), G(kw), G(cos), G(sin), 1e-6, 1e-6,
+                              cache_b, 0, meta, gslots, out, scale=d ** -0.5)
+    torch.cuda.synchronize()
+    for name in ("key", "value"):
+        a = getattr(cache_a, name)[0].cpu().view(torch.uint8)
+        b = getattr(cache_b, name)[0].cpu().view(torch.uint8)
+        assert torch.equal(a, b), f"{name} cache bytes differ from the unfused write"
+    # The oracle of the whole step attends over the cache as the step left it
+    # (its new rows are the unfused kernels' bytes, pinned above).
+    if c["fp8"]:
+        kd = OK.fp8_dequantize(cache_b.key[0].cpu().view(torch.uint8), ks)
+        vd = OK.fp8_dequantize(cache_b.value[0].cpu().view(torch.uint8), vs)
+    else:
+        kd, vd = cache_b.key[0].cpu(), cache_b.value[0].cpu()
+    q_ref, _ = OP.qk_norm_rope(qkv[:, :heads * d].view(rows, heads, d),
+                               qkv[:, heads * d:(heads + hkv) * d].view(rows, hkv, d),
+                               qw, kw, cos, sin)
+    expect = torch.zeros(rows, heads, d, dtype=torch.bfloat16)
+    OA.decode_attention(q_ref, kd, vd, torch.arange(rows), blocks, offsets,
+                        torch.tensor(lengths), bs, d ** -0.5, expect)
+    assert_bf16_close(out.cpu(), expect)
+    for r, n in enumerate(lengths):
+        if n == 0:
+            assert (out[r].cpu() == 0).all()
