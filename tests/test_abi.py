@@ -154,6 +154,18 @@ def test_decode_workspace_sizes():
     # 4 waves x 4 workgroups, two KV heads per workgroup.
     assert lib.tvllm_paged_decode_workspace_size(16, 64, 8, 128, 32768, 16) == \
         16 * 64 * 4 * 130 * 4
+    # Groups above 16 run the one-wave-per-head kernel: no splits, no
+    # workspace (the no-alloc entry point then never rejects them).
+    assert lib.tvllm_paged_decode_workspace_size(63, 64, 2, 128, 16384, 16) == 0
+    assert lib.tvllm_paged_decode_workspace_size(1, 17, 1, 128, 32768, 16) == 0
+    assert lib.tvllm_paged_decode_workspace_size(1, 16, 1, 128, 32768, 16) > 0
+    # The largest request of any plan with group <= 16 fits the no-alloc
+    # entry point's 8 MiB scratch.
+    worst = max(lib.tvllm_paged_decode_workspace_size(rows, kv * g, kv, 128, ctx, 16)
+                for kv in (1, 2, 4, 8, 16) for g in (1, 2, 4, 8, 16)
+                for rows in (1, 2, 4, 8, 15, 16, 31, 32, 63, 64, 96)
+                for ctx in (1024, 8192, 16384, 65536))
+    assert 0 < worst <= 8 << 20
 
 
 def _plan(lib, *args):

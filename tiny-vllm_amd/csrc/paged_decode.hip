@@ -1104,8 +1104,10 @@ extern "C" int64_t tvllm_paged_decode_workspace_size(int64_t num_rows,
                                                      int64_t block_size) {
     // Partials of the waves of one workgroup merge in LDS; only contexts
     // split over several workgroups (few rows, long contexts) need HBM
-    // partials for the merge kernel.
-    if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || head_dim != 128)
+    // partials for the merge kernel. Groups above 16 take the one-wave-per-
+    // head kernel, which splits nothing.
+    if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || head_dim != 128 ||
+        num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > 16)
         return 0;
     const SplitPlan p = plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
     if (p.grid <= 1) return 0;
