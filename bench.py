@@ -135,13 +135,13 @@ COUNTERS_FILE = ROOT / "profiles" / "paged_decode_qwen3-8b_bs64_ctx2k_counters.t
 def measured_traffic() -> int | None:
     """HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes (copy-calibrated); None if that summary is absent."""
+    import re
+
     try:
-        for line in COUNTERS_FILE.read_text().splitlines():
-            if "traffic_bytes_per_launch:" in line:
-                return int(line.split("traffic_bytes_per_launch:")[1].strip(" )"))
-    except (OSError, ValueError):
-        pass
-    return None
+        found = re.search(r"traffic_bytes_per_launch:\s*(\d+)", COUNTERS_FILE.read_text())
+    except OSError:
+        return None
+    return int(found.group(1)) if found else None
 
 
 def attention_roofline(executor, workload, cfg, iters: int = 30,
