@@ -4,7 +4,10 @@ configurations: GQA groups 1-16, head dims 64/128/256, page sizes 1-32
 caches, both storage layouts, ragged lengths with empty rows, query rows
 picked out of a larger token axis and max_context_len hints above the
 longest row; and the fused decode step (QK-norm, RoPE, KV write and
-attention in one launch) over the same kind of draw. Each configuration comes from its own seed and is printed in
+attention in one launch) over the same kind of draw; and sampling (greedy
+rows exact, temperature / top-k / top-p draws inside the oracle's kept set)
+over vocab sizes around the scan spans, three logit dtypes and tied maxima.
+Each configuration comes from its own seed and is printed in
 the test id; the bar is the one every attention test uses (max abs 2e-2,
 mean relative 1e-3), with empty rows exactly zero."""
 import math
@@ -251,3 +254,57 @@ def test_fused_decode_step_random_configuration(device, seed):
     for r, n in enumerate(lengths):
         if n == 0:
             assert (out[r].cpu() == 0).all()
+
+
+SAMPLING_CASES = 16
+
+
+def _sampling_config(seed: int) -> dict:
+    r = random.Random(5000 + seed)
+    vocab = r.choice([1, 7, 1000, 8191, 8192, 8193, 32000, 151936, 151939])
+    rows = r.randint(1, 8)
+    return dict(vocab=vocab, rows=rows, dtype=r.choice(["bf16", "fp16", "fp32"]),
+                scale=r.choice([0.5, 2.0, 8.0]),
+                temperature=[r.choice([0.0, 0.0, 0.3, 1.0, 1.7]) for _ in range(rows)],
+                top_k=[r.choice([0, 0, 1, 5, 50, vocab]) for _ in range(rows)],
+                top_p=[r.choice([1.0, 1.0, 0.95, 0.5, 0.01]) for _ in range(rows)])
+
+
+def _sampling_id(seed: int) -> str:
+    c = _sampling_config(seed)
+    return f"s{seed}-V{c['vocab']}-R{c['rows']}-{c['dtype']}-x{c['scale']}"
+
+
+@pytest.mark.parametrize("seed", range(SAMPLING_CASES), ids=_sampling_id)
+def test_sampling_random_configuration(device, seed):
+    """Greedy rows (temperature 0) equal the first index of the maximum;
+    every other row's draws, over several noise counters, stay inside the
+    oracle's float64 top-k / top-p kept set."""
+    from oracle import sampling as OS
+    from tinyvllm.kernels.sampling import argmax, sample
+
+    c = _sampling_config(seed)
+    g = torch.Generator().manual_seed(seed)
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[c["dtype"]]
+    rows, vocab = c["rows"], c["vocab"]
+    logits = (c["scale"] * torch.randn(rows, vocab, generator=g)).to(dt)
+    if vocab > 3:  # a tied maximum resolves to its first index
+        logits[0, vocab // 2] = logits[0, vocab - 1] = logits[0].float().max() + 1
+    gl = logits.to(device)
+    greedy = OS.greedy(logits)
+    assert torch.equal(argmax(gl).cpu(), greedy)
+    temp = torch.tensor(c["temperature"], dtype=torch.float32)
+    top_k = torch.tensor(c["top_k"], dtype=torch.long)
+    top_p = torch.tensor(c["top_p"], dtype=torch.float32)
+    kept = [None if c["temperature"][i] == 0 else
+            OS.kept_set(logits[i], c["temperature"][i], c["top_k"][i], c["top_p"][i])
+            for i in range(rows)]
+    seeds = torch.arange(rows, dtype=torch.long) * 7919 + seed
+    for step in range(8):
+        counters = torch.full((rows,), step, dtype=torch.long)
+        drawn = sample(gl, *(t.to(device) for t in (temp, top_k, top_p, seeds, counters))).cpu()
+        for i in range(rows):
+            if kept[i] is None:
+                assert int(drawn[i]) == int(greedy[i]), (step, i)
+            else:
+                assert bool(kept[i][int(drawn[i])]), (step, i, int(drawn[i]))
