@@ -96,3 +96,38 @@ def test_noalloc_rejects_geometry_beyond_scratch():
     proc = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True,
                           text=True, timeout=120)
     assert proc.returncode == 0, proc.stderr
+
+
+@pytest.mark.gpu
+def test_noalloc_decode_random_sequence(device):
+    """Eight seeded geometries in a row on the same static scratch (row
+    counts, GQA groups up to 32 - above 16 the one-wave-per-head kernel,
+    which needs no scratch - long and short contexts, either cache
+    nesting), each bit-identical to the workspace entry point."""
+    import random
+
+    from tinyvllm.kernels._extension import load_kernels
+
+    lib = load_kernels()
+    r = random.Random(77)
+    for step in range(8):
+        kv_heads = r.choice([1, 2, 4, 8])
+        group = r.choice([1, 2, 4, 8, 16, 32])
+        rows = r.randint(1, 6)
+        lengths = [r.choice([1, 300, 4000, 12000, 30000]) for _ in range(rows)]
+        print(f"noalloc sequence step={step} rows={rows} heads={kv_heads * group}/{kv_heads} "
+              f"lengths={lengths}", flush=True)
+        c = _case(100 + step, rows, kv_heads * group, kv_heads, lengths, device)
+        if r.random() < 0.5:
+            for name in ("k_d", "v_d"):
+                c[name] = c[name].transpose(0, 1).contiguous().transpose(0, 1)
+        need = lib.tvllm_paged_decode_workspace_size(
+            rows, kv_heads * group, kv_heads, 128, c["max_len"], 16)
+        assert need <= 8 << 20
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+        expect = torch.empty_like(c["q_d"])
+        got = torch.full_like(c["q_d"], float("nan"))
+        _call(lib, "tvllm_paged_decode", c, device, expect, workspace=ws)
+        _call(lib, "tvllm_paged_decode_noalloc", c, device, got)
+        torch.cuda.synchronize()
+        assert torch.equal(got, expect), step
