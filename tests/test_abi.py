@@ -185,6 +185,15 @@ def test_decode_split_plans():
     assert _plan(lib, 8, 16, 8, 128, 1024, 16) == (8, 4, 1)       # C1
     assert _plan(lib, 16, 32, 8, 128, 8192, 16) == (4, 4, 2)      # 512 tokens per split
     assert _plan(lib, 16, 32, 8, 128, 8191, 16) == (8, 2, 1)
+    # One long row: up to 256 page ranges per (row, KV head), so 8 KV heads
+    # still put a wave on every SIMD (8 x 32 workgroups of 8 waves).
+    assert _plan(lib, 1, 32, 8, 128, 32768, 16) == (8, 32, 1)
+    assert _plan(lib, 2, 32, 8, 128, 32768, 16) == (8, 16, 1)
+    assert _plan(lib, 1, 64, 8, 128, 131072, 16) == (4, 64, 2)
+    # The merge launch holds one workgroup-level split per lane.
+    assert max(_plan(lib, rows, 4 * kv, kv, 128, ctx, 16)[1]
+               for rows in range(1, 80) for kv in (1, 2, 4, 8)
+               for ctx in (16, 512, 4096, 32768, 131072, 1 << 20)) <= 64
 
 
 def test_decode_workspace_at_the_longest_context_covers_shorter_ones():
