@@ -62,18 +62,33 @@ def random_weights(cfg: TinyQwen3, seed: int, dtype: torch.dtype,
     return w
 
 
-def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    return (x.float() @ w.float().t()).to(x.dtype)
+def linear(x: torch.Tensor, w: torch.Tensor, k_slices: int = 1) -> torch.Tensor:
+    """bf16-style linear: fp32 products and sums, one rounding to x's dtype.
+    ``k_slices > 1`` sums the reduction in that many contiguous slices (each
+    an fp32 matmul, added in slice order) - the same arithmetic in another
+    fp32 summation order, as a split-K GEMM does it."""
+    if k_slices == 1:
+        return (x.float() @ w.float().t()).to(x.dtype)
+    k = x.shape[-1]
+    bounds = [k * i // k_slices for i in range(k_slices + 1)]
+    acc = None
+    for lo, hi in zip(bounds, bounds[1:]):
+        part = x[..., lo:hi].float() @ w[:, lo:hi].float().t()
+        acc = part if acc is None else acc + part
+    return acc.to(x.dtype)
 
 
 def forward(cfg: TinyQwen3, w: dict[str, torch.Tensor], token_ids: list[int],
             kv_fp8: tuple[float, float] | None = None,
-            logit_rows: list[int] | None = None) -> torch.Tensor:
+            logit_rows: list[int] | None = None, k_slices: int = 1) -> torch.Tensor:
     """Full causal forward of one sequence; logits [L, vocab] (storage-dtype values).
     ``kv_fp8=(k_scale, v_scale)`` attends over K/V passed through the FP8 E4M3
     cache layout (quantised, then read back), as an engine with that layout
     does. ``logit_rows`` limits the LM head to those positions (logits
-    [len(logit_rows), vocab])."""
+    [len(logit_rows), vocab]). ``k_slices`` sums every linear layer's
+    reduction in that many slices (``linear``): the same rounding points in
+    another fp32 summation order, which measures how far the bf16 roundings
+    alone move the logits."""
     ids = torch.tensor(token_ids, dtype=torch.long)
     length = ids.numel()
     dtype = w["model.embed_tokens.weight"].dtype
@@ -90,7 +105,7 @@ def forward(cfg: TinyQwen3, w: dict[str, torch.Tensor], token_ids: list[int],
         else:
             x, residual = P.add_rms_norm(hidden, residual, w[f"{p}.input_layernorm.weight"],
                                          cfg.rms_norm_eps)
-        qkv = linear(x, w[f"{p}.self_attn.qkv_proj.weight"])
+        qkv = linear(x, w[f"{p}.self_attn.qkv_proj.weight"], k_slices)
         q = qkv[:, :hq * d].view(length, hq, d)
         k = qkv[:, hq * d:(hq + hkv) * d].view(length, hkv, d)
         v = qkv[:, (hq + hkv) * d:].view(length, hkv, d)
@@ -107,17 +122,17 @@ def forward(cfg: TinyQwen3, w: dict[str, torch.Tensor], token_ids: list[int],
         s = torch.einsum("qhd,khd->hqk", q.float(), kf) * d ** -0.5
         s = s.masked_fill(~causal[None], float("-inf"))
         attn = torch.einsum("hqk,khd->qhd", torch.softmax(s, -1), vf).to(dtype)
-        hidden = linear(attn.reshape(length, hq * d), w[f"{p}.self_attn.o_proj.weight"])
+        hidden = linear(attn.reshape(length, hq * d), w[f"{p}.self_attn.o_proj.weight"], k_slices)
         x, residual = P.add_rms_norm(hidden, residual,
                                      w[f"{p}.post_attention_layernorm.weight"], cfg.rms_norm_eps)
-        gu = linear(x, w[f"{p}.mlp.gate_up_proj.weight"])
-        hidden = linear(P.silu_and_mul(gu), w[f"{p}.mlp.down_proj.weight"])
+        gu = linear(x, w[f"{p}.mlp.gate_up_proj.weight"], k_slices)
+        hidden = linear(P.silu_and_mul(gu), w[f"{p}.mlp.down_proj.weight"], k_slices)
     if logit_rows is not None:
         rows = torch.tensor(logit_rows, dtype=torch.long)
         hidden, residual = hidden[rows], residual[rows]
     hidden, _ = P.add_rms_norm(hidden, residual, w["model.norm.weight"], cfg.rms_norm_eps)
     head = w.get("lm_head.weight", w["model.embed_tokens.weight"])
-    return linear(hidden, head).float()  # bf16 logits, as F.linear produces
+    return linear(hidden, head, k_slices).float()  # bf16 logits, as F.linear produces
 
 
 def greedy_generate(cfg: TinyQwen3, w, prompt: list[int], new_tokens: int) -> list[int]:

@@ -1,25 +1,34 @@
 """Model-level parity at the benchmark architectures (configs C3, C4, C5).
 
 * C3: the whole Qwen3-0.6B (28 layers, vocab 151936, tied embeddings) with
-  N(0, 0.02) weights, 32 requests of 512 random ids, greedy, through the
-  engine (chunked prefill, graph-replayed decode at batch 32). The sampled
-  tokens of 4 rows are checked teacher-forced against the CPU oracle model.
-* C4: Qwen3-8B geometry (hidden 4096, 32Q/8KV, FFN 12288, vocab 151936),
-  64 requests of 2048 ids, chunked prefill 512, Poisson arrivals (mean gap
-  20 ms on a simulated clock), greedy. A 2-layer model is checked token by
-  token against the oracle (and pipelined == serial, all blocks freed); the
-  full 36-layer model is checked one layer at a time in a live decode step
-  (attention output, post-attention norm, residual and KV write against the
-  oracle layer on the engine's own cache).
-* C5: Qwen3-32B geometry (hidden 5120, 64Q/8KV, FFN 25600), 16 requests of
-  16k-32k ids sharing a 4096-token prefix through the prefix cache: the
-  live-layer check at the second layer of a 2-layer model, the first layer's
-  K/V of the shared prefix against the oracle, and shared prefix pages.
+  N(0, 0.02) weights, 32 requests of 512 random ids, 256 new tokens each,
+  greedy, through the engine (chunked prefill, graph-replayed decode at
+  batch 32). 8 rows are checked teacher-forced against the CPU oracle model
+  over all their tokens (2048 steps).
+* C4: Qwen3-8B (hidden 4096, 32Q/8KV, FFN 12288, vocab 151936, 36 layers,
+  untied LM head), 64 requests of 2048 ids, chunked prefill 512, Poisson
+  arrivals (mean gap 20 ms on a simulated clock), greedy. The full 36-layer
+  model: 2 rows x 64 tokens teacher-forced against the 36-layer oracle, and
+  layer 20 of a live batch-64 decode step (attention output, post-attention
+  norm, residual and KV write against the oracle layer on the engine's own
+  cache). A 2-layer model of the same geometry checks pipelined == serial
+  tokens and that all blocks return to the pool.
+* C5: the full 64-layer Qwen3-32B (hidden 5120, 64Q/8KV, FFN 25600), 16
+  requests of 16k-32k ids sharing a 4096-token prefix through the prefix
+  cache, 128 new tokens: the live-layer check at layer 40, the first
+  layer's K/V of the shared prefix against the oracle, and shared prefix
+  pages.
 
 Greedy agreement (north star: >= 99% of steps) is teacher-forced: a step
 agrees when our token is the oracle's argmax for the same context, or when
 the oracle scores it within one bf16 ulp of its best logit (a tie at bf16
-resolution that another summation order may legitimately break).
+resolution that another summation order may legitimately break). At the
+36-layer depth one ulp is below what bf16 rounding alone does to the
+logits: the oracle recomputed with its linear layers summed in four slices
+(the same rounding points, another fp32 order) moves them by up to ~10 ulps
+and misses its own argmax on a few percent of steps. There a step also
+agrees when the deficit is within that step's largest such move, and at
+least 90% of steps must still agree within one ulp.
 Reference path: models/qwen3.py:458-494 and :703-717, executor.py:126-141.
 """
 
@@ -50,19 +59,50 @@ def oracle_config(name, layers=None, max_position=4096):
                         max_position_embeddings=max_position)
 
 
-def teacher_forced(cfg, weights, prompt, ours):
+def teacher_forced(cfg, weights, prompt, ours, label="", reorder_band=False):
     """(agreeing steps, worst oracle logit deficit in ulps) of our greedy
-    tokens against one oracle forward over prompt + ours."""
+    tokens against one oracle forward over prompt + ours. A step agrees when
+    the oracle's best logit exceeds its logit of our token (the deficit) by
+    at most one bf16 ulp of the best.
+
+    ``reorder_band``: a second oracle forward with every linear layer summed
+    in 4 slices (the same roundings, another fp32 summation order) measures
+    how far bf16 rounding alone moves this step's logits; a step also agrees
+    when the deficit is within that step's largest such move. Returns
+    (agree, worst, strict agreements, reordered-oracle misses) then.
+    Prints the per-step deficits when ``label`` is given."""
     rows = [len(prompt) - 1 + i for i in range(len(ours))]
-    logits = OM.forward(cfg, weights, list(prompt) + list(ours), logit_rows=rows)
-    agree, worst = 0, 0.0
+    seq = list(prompt) + list(ours)
+    logits = OM.forward(cfg, weights, seq, logit_rows=rows)
+    band = alt_miss = None
+    if reorder_band:
+        alt = OM.forward(cfg, weights, seq, logit_rows=rows, k_slices=4)
+        band = (logits - alt).abs().amax(-1)
+        alt_miss = 0
+    agree, strict, worst, deficits = 0, 0, 0.0, []
     for i, token in enumerate(ours):
         row = logits[i]
         best = float(row.max())
-        deficit = (best - float(row[token])) / bf16_ulp(best)
+        ulp = bf16_ulp(best)
+        deficit = (best - float(row[token])) / ulp
+        deficits.append(deficit)
         worst = max(worst, deficit)
-        agree += int(deficit <= 1.0)
-    return agree, worst
+        strict += int(deficit <= 1.0)
+        allowed = 1.0 if band is None else max(1.0, float(band[i]) / ulp)
+        agree += int(deficit <= allowed)
+        if band is not None:
+            alt_miss += int((best - float(row[int(alt[i].argmax())])) / ulp > 1.0)
+    if label:
+        ties = sum(0.0 < d <= 1.0 for d in deficits)
+        extra = "" if band is None else (
+            f"; reordered oracle: {alt_miss} misses beyond one ulp, logit moves up to "
+            f"{float(band.max()):.3f} (mean of row maxima {float(band.mean()):.3f})")
+        print(f"{label}: {agree}/{len(ours)} agree, {strict} within one ulp "
+              f"({ties} ties){extra}; per-step deficits (ulp) "
+              + " ".join(f"{d:.1f}" for d in deficits), flush=True)
+    if band is None:
+        return agree, worst
+    return agree, worst, strict, alt_miss
 
 
 def run_engine(engine, prompts, params, arrivals_ns=None, step_ns=2_000_000,
@@ -250,12 +290,27 @@ def check_layer_against_oracle(cap, w, key_cache, value_cache, cfg, block_size=1
     # projection and one of the sum (2 ulps of the operands' magnitude).
     assert_within_ulp(cap["residual_out"], res2,
                       scale=torch.maximum(o.float().abs(), res.float().abs()), ulps=2.0)
-    # The norm given our residual: the strict bar. Against the independent
-    # oracle chain only the mean error is bounded: where o and the residual
-    # cancel, one rounding flip of o is many ulps of the sum, and the norm
-    # scales that up.
+    # The norm given our residual: the strict bar.
     assert_bf16_close(cap["normed"], OP.rms_norm(cap["residual_out"], w["post"], eps))
-    assert_within_ulp(cap["normed"], normed, max_abs=float("inf"))
+    # Against the independent oracle chain, element by element: the residual
+    # differs by at most 2 ulps of m = max(|o|, |res|) (checked above); where
+    # o and the residual cancel that is many ulps of the sum itself, so the
+    # bound is carried through the norm: 2 ulp(m) x rstd x |w|, plus the
+    # norm's own two roundings (of x * rstd, then of the weight product),
+    # with the bar's 2e-2 as the floor; the mean error at the bar.
+    rstd = torch.rsqrt(res2.float().pow(2).mean(-1, keepdim=True) + eps)
+    ulp_in = _ulp(torch.maximum(o.float().abs(), res.float().abs()))
+    e = normed.float()
+    allowed = torch.clamp(2 * ulp_in * rstd * w["post"].float().abs() + 2 * _ulp(e.abs()),
+                          min=2e-2)
+    excess = ((cap["normed"].float() - e).abs() / allowed).max().item()
+    assert excess <= 1.0, f"post-attention norm error {excess:.2f}x its element-wise bound"
+    assert_bf16_close(cap["normed"], normed, max_abs=float("inf"))
+
+
+def _ulp(mag):
+    """One bf16 ulp at each |value| (7 fraction bits)."""
+    return torch.exp2(torch.floor(torch.log2(mag.clamp_min(2.0 ** -126))) - 7)
 
 
 def probe_run(engine, model, idx, prompts, params, arrivals_ns, step_ns=50_000_000):
@@ -297,6 +352,9 @@ def probe_run(engine, model, idx, prompts, params, arrivals_ns, step_ns=50_000_0
 # ---------------------------------------------------------------------- C3 --
 
 def test_c3_qwen3_0_6b_engine_greedy_matches_oracle(device):
+    """The whole C3 workload (32 requests x 512 ids, 256 new tokens each,
+    greedy); 8 rows spread over the batch are teacher-forced against the
+    oracle model over all 256 tokens (2048 steps)."""
     from tinyvllm import SamplingParams
     from tinyvllm.bootstrap import build_engine
 
@@ -304,7 +362,7 @@ def test_c3_qwen3_0_6b_engine_greedy_matches_oracle(device):
     model, weights = model_and_weights(cfg, device, seed=3)
     g = torch.Generator().manual_seed(33)
     prompts = [torch.randint(0, VOCAB, (512,), generator=g).tolist() for _ in range(32)]
-    new = 8
+    new = 256
     engine = build_engine(model, max_model_len=1024, max_num_seqs=32,
                           max_num_batched_tokens=4096, num_blocks=blocks_for([512] * 32, new),
                           prefill_chunk_size=512)
@@ -315,10 +373,11 @@ def test_c3_qwen3_0_6b_engine_greedy_matches_oracle(device):
     engine.close()
     agree = total = 0
     worst = 0.0
-    for r in (0, 9, 20, 31):
-        a, w = teacher_forced(cfg, weights, prompts[r], outs[r])
+    for r in (0, 4, 9, 13, 20, 22, 27, 31):
+        a, w = teacher_forced(cfg, weights, prompts[r], outs[r], label=f"C3 row {r}")
         agree, total, worst = agree + a, total + new, max(worst, w)
     print(f"C3 teacher-forced agreement {agree}/{total}, worst deficit {worst:.2f} ulp")
+    assert total >= 2048
     assert agree / total >= 0.99, (agree, total, worst)
 
 
@@ -359,35 +418,65 @@ def test_c4_qwen3_8b_geometry_engine_tokens_match_oracle(device):
     agree = total = 0
     worst = 0.0
     for r in (0, 63):
-        a, w = teacher_forced(cfg, weights, prompts[r], runs[0][r])
+        a, w = teacher_forced(cfg, weights, prompts[r], runs[0][r], label=f"C4 2-layer row {r}")
         agree, total, worst = agree + a, total + new, max(worst, w)
     print(f"C4 teacher-forced agreement {agree}/{total}, worst deficit {worst:.2f} ulp")
     assert agree / total >= 0.99, (agree, total, worst)
 
 
-def test_c4_qwen3_8b_live_decode_layer_matches_oracle(device):
-    """The full 36-layer Qwen3-8B (random N(0, 0.02), norms 1) through the C4
-    workload; in one decode step at batch 64 (contexts 2050-2100) layer 20 is
-    recomputed by the oracle from its captured input over the engine's own
-    cache. Layer 0's K/V of request 0's whole prompt (written by chunked
-    prefill) is checked against the oracle too."""
+@pytest.mark.timeout(900)
+def test_c4_qwen3_8b_full_depth_engine_greedy_and_live_layer_match_oracle(device):
+    """The full 36-layer Qwen3-8B (random N(0, 0.02), norms 1, untied LM
+    head) through the C4 workload (64 x 2048 ids, chunked prefill 512,
+    Poisson arrivals, 64 new tokens each, graph-replayed decode at batch 64):
+
+    * greedy tokens: rows 0 and 63 (first and last to arrive) teacher-forced
+      against the 36-layer oracle model over all 64 tokens (128 steps; one
+      oracle forward of a row is ~29 TFLOP of fp32 CPU work, and a second
+      one with the linear layers summed in slices gives each step's rounding
+      band);
+    * in one decode step at batch 64 (contexts 2050-2100) layer 20 is
+      recomputed by the oracle from its captured input over the engine's own
+      cache;
+    * layer 0's K/V of request 0's whole prompt (written by chunked prefill)
+      against the oracle."""
     from tinyvllm import SamplingParams
     from tinyvllm.bootstrap import build_engine
-    from tinyvllm.models.qwen3 import Qwen3ForCausalLM
 
     cfg = oracle_config("qwen3-8b", max_position=4096)
-    model = Qwen3ForCausalLM.random_init(_our_config(cfg), device=device, seed=8)
+    model, weights = model_and_weights(cfg, device, seed=8)
+    assert "lm_head.weight" in weights and len(
+        [n for n in weights if n.endswith("down_proj.weight")]) == 36
     prompts, arrivals = _c4_workload(seed=45)
+    new = 64
     engine = build_engine(model, max_model_len=4096, max_num_seqs=64,
-                          max_num_batched_tokens=4096, num_blocks=blocks_for([2048] * 64, 64),
+                          max_num_batched_tokens=4096, num_blocks=blocks_for([2048] * 64, new),
                           prefill_chunk_size=512)
-    params = SamplingParams(max_new_tokens=64, ignore_eos=True)
+    params = SamplingParams(max_new_tokens=new, ignore_eos=True)
     cap, (kc, vc), outs = probe_run(engine, model, 20, prompts, params, arrivals)
-    assert all(len(o) == 64 for o in outs)
+    assert all(len(o) == new for o in outs)
     assert int(cap["lengths"].min()) >= 2049
     check_layer_against_oracle(cap, layer_weights(model, 20), kc, vc, cfg)
     _check_layer0_prompt_kv(engine, model, cfg, prompts[0], cap, row=cap["row_of"][0])
     engine.close()
+    del engine, kc, vc
+    torch.cuda.empty_cache()
+    agree = total = strict = alt_miss = 0
+    worst = 0.0
+    for r in (0, 63):
+        a, w, st, am = teacher_forced(cfg, weights, prompts[r], outs[r],
+                                      label=f"C4 36-layer row {r}", reorder_band=True)
+        agree, total, worst = agree + a, total + new, max(worst, w)
+        strict, alt_miss = strict + st, alt_miss + am
+    print(f"C4 36-layer teacher-forced agreement {agree}/{total} within the reorder band, "
+          f"{strict}/{total} within one ulp (the reordered oracle itself: {alt_miss} "
+          f"misses), worst deficit {worst:.2f} ulp")
+    assert total >= 32
+    # At 36 layers a reordering of the oracle's own fp32 sums moves the bf16
+    # logits by up to ~10 ulps and flips a few percent of near-tied argmaxes
+    # by itself; a kernel bug moves them by tens of ulps on most steps.
+    assert strict / total >= 0.9, (strict, total, worst)
+    assert agree / total >= 0.99, (agree, total, worst)
 
 
 def _our_config(cfg):
@@ -428,37 +517,39 @@ def _check_layer0_prompt_kv(engine, model, cfg, prompt, cap, row, count=None):
 
 # ---------------------------------------------------------------------- C5 --
 
-def test_c5_qwen3_32b_geometry_long_context_shared_prefix(device):
-    """Two layers of the Qwen3-32B geometry, 16 requests of U[16k, 32k]
-    random ids sharing a 4096-token prefix: prefix pages are shared (not
-    copied) between rows, layer 0's K/V of the prefix matches the oracle,
-    and in a live decode step (split-K over ~24k-token contexts, 64Q/8KV)
-    layer 1 matches the oracle layer over the engine's cache."""
+@pytest.mark.timeout(600)
+def test_c5_qwen3_32b_long_context_shared_prefix(device):
+    """The full 64-layer Qwen3-32B (random N(0, 0.02), norms 1), 16 requests
+    of U[16k, 32k] random ids sharing a 4096-token prefix, 128 new tokens
+    each: prefix pages are shared (not copied) between rows, layer 0's K/V
+    of the prefix matches the oracle, and in a live decode step (split-K
+    over ~24k-token contexts, 64Q/8KV) layer 40 matches the oracle layer
+    over the engine's cache."""
     from tinyvllm import SamplingParams
     from tinyvllm.bootstrap import build_engine
     from tinyvllm.models.qwen3 import Qwen3ForCausalLM
 
-    cfg = oracle_config("qwen3-32b", layers=2, max_position=40960)
+    cfg = oracle_config("qwen3-32b", max_position=40960)
     model = Qwen3ForCausalLM.random_init(_our_config(cfg), device=device, seed=32)
     rng = np.random.default_rng(55)
     lengths = rng.integers(16384, 32768 + 1, size=16).tolist()
     shared = rng.integers(0, VOCAB, size=4096).tolist()
     prompts = [shared + rng.integers(0, VOCAB, size=n - 4096).tolist() for n in lengths]
     engine = build_engine(model, max_model_len=40960, max_num_seqs=16,
-                          max_num_batched_tokens=4096, num_blocks=blocks_for(lengths, 160),
+                          max_num_batched_tokens=4096, num_blocks=blocks_for(lengths, 128),
                           prefill_chunk_size=512)
     # ~100 chunked-prefill steps: early requests keep decoding until the last
     # prompt is in, so one step decodes all 16 rows.
-    params = SamplingParams(max_new_tokens=160, ignore_eos=True)
-    cap, (kc, vc), outs = probe_run(engine, model, 1, prompts, params, [0] * 16)
-    assert all(len(o) == 160 for o in outs)
+    params = SamplingParams(max_new_tokens=128, ignore_eos=True)
+    cap, (kc, vc), outs = probe_run(engine, model, 40, prompts, params, [0] * 16)
+    assert all(len(o) == 128 for o in outs)
     prefix_pages = 4096 // 16
     tables = [cap["blocks"][int(cap["offsets"][r]):int(cap["offsets"][r + 1])]
               for r in range(16)]
     sharing = sum(torch.equal(t[:prefix_pages], tables[0][:prefix_pages]) for t in tables[1:])
     assert sharing >= 8, sharing  # most requests reuse the published prefix pages
     assert engine.scheduler.block_manager.prefix_cache.hit_tokens >= 8 * 4096
-    check_layer_against_oracle(cap, layer_weights(model, 1), kc, vc, cfg)
+    check_layer_against_oracle(cap, layer_weights(model, 40), kc, vc, cfg)
     _check_layer0_prompt_kv(engine, model, cfg, prompts[0], cap, row=cap["row_of"][0],
                             count=4096)
     engine.close()
