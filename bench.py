@@ -14,6 +14,10 @@ Also reported on the same JSON line:
                   it runs on: algorithmic bytes / average launch duration.
   cpu_baseline -- the CPU oracle's decode step, one layer at full batch
                   timed and extrapolated to all layers + LM head.
+  engine_ms_per_step -- the same batch driven through Engine.step (scheduler,
+                  block manager, batch builder, commit and resolve inside the
+                  timing) after prefilling 64 prompts of 2048 ids: the mean
+                  decode-only step time, beside the headline's ms_per_step.
 """
 from __future__ import annotations
 
@@ -275,6 +279,62 @@ def cpu_baseline(cfg, batch: int, context: int, reps: int = 21) -> dict:
             "sample": (f"oracle decode step, 1 of {cfg.num_hidden_layers} layers at bs{batch} "
                        f"ctx{context} timed x{reps} (median {per_layer:.2f} s) + LM head "
                        f"({head:.2f} s), extrapolated to the full model")}
+
+
+def engine_decode_step(model, cfg, batch: int, context: int, steps: int,
+                       warmup: int) -> dict:
+    """The same decode batch driven through the whole engine: ``batch``
+    requests of ``context`` random ids are prefilled (chunks of 512), then
+    ``steps`` decode-only ``Engine.step`` calls are timed - scheduler,
+    block-manager transaction, BatchBuilder, the launch, commit and the
+    resolve of the previous step's tokens all inside the timing, pipelined
+    as the engine runs them."""
+    import numpy as np
+    import torch
+
+    from tinyvllm import SamplingParams
+    from tinyvllm.bootstrap import build_engine
+
+    rng = np.random.default_rng(7)
+    prompts = [rng.integers(0, cfg.vocab_size, size=context).tolist() for _ in range(batch)]
+    # Prefill admits ~4096 tokens a step, so early rows decode meanwhile.
+    prefill_steps = -(-batch * context // 4096) + 2
+    new = prefill_steps + warmup + steps + 8
+    max_model_len = 1 << (context + new + 16 - 1).bit_length()
+    engine = build_engine(model, max_model_len=max_model_len, max_num_seqs=batch,
+                          max_num_batched_tokens=4096,
+                          num_blocks=batch * -(-(context + new) // 16) + 64,
+                          prefill_chunk_size=512)
+    params = SamplingParams(max_new_tokens=new, ignore_eos=True)
+    ids = [engine.submit(p, params) for p in prompts]
+    got = {rid: 0 for rid in ids}
+    calls = 0
+    while min(got.values()) < 2:  # every prompt prefilled, first tokens out
+        for ev in engine.step().token_events:
+            got[ev.request_id] += 1
+        calls += 1
+        if calls > 10 * prefill_steps:
+            raise RuntimeError("engine benchmark: prefill did not finish")
+    for _ in range(warmup):
+        engine.step()
+    torch.cuda.synchronize()
+    tokens = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tokens += len(engine.step().token_events)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    if tokens != batch * steps:
+        raise RuntimeError(f"engine benchmark: {tokens} tokens in {steps} steps of {batch} rows")
+    unfinished = engine.has_unfinished()
+    engine.close()
+    assert unfinished  # no request ended inside the timed steps
+    return {"engine_ms_per_step": round(elapsed / steps * 1e3, 3),
+            "engine_tok_s": round(tokens / elapsed, 1),
+            "engine_steps": steps,
+            "engine_sample": f"Engine.step decode-only at bs{batch}, contexts "
+                             f"{context}-{context + prefill_steps + warmup + steps}, "
+                             f"after {calls} prefill steps"}
 
 
 def kernel_only(args) -> None:
@@ -865,6 +925,8 @@ def main() -> None:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-engine-step", action="store_true",
+                    help="skip the engine-driven decode step timing beside the headline")
     ap.add_argument("--full-tables", action="store_true",
                     help="upload every block table each step (no device-resident tables)")
     ap.add_argument("--kv-layout", choices=["auto", "head_major", "token_major"],
@@ -967,6 +1029,13 @@ def main() -> None:
     roof = attention_roofline(executor, workload, cfg, headline=(
         args.model == "qwen3-8b" and args.batch == 64 and args.context == 2048
         and not fp8))
+    engine_line = None
+    if not args.no_engine_step:
+        # The headline executor's KV stays allocated; the engine adds its own.
+        engine_line = engine_decode_step(model, cfg, args.batch, args.context, args.steps,
+                                         args.warmup)
+        engine_line["engine_vs_ms_per_step"] = round(
+            engine_line["engine_ms_per_step"] / (elapsed / args.steps * 1e3), 3)
     cpu = None if args.no_cpu_baseline else cpu_baseline(cfg, args.batch, args.context)
     line = {
         "metric": "decode tok/s Qwen3-8B bs64 ctx2k; paged-attn HBM GB/s and % of peak",
@@ -985,6 +1054,8 @@ def main() -> None:
         "roofline": roof,
         "cpu_baseline": cpu,
         "decode_inputs": inputs_cost,
+        "engine_ms_per_step": engine_line and engine_line["engine_ms_per_step"],
+        "engine_step": engine_line,
     }
     print(json.dumps(line), flush=True)
 

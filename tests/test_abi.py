@@ -1,5 +1,6 @@
 """The C-ABI library loads (no GPU needed) and exports every declared symbol."""
 import ctypes
+import os
 import re
 from pathlib import Path
 
@@ -207,3 +208,27 @@ def test_decode_workspace_at_the_longest_context_covers_shorter_ones():
             cap = lib.tvllm_paged_decode_workspace_size(rows, 64, 8, 128, max_len, 16)
             for ctx in range(16, max_len + 1, 16 * 37):
                 assert lib.tvllm_paged_decode_workspace_size(rows, 64, 8, 128, ctx, 16) <= cap
+
+
+def test_decode_split_plan_under_tuning_override_keeps_the_merge_bound():
+    """A TVLLM_DECODE_TUNING override with one page range per workgroup
+    would ask for up to 256 workgroup splits; the plan caps them at the
+    merge launch's 64, and the workspace size follows the capped plan (the
+    override is read once per process, hence the child process)."""
+    import subprocess
+    import sys
+
+    code = (
+        "from tinyvllm.kernels._extension import load_kernels\n"
+        "lib = load_kernels()\n"
+        "p = lib.tvllm_paged_decode_split_plan(1, 32, 8, 128, 131072, 16)\n"
+        "w = lib.tvllm_paged_decode_workspace_size(1, 32, 8, 128, 131072, 16)\n"
+        "print(p >> 16, (p >> 8) & 0xFF, p & 0xFF, w)\n")
+    env = dict(os.environ, TVLLM_DECODE_TUNING="0,2,4,1")
+    root = Path(__file__).resolve().parents[1]
+    env["PYTHONPATH"] = os.pathsep.join([str(root / "tiny-vllm_amd"), str(root)])
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True,
+                         text=True, timeout=120, check=True).stdout.split()
+    waves, grid, heads, workspace = map(int, out)
+    assert waves == 1 and grid == 64
+    assert workspace == 1 * 32 * 64 * 130 * 4

@@ -57,6 +57,10 @@ def test_device_tables_track_growth_swaps_and_slot_reuse(device):
             assert start == slot[r] * inputs.pitch
             got = table[start:start + len(tables[r])]
             assert list(got) == [int(x) for x in tables[r]], r
+        # Padding rows and the closing entry: one past the tables' end.
+        full = inputs.d["offsets"].cpu().numpy()
+        assert offs.size == len(rids) + 1
+        assert (full[len(rids):] == inputs.table_capacity).all()
 
     step([7, 8, 9])                     # whole tables: 3 + 5 + 1
     assert uploads[-1] == 9

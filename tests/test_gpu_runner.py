@@ -267,3 +267,63 @@ def test_cache_layouts_give_bit_identical_runs(device, kv_dtype):
     assert runs["token_major"][1] == runs["head_major"][1]
     for a, b in zip(runs["token_major"][0], runs["head_major"][0]):
         assert torch.equal(a, b)
+
+
+def test_prefill_graphs_exact_fallback_for_v_beyond_fp16(device, monkeypatch):
+    """A cache holding V values beyond the fp16 range (layer 0's V rows of
+    the packed projection scaled by 4e4): the prefill graphs' replays take
+    the exact bf16 fallback launch like eager prefill does, give the eager
+    logits and tokens, and leave the graphs' own fallback guard clear."""
+    from tinyvllm.executor import Executor
+    from tinyvllm.runtime.prefill_graphs import PrefillGraphs
+
+    replays = []
+    original = PrefillGraphs.replay
+
+    def counted(self, tokens, items):
+        replays.append((tokens, items))
+        return original(self, tokens, items)
+
+    monkeypatch.setattr(PrefillGraphs, "replay", counted)
+    weights = OM.random_weights(CFG, seed=11, dtype=torch.bfloat16, std=0.2)
+    name = "model.layers.0.self_attn.qkv_proj.weight"
+    q = CFG.num_attention_heads * CFG.head_dim
+    kv = CFG.num_key_value_heads * CFG.head_dim
+    w = weights[name].float()
+    w[q + kv:] *= 4.0e4
+    weights[name] = w.to(torch.bfloat16)
+    model = _our_model(weights, device)
+    g = torch.Generator().manual_seed(12)
+    prompts = [torch.randint(0, CFG.vocab_size, (n,), generator=g).tolist()
+               for n in (37, 120, 64)]
+    steps = ([(0, 37, True), (1, 60, False)], [(1, 60, True), (2, 64, True)])
+    results = {}
+    for eager in (True, False):
+        executor = Executor(model, block_size=16, num_blocks=64, max_model_len=512,
+                            max_num_seqs=4, enforce_eager=eager)
+        runner = executor.runner
+        assert (runner.prefill_graphs is None) == eager
+        mb = ManualBatches(prompts, block_size=16, num_blocks=64)
+        logits, tokens = [], []
+        for items in steps:
+            batch = mb.step(items)
+            out = runner.run_and_sample(batch, [0] * batch.num_samples)
+            logits.append(out[0].float().cpu())
+            tokens.append(out[1].cpu().tolist())
+            mb.commit(items, tokens[-1])
+        torch.cuda.synchronize()
+        v0 = runner.kv_cache.value[0].float()  # slots never written hold NaN
+        assert torch.nan_to_num(v0, nan=0.0).abs().max().item() >= 65536.0
+        if not eager:
+            guard = runner.prefill_graphs.guard
+            assert guard is not None and int(guard.count_nonzero()) == 0
+        results[eager] = (logits, tokens)
+        executor.clear()
+    assert len(replays) == len(steps)
+    # Padded buckets may run other GEMM tilings than the eager step: the
+    # end-to-end logit bar of the graph test above.
+    assert results[True][1] == results[False][1]
+    for a, b in zip(results[True][0], results[False][0]):
+        assert torch.isfinite(b).all()
+        diff = (a - b).abs()
+        assert diff.max() < 0.15 and diff.mean() / a.abs().mean() < 2e-2, diff.max()

@@ -179,6 +179,7 @@ constexpr int kMaxWaves = 8;  // 2 resident waves per SIMD at <= 256 VGPRs
 // 64, 36.8 us with 256); the workgroup-level splits stay <= 64 (the merge
 // kernel holds one per lane) because a workgroup takes at least four ranges.
 constexpr int64_t kMaxSplits = 256;
+constexpr int64_t kMaxGridSplits = 64;
 
 __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);  // v_exp_f32; inputs here are <= 0
@@ -1051,7 +1052,9 @@ SplitPlan plan_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
     }
     SplitPlan p;
     p.waves = std::min<int64_t>(total, split_waves);
-    p.grid = (total + p.waves - 1) / p.waves;
+    // The merge launch holds one workgroup split per lane: at most 64, even
+    // when a tuning override makes the page ranges per workgroup few.
+    p.grid = std::min<int64_t>((total + p.waves - 1) / p.waves, kMaxGridSplits);
     p.heads = heads_per_group(kv_heads, p.waves, waves);
     return p;
 }
@@ -1193,6 +1196,8 @@ int paged_decode_impl(
         const int hpg = plan.heads;
         const int64_t grid = num_rows * (num_kv_heads / hpg) * plan.grid;
         TVLLM_CHECK(grid <= INT32_MAX, "paged_decode: decode grid is too large");
+        TVLLM_CHECK(plan.grid <= kMaxGridSplits,
+                    "paged_decode: at most 64 workgroup splits per row");
         const int threads = int(64 * hpg * plan.waves);
         const int64_t need = plan.grid > 1
             ? num_rows * num_heads * plan.grid * (head_dim + 2) * int64_t(sizeof(float))
@@ -1298,8 +1303,6 @@ int paged_decode_impl(
 #undef TVLLM_DEC
         const int st = launch_status("paged_decode");
         if (st != TVLLM_OK || plan.grid <= 1) return st;
-        // The merge holds one split per lane (the plan makes at most kMaxSplits).
-        TVLLM_CHECK(plan.grid <= 64, "paged_decode: at most 64 workgroup splits per row");
         paged_decode_merge<T><<<int(num_rows * num_heads), 64, 0, s>>>(
             args.part_o, args.part_ml, static_cast<T*>(out), rows, out_token_stride,
             out_head_stride, int(num_heads), int(plan.grid), int(head_dim), v_scale);

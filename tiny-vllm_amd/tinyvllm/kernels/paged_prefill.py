@@ -6,6 +6,9 @@ wrapper (runtime/prefill.py:15-225).
 """
 from __future__ import annotations
 
+import threading
+from contextlib import contextmanager
+
 import torch
 
 from tinyvllm.kernels._extension import (
@@ -65,14 +68,40 @@ def paged_prefill_attention(
 
 
 _GUARDS: dict[tuple[torch.device, int], torch.Tensor] = {}
+_OWNED = threading.local()
+
+# Bytes of the largest fallback guard any call needs (two int32 words).
+GUARD_BYTES = 8
+
+
+@contextmanager
+def fallback_guard(guard: torch.Tensor):
+    """Calls inside this context use ``guard`` (zero-initialised uint8 of
+    GUARD_BYTES on the calls' device) as their fallback guard. A captured
+    graph owns its guard this way for the graph's lifetime, instead of one
+    keyed by the capture stream's handle, which torch may hand to another
+    stream once the capture stream is gone."""
+    if guard.dtype != torch.uint8 or guard.numel() < GUARD_BYTES or not guard.is_cuda:
+        raise ValueError(f"a fallback guard is a CUDA uint8 tensor of >= {GUARD_BYTES} bytes")
+    previous = getattr(_OWNED, "guard", None)
+    _OWNED.guard = guard
+    try:
+        yield guard
+    finally:
+        _OWNED.guard = previous
 
 
 def _guard(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """The zero-initialised fallback guard of ``device``'s current stream
-    (calls on one stream are ordered, so they can share it; the kernels
-    leave it zero)."""
+    """The zero-initialised fallback guard: the one ``fallback_guard``
+    installed, else that of ``device``'s current stream (calls on one stream
+    are ordered, so they can share it; the kernels leave it zero)."""
     if nbytes == 0:
         return None
+    owned = getattr(_OWNED, "guard", None)
+    if owned is not None:
+        if owned.device != device or owned.numel() < nbytes:
+            raise RuntimeError("the installed fallback guard does not fit this call")
+        return owned
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     guard = _GUARDS.get(key)
     if guard is None or guard.numel() < nbytes:

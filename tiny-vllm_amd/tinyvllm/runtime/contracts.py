@@ -42,7 +42,10 @@ class SingleQueryMetadata:
     context_lens[r] / block_size)]``: a CSR (offsets ascending, as the
     reference builds them) is one layout, the decode step's device-resident
     tables (one pitched row per request slot) another; the kernels read
-    only ``block_table_offsets[r]``.
+    only ``block_table_offsets[r]``. In the pitched layout the offsets are
+    not ascending and ``block_table_offsets[r + 1] - block_table_offsets[r]``
+    is no row's table size: padding rows and the closing entry hold the
+    table capacity (one past the end), as the reference pads them.
     """
 
     query_rows: torch.Tensor

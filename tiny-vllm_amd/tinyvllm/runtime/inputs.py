@@ -117,7 +117,10 @@ class DecodeInputs:
         h["tokens"][count:] = 0
         h["positions"][count:] = 0
         h["slots"][count:] = -1
-        h["offsets"][count:] = 0
+        # One past the tables' end, as the reference pads (inputs.py:94-98):
+        # never a row start, so a stray read of a padded row's table faults
+        # loudly in a bounds check instead of aliasing request slot 0.
+        h["offsets"][count:] = self.table_capacity
         h["lengths"][count:] = 0
         h["temperature"][count:] = 0.0
         h["top_p"][count:] = 1.0

@@ -37,6 +37,7 @@ import torch
 
 from tinyvllm._validation import _check_positive_int
 from tinyvllm.batch import PreparedBatch
+from tinyvllm.kernels.paged_prefill import GUARD_BYTES, fallback_guard
 from tinyvllm.kernels.sampling import resolve_tokens, sample
 from tinyvllm.paged_kv import PagedKVCache
 from tinyvllm.runtime.attention import HipAttention
@@ -204,6 +205,9 @@ class PrefillGraphs:
         self.entries: dict[tuple[int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor,
                                                   torch.Tensor]] = {}
         self.pool = None
+        # The prefill kernels' fallback guard of every captured graph: owned
+        # here, so it lives exactly as long as the graphs that point at it.
+        self.guard: torch.Tensor | None = None
 
     @torch.inference_mode()
     def capture(self, model: torch.nn.Module, inputs: PrefillInputs,
@@ -227,8 +231,9 @@ class PrefillGraphs:
         side = torch.cuda.Stream(device=inputs.device)
         side.wait_stream(self.stream)
         self.pool = torch.cuda.graph_pool_handle()
+        self.guard = torch.zeros(GUARD_BYTES, dtype=torch.uint8, device=inputs.device)
         try:
-            with torch.cuda.stream(side):
+            with torch.cuda.stream(side), fallback_guard(self.guard):
                 below = 0  # the previous token bucket
                 for tokens in TOKEN_BUCKETS:
                     if tokens > inputs.max_tokens:
@@ -267,7 +272,7 @@ class PrefillGraphs:
             logits = model.compute_logits(hidden, model_input.sample_token_indices)
             return logits, sample(logits, *params)
 
-        for _ in range(2):  # also creates the prefill fallback guard of ``side``
+        for _ in range(2):
             step()
         side.synchronize()
         graph = torch.cuda.CUDAGraph()
@@ -287,3 +292,4 @@ class PrefillGraphs:
         self.stream.synchronize()
         self.entries.clear()
         self.pool = None
+        self.guard = None
