@@ -448,11 +448,14 @@ def summarize_profile(directory: str, tail: int = 30) -> None:
 EAGER_OPS = False  # --eager: launch op-benchmark kernels directly (PMC passes)
 
 
-def _event_time(fn, iters: int) -> float:
+def _event_time(fn, iters: int, replays: int = 7) -> float:
     """Mean device seconds per call of `fn`: `iters` calls captured in one
-    hipGraph (so Python launch overhead is not timed), replayed and timed
-    with HIP events on the replay stream. With --eager the calls are
-    launched directly (rocprofv3 counter passes see only such dispatches)."""
+    hipGraph (so Python launch overhead is not timed), replayed `replays`
+    times back to back, each replay timed with HIP events on the replay
+    stream; the median replay is returned. (Single timed replays were
+    bimodal on these boxes: a replay that follows host-side idle time runs
+    ~4 % slower at the 8B decode shape.) With --eager the calls are launched
+    directly (rocprofv3 counter passes see only such dispatches)."""
     import torch
 
     for _ in range(3):
@@ -473,13 +476,15 @@ def _event_time(fn, iters: int) -> float:
             fn()
     graph.replay()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
     with torch.cuda.stream(stream):
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-    end.synchronize()
-    return start.elapsed_time(end) / 1e3 / iters
+        events[0].record(stream)
+        for i in range(replays):
+            graph.replay()
+            events[i + 1].record(stream)
+    events[-1].synchronize()
+    times = sorted(events[i].elapsed_time(events[i + 1]) for i in range(replays))
+    return times[len(times) // 2] / 1e3 / iters
 
 
 def _cpu_time(fn, reps: int = 5) -> float:
