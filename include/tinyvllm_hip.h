@@ -125,12 +125,13 @@ int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
  * rows, offsets (num_rows + 1; only offsets[r], the start of row r's table, is
  * read - a CSR or pitched per-slot rows), lengths, blocks: int64 device vectors.
  * workspace: >= tvllm_paged_decode_workspace_size(...) bytes (may be NULL
- * when that size is 0). head_dim 128 with group <= 16 runs the MFMA kernel
- * (GQA heads share each K/V load); any other head_dim <= 256 or group runs a
- * slower generic kernel (one wave per query head, no MFMA).
+ * when that size is 0). head_dim 128 with group <= 16 and 16-byte aligned
+ * rows runs the MFMA kernel; any other head_dim <= 256, group or alignment
+ * runs the general kernel (one wave per row, KV head and group of up to 16
+ * query heads, sharing each K/V load; fp32 arithmetic, no MFMA).
  * cache_dtype: dtype (caches hold q's element type; k_scale = v_scale = 1)
  * or TVLLM_FP8_E4M3 (caches hold E4M3 bytes in the paged layout;
- * K = stored * k_scale, V = stored * v_scale; head_dim 128, group <= 16).
+ * K = stored * k_scale, V = stored * v_scale).
  * Replaces: torch.ops.tinyvllm_cuda.paged_decode
  *           (reference tinyvllm/kernels/paged_decode.cu:469-669, wrapper
  *            tinyvllm/kernels/paged_decode.py:10-32). */
@@ -345,6 +346,9 @@ int tvllm_resolve_tokens(int64_t* tokens, const int64_t* src, const int64_t* pre
  * tvllm_paged_decode. Items with q_offsets[i+1] - q_offsets[i] <= 0 are
  * skipped. max_query_len bounds every item's query length (grid size).
  * cache_dtype / k_scale / v_scale as for tvllm_paged_decode.
+ * head_dim 128 runs the MFMA kernel (16-byte aligned Q and cache rows, cache
+ * strides in whole 8-element units); any other head_dim <= 256 runs the
+ * general kernel of tvllm_paged_decode (fp32, one wave per query token).
  * workspace: >= tvllm_paged_prefill_workspace_size(dtype, cache_dtype)
  * bytes, 4-byte aligned, zero before the first call; every call leaves it
  * zero. (A bf16 cache's V is converted to fp16 for the P.V products; a call

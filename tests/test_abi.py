@@ -155,7 +155,7 @@ def test_decode_workspace_sizes():
     # 4 waves x 4 workgroups, two KV heads per workgroup.
     assert lib.tvllm_paged_decode_workspace_size(16, 64, 8, 128, 32768, 16) == \
         16 * 64 * 4 * 130 * 4
-    # Groups above 16 run the one-wave-per-head kernel: no splits, no
+    # Groups above 16 run the general kernel: no splits, no
     # workspace (the no-alloc entry point then never rejects them).
     assert lib.tvllm_paged_decode_workspace_size(63, 64, 2, 128, 16384, 16) == 0
     assert lib.tvllm_paged_decode_workspace_size(1, 17, 1, 128, 32768, 16) == 0

@@ -1,5 +1,7 @@
 """Paged decode and chunked prefill against the oracle over seeded random
-configurations: GQA groups 1-16, head dims 64/128/256, page sizes 1-32
+configurations: GQA groups 1-32, head dims 32-256 (128 on the MFMA
+kernels; 32, 36, 64, 96 and 256, and groups above 16, on the general
+kernel, 36 through its unvectorised loads), page sizes 1-32
 (powers of two and not), bf16 / fp16 queries, bf16 / fp16 / FP8 E4M3
 caches, both storage layouts, ragged lengths with empty rows, query rows
 picked out of a larger token axis and max_context_len hints above the
@@ -23,16 +25,16 @@ from test_gpu_kernels import _Cache
 
 pytestmark = pytest.mark.gpu
 
-DECODE_CASES = 28
-PREFILL_CASES = 16
+DECODE_CASES = 36
+PREFILL_CASES = 26
 
 
 def _decode_config(seed: int) -> dict:
     r = random.Random(1000 + seed)
     kv_heads = r.choice([1, 2, 4, 8])
-    group = r.choice([1, 2, 3, 4, 5, 8, 16])
-    head_dim = r.choice([128, 128, 128, 64, 256])
-    cache = r.choice(["same", "same", "fp8"]) if head_dim == 128 else "same"
+    group = r.choice([1, 2, 3, 4, 5, 8, 16, 20, 32])
+    head_dim = r.choice([128, 128, 128, 64, 256, 32, 96, 36])
+    cache = r.choice(["same", "same", "fp8"])
     block_size = r.choice([16, 16, 16, 1, 2, 5, 8, 32])
     longest = r.choice([1, 17, 300, 2500, 6000])
     batch = r.randint(1, 12 if longest <= 2500 else 5)
@@ -109,13 +111,14 @@ def test_decode_random_configuration(device, seed):
 def _prefill_config(seed: int) -> dict:
     r = random.Random(2000 + seed)
     kv_heads = r.choice([1, 2, 4, 8])
-    group = r.choice([1, 2, 4, 8])
+    group = r.choice([1, 2, 4, 8, 16, 24])
+    head_dim = r.choice([128, 128, 128, 64, 256, 32, 96, 36])
     items = []
     for _ in range(r.randint(1, 6)):
         q_len = r.choice([1, r.randint(2, 40), r.randint(41, 300), 512])
         history = r.choice([0, 0, r.randint(1, 200), r.randint(200, 3000)])
         items.append((history + q_len, q_len))
-    return dict(kv_heads=kv_heads, heads=kv_heads * group, items=items,
+    return dict(kv_heads=kv_heads, heads=kv_heads * group, items=items, head_dim=head_dim,
                 block_size=r.choice([16, 16, 1, 4, 5, 8, 12, 32]),
                 cache=r.choice(["bf16", "bf16", "fp16", "fp8"]),
                 layout=r.choice(["head_major", "token_major"]))
@@ -123,8 +126,8 @@ def _prefill_config(seed: int) -> dict:
 
 def _prefill_id(seed: int) -> str:
     c = _prefill_config(seed)
-    return (f"s{seed}-h{c['heads']}kv{c['kv_heads']}-bs{c['block_size']}-{c['cache']}-"
-            f"{c['layout']}-{len(c['items'])}items-q{sum(q for _, q in c['items'])}")
+    return (f"s{seed}-h{c['heads']}kv{c['kv_heads']}-d{c['head_dim']}-bs{c['block_size']}-"
+            f"{c['cache']}-{c['layout']}-{len(c['items'])}items-q{sum(q for _, q in c['items'])}")
 
 
 @pytest.mark.parametrize("seed", range(PREFILL_CASES), ids=_prefill_id)
@@ -134,7 +137,7 @@ def test_prefill_random_configuration(device, seed):
 
     c = _prefill_config(seed)
     g = torch.Generator().manual_seed(seed)
-    bs, d = c["block_size"], 128
+    bs, d = c["block_size"], c["head_dim"]
     contexts = [ctx for ctx, _ in c["items"]]
     pool, blocks, boffsets = _tables(g, contexts, bs)
     k = torch.randn(pool * bs, c["kv_heads"], d, generator=g)

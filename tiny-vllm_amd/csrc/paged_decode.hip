@@ -35,6 +35,7 @@
 //  * 64 tokens per iteration: 16 K and 16 V 16-byte loads per lane in flight
 //    (32 KiB per wave) before any arithmetic waits on them.
 #include "common.h"
+#include "general_attention.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -907,66 +908,6 @@ paged_decode_merge(const float* __restrict__ part_o, const float* __restrict__ p
 }
 
 
-// Any head_dim <= 256 and any group: one wave per (row, query head), one
-// token at a time. Used for shapes the MFMA path does not cover.
-template <typename T>
-__global__ void __launch_bounds__(64)
-paged_decode_generic(const T* __restrict__ q, int64_t qts, int64_t qhs,
-                     const T* __restrict__ k, const T* __restrict__ v, int64_t css,
-                     int64_t chs, T* __restrict__ out, int64_t ots, int64_t ohs,
-                     const int64_t* __restrict__ rows,
-                     const int64_t* __restrict__ blocks,
-                     const int64_t* __restrict__ offsets,
-                     const int64_t* __restrict__ lengths, int heads, int kv_heads,
-                     int head_dim, int block_size, float scale_log2) {
-    const int lane = threadIdx.x;
-    const int r = blockIdx.x / heads;
-    const int h = blockIdx.x - r * heads;
-    const int kvh = h / (heads / kv_heads);
-    const int64_t row = rows[r];
-    const int64_t length = lengths[r];
-    T* o = out + row * ots + h * ohs;
-    if (length == 0) {
-        for (int d = lane; d < head_dim; d += 64) o[d] = static_cast<T>(0.f);
-        return;
-    }
-    float qv[4], acc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        qv[i] = d < head_dim ? to_f<T>(q[row * qts + h * qhs + d]) : 0.f;
-        acc[i] = 0.f;
-    }
-    const int64_t table = offsets[r];
-    float m = -INFINITY, l = 0.f;
-    for (int64_t t = 0; t < length; ++t) {
-        const int64_t page = t / block_size;
-        const int64_t slot = blocks[table + page] * block_size + (t - page * block_size);
-        const int64_t base = slot * css + kvh * chs;
-        float dot = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int d = lane + 64 * i;
-            if (d < head_dim) dot = fmaf(qv[i], to_f<T>(k[base + d]), dot);
-        }
-        const float sc = wave_sum(dot) * scale_log2;
-        const float mn = fmaxf(m, sc);
-        const float alpha = exp2f(m - mn);
-        const float p = exp2f(sc - mn);
-        l = l * alpha + p;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int d = lane + 64 * i;
-            if (d < head_dim) acc[i] = fmaf(p, to_f<T>(v[base + d]), acc[i] * alpha);
-        }
-        m = mn;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        if (d < head_dim) o[d] = static_cast<T>(acc[i] / l);
-    }
-}
 
 // Launch shape of the MFMA decode kernel. `target` is the number of
 // (row, KV head, split) waves the split heuristic aims for (0 = the default
@@ -1107,8 +1048,8 @@ extern "C" int64_t tvllm_paged_decode_workspace_size(int64_t num_rows,
                                                      int64_t block_size) {
     // Partials of the waves of one workgroup merge in LDS; only contexts
     // split over several workgroups (few rows, long contexts) need HBM
-    // partials for the merge kernel. Groups above 16 take the one-wave-per-
-    // head kernel, which splits nothing.
+    // partials for the merge kernel. Groups above 16 take the general kernel,
+    // which splits nothing (as do head dims other than 128).
     if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || head_dim != 128 ||
         num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > 16)
         return 0;
@@ -1178,18 +1119,38 @@ int paged_decode_impl(
         TVLLM_CHECK(fused == nullptr || fast,
                     "paged_decode_qk_norm_rope: needs head_dim 128, group <= 16 and "
                     "16-byte aligned rows");
-        TVLLM_CHECK(!f8 || fast,
-                    "paged_decode: an FP8 KV cache needs head_dim 128, group <= 16 and "
-                    "16-byte aligned rows");
         if (!fast) {
-            paged_decode_generic<T><<<int(num_rows * num_heads), 64, 0, s>>>(
-                static_cast<const T*>(q), q_token_stride, q_head_stride,
-                static_cast<const T*>(k_cache), static_cast<const T*>(v_cache),
-                cache_slot_stride, cache_head_stride,
-                static_cast<T*>(out), out_token_stride, out_head_stride, rows,
-                blocks, offsets, lengths, int(num_heads), int(num_kv_heads),
-                int(head_dim), int(block_size), scale_log2);
-            return launch_status("paged_decode");
+            // Other head dims, GQA groups above 16 or unaligned rows: the
+            // general kernel (one wave per row, KV head and group of up to 16
+            // query heads; fp32 arithmetic).
+            GeneralAttention g{};
+            g.q = q;
+            g.qts = q_token_stride;
+            g.qhs = q_head_stride;
+            g.k = k_cache;
+            g.v = v_cache;
+            g.css = cache_slot_stride;
+            g.chs = cache_head_stride;
+            g.out = out;
+            g.ots = out_token_stride;
+            g.ohs = out_head_stride;
+            g.rows = rows;
+            g.q_offsets = nullptr;
+            g.blocks = blocks;
+            g.offsets = offsets;
+            g.lengths = lengths;
+            g.num_items = num_rows;
+            g.max_query_len = 1;
+            g.heads = int(num_heads);
+            g.kv_heads = int(num_kv_heads);
+            g.head_dim = int(head_dim);
+            g.block_size = int(block_size);
+            g.dtype = dtype;
+            g.cache_dtype = cache_dtype;
+            g.scale = scale;
+            g.k_scale = k_scale;
+            g.v_scale = v_scale;
+            return launch_general_attention(g, s);
         }
         const SplitPlan plan =
             plan_splits(num_rows, num_kv_heads, max_context_len, block_size);

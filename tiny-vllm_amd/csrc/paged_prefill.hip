@@ -41,6 +41,7 @@
 // (item, KV head) share an XCD's L2, and the causal tiles with the most keys
 // start first.
 #include "common.h"
+#include "general_attention.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -614,7 +615,7 @@ extern "C" int tvllm_paged_prefill(
     int64_t cache_head_stride, int64_t block_size, float scale,
     void* workspace, int64_t workspace_bytes,
     int dtype, int cache_dtype, float k_scale, float v_scale, tvllm_stream_t stream) {
-    TVLLM_CHECK(head_dim == 128, "paged_prefill: head_dim must be 128");
+    TVLLM_CHECK(head_dim > 0 && head_dim <= 256, "paged_prefill: head_dim must be in 1..256");
     const bool f8 = cache_dtype == TVLLM_FP8_E4M3;
     TVLLM_CHECK(f8 || cache_dtype == dtype,
                 "paged_prefill: KV cache dtype must match Q or be FP8 E4M3");
@@ -630,10 +631,6 @@ extern "C" int tvllm_paged_prefill(
     TVLLM_CHECK(cache_layout_ok(num_slots, num_kv_heads, head_dim, cache_slot_stride,
                                 cache_head_stride),
                 "paged_prefill: cache strides must give non-overlapping head rows");
-    TVLLM_CHECK(cache_slot_stride % 8 == 0 && cache_head_stride % 8 == 0 &&
-                    cache_slot_stride * (f8 ? 1 : 2) <= int64_t(UINT32_MAX),
-                "paged_prefill: cache strides must be whole 8-element units "
-                "(slot stride below 2^32 bytes)");
     TVLLM_CHECK(num_items >= 0 && max_query_len >= 0,
                 "paged_prefill: negative sizes");
     TVLLM_CHECK(scale > 0.f && scale < INFINITY, "paged_prefill: scale must be positive");
@@ -647,6 +644,43 @@ extern "C" int tvllm_paged_prefill(
     TVLLM_CHECK(q && k_cache && v_cache && out && q_offsets && blocks &&
                     block_offsets && context_lens,
                 "paged_prefill: null pointer");
+    if (head_dim != 128) {
+        // Other head dims: the general kernel (one wave per query token, KV
+        // head and group of up to 16 query heads; fp32 arithmetic, so no
+        // fallback guard is raised).
+        GeneralAttention g{};
+        g.q = q;
+        g.qts = q_token_stride;
+        g.qhs = q_head_stride;
+        g.k = k_cache;
+        g.v = v_cache;
+        g.css = cache_slot_stride;
+        g.chs = cache_head_stride;
+        g.out = out;
+        g.ots = out_token_stride;
+        g.ohs = out_head_stride;
+        g.rows = nullptr;
+        g.q_offsets = q_offsets;
+        g.blocks = blocks;
+        g.offsets = block_offsets;
+        g.lengths = context_lens;
+        g.num_items = num_items;
+        g.max_query_len = max_query_len;
+        g.heads = int(num_heads);
+        g.kv_heads = int(num_kv_heads);
+        g.head_dim = int(head_dim);
+        g.block_size = int(block_size);
+        g.dtype = dtype;
+        g.cache_dtype = cache_dtype;
+        g.scale = scale;
+        g.k_scale = k_scale;
+        g.v_scale = v_scale;
+        return launch_general_attention(g, as_hip(stream));
+    }
+    TVLLM_CHECK(cache_slot_stride % 8 == 0 && cache_head_stride % 8 == 0 &&
+                    cache_slot_stride * (f8 ? 1 : 2) <= int64_t(UINT32_MAX),
+                "paged_prefill: cache strides must be whole 8-element units "
+                "(slot stride below 2^32 bytes)");
     TVLLM_CHECK(aligned16(q) && q_token_stride % 8 == 0 && q_head_stride % 8 == 0 &&
                     aligned16(k_cache) && aligned16(v_cache),
                 "paged_prefill: Q and caches must be 16-byte aligned rows");

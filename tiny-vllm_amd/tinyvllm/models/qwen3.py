@@ -155,7 +155,7 @@ class Qwen3Attention(nn.Module):
         # Decode-only steps on a backend that takes the qkv projection as
         # split-K partials: the fused decode kernel sums them itself.
         from_partials = getattr(attention, "attend_qkv_partials", None)
-        if from_partials is not None and attention.takes_qkv_partials:
+        if from_partials is not None and attention.takes_qkv_partials(self.num_heads):
             parts = self.qkv_proj.decode_partials(hidden_states)
             if parts is not None:
                 out = from_partials(layer_idx, parts, self.num_heads, self.q_norm.weight,

@@ -2,12 +2,15 @@
 (reference: tinyvllm/runtime/attention.py:12-348).
 
 ``HipAttention`` (the default, "hip") runs everything on the gfx950 kernels:
-  * decode-only steps: one kernel per layer does QK-norm + RoPE, the
-    slot-mapped KV write and split-K paged decode attention;
+  * decode-only steps (head dim 128, GQA group <= 16): one kernel per layer
+    does QK-norm + RoPE, the slot-mapped KV write and split-K paged decode
+    attention;
   * other steps, ``prepare_qkv``: QK-norm + RoPE with the KV write fused in;
   * decode rows (query length 1): split-K paged decode attention;
   * multi-query rows (fresh prompts and chunks with history): MFMA paged
-    prefill attention, reading the just-written chunk from the cache too.
+    prefill attention, reading the just-written chunk from the cache too;
+  * other head dims (up to 256; the reference dispatches 32, 64, 128, 256)
+    take the same calls, served by the library's general kernel.
 ``SDPAAttention`` ("reference") is the reference's own torch algorithm
 (gather in logical order + ``F.scaled_dot_product_attention``) kept for
 cross-checking; it is only used when selected explicitly.
@@ -42,11 +45,19 @@ class HipAttention:
         self._written_layer = -1
         self._fused = None
 
-    @property
-    def takes_qkv_partials(self) -> bool:
+    def fuses_decode(self, num_heads: int) -> bool:
+        """Decode-only steps whose shape the fused decode kernel takes (head
+        dim 128, GQA group <= 16): QK-norm + RoPE + KV write + attention in
+        one launch. Other head dims run the unfused kernels (QK-norm + RoPE
+        with the KV write, then the general paged-attention kernel)."""
+        group = num_heads // self.cache.num_kv_heads
+        return (self.kv.prefill is None and self.kv.decode is not None
+                and self.cache.head_dim == 128 and 1 <= group <= 16)
+
+    def takes_qkv_partials(self, num_heads: int) -> bool:
         """Decode-only steps: the fused decode kernel can take the qkv
         projection as split-K partials (``attend_qkv_partials``)."""
-        return self.kv.prefill is None and self.kv.decode is not None
+        return self.fuses_decode(num_heads)
 
     def attend_qkv_partials(self, layer_idx, parts, num_heads, q_weight, k_weight, cos, sin,
                             q_eps, k_eps, *, scale):
@@ -65,7 +76,7 @@ class HipAttention:
         (QK-norm + RoPE + KV write + attention in one launch). Otherwise
         normalise/rotate Q and K and write K/V into their cache slots in one
         kernel and return (q, None, None) - K/V now live in the cache."""
-        if self.kv.prefill is None and self.kv.decode is not None:
+        if self.fuses_decode(q.shape[1]):
             self._fused = (layer_idx, k, v, q_weight, k_weight, cos, sin, q_eps, k_eps)
             return q, None, None
         q, _ = qk_norm_rope_store(
@@ -152,8 +163,8 @@ def check_backend(name: str, model: torch.nn.Module) -> str:
     if parameter.device.type != "cuda" or parameter.dtype not in (torch.float16,
                                                                    torch.bfloat16):
         raise ValueError("GPU attention requires float16 or bfloat16 weights on the GPU")
-    if name == "hip" and config.head_dim != 128:
-        raise ValueError("the hip backend's paged kernels require head_dim 128")
+    if name == "hip" and not (0 < config.head_dim <= 256 and config.head_dim % 2 == 0):
+        raise ValueError("the hip backend's paged kernels take even head dims up to 256")
     if config.num_attention_heads % config.num_key_value_heads:
         raise ValueError("query heads must be divisible by KV heads")
     from tinyvllm.kernels._extension import load_kernels
