@@ -21,6 +21,7 @@
 #include "general_attention.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace tvllm {
 namespace {
@@ -28,6 +29,15 @@ namespace {
 constexpr int GH = 16;     // query heads per wave
 constexpr int DMAX = 256;  // largest head dim
 constexpr float kLog2eG = 1.4426950408889634f;
+constexpr int kRowWaves = 4;  // waves per workgroup of the row-tiled kernel
+
+// Orders one wave's LDS writes before its own later reads (no other wave is
+// involved): a compiler barrier - the wave's LDS operations run in order.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // Eight elements of a cache row starting at element e (FP8: bytes), as
 // floats; elements at or past `left` read as 0.
@@ -136,7 +146,7 @@ __global__ void __launch_bounds__(64) general_attention_kernel(GeneralAttention 
             load8<T, F8, VEC>(a.k, kb + d, D - d, x);
 #pragma unroll
             for (int g = 0; g < GH; ++g) {
-                if (g >= gw) break;  // uniform
+                if (g >= gw) continue;  // uniform
                 const float4 qa = *reinterpret_cast<const float4*>(&qs[g][d]);
                 const float4 qb = *reinterpret_cast<const float4*>(&qs[g][d + 4]);
                 float v = s[g];
@@ -155,7 +165,7 @@ __global__ void __launch_bounds__(64) general_attention_kernel(GeneralAttention 
         // every chunk maximum is finite.
 #pragma unroll
         for (int g = 0; g < GH; ++g) {
-            if (g >= gw) break;
+            if (g >= gw) continue;
             const float sg = valid ? s[g] : -INFINITY;
             const float mn = fmaxf(m[g], wave_max(sg));
             const float alpha = exp2f(m[g] - mn);
@@ -182,7 +192,7 @@ __global__ void __launch_bounds__(64) general_attention_kernel(GeneralAttention 
             }
 #pragma unroll
             for (int g = 0; g < GH; ++g) {
-                if (g >= gw) break;
+                if (g >= gw) continue;
                 const float p = ps[g][j];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(p, vv[i], acc[g][i]);
@@ -193,12 +203,268 @@ __global__ void __launch_bounds__(64) general_attention_kernel(GeneralAttention 
 
 #pragma unroll
     for (int g = 0; g < GH; ++g) {
-        if (g >= gw) break;
+        if (g >= gw) continue;
         const float inv = a.v_scale / l[g];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int d = lane + 64 * i;
             if (d < D) out[(h0 + g) * a.ohs + d] = static_cast<T>(acc[g][i] * inv);
+        }
+    }
+}
+
+// The reference's head dims (32, 64, 128, 256) with vector-aligned rows.
+// A workgroup serves up to 16 (query token, query head) rows of one KV head:
+// one query's group of heads (up to 16), or for groups below 16 several
+// consecutive queries of one prefill item, each row with its own causal
+// bound. Its four waves take interleaved chunks of KPC keys: LPK lanes share
+// a key (each holds EPL <= 64 of its dims), K and V pieces of the whole
+// chunk are loaded at once and the wave's next chunk is in flight during
+// this chunk's P.V; V is staged in the wave's own LDS buffer (FP8 widened
+// exactly to T) for P.V with the lanes over the dims, each key's
+// probabilities broadcast from the lanes that scored it. The waves' (max,
+// sum, accumulator) merge through LDS at the end.
+template <typename T, bool F8, int D>
+__global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralAttention a) {
+    constexpr int LPK = D > 64 ? D / 64 : 1;  // lanes per key
+    constexpr int EPL = D / LPK;               // elements per lane
+    constexpr int KPC = 64 / LPK;              // keys per chunk
+    constexpr int NV = EPL / 8;                // 8-element pieces per lane
+    constexpr int DI = (D + 63) / 64;          // output dims per lane
+    using Piece = std::conditional_t<F8, uint2, uint4>;  // native vectors: kept in registers
+    constexpr int NW = kRowWaves;
+    // LDS: the rows' queries and each wave's staged V chunk; after the key
+    // loop the same bytes hold waves 1..NW-1's partial results for the merge.
+    constexpr int kMain = GH * D * 4 + NW * KPC * D * 2;
+    constexpr int kMerge = (NW - 1) * GH * (D + 2) * 4;
+    __shared__ __align__(16) unsigned char smem[kMain > kMerge ? kMain : kMerge];
+    float (*const qs)[D] = reinterpret_cast<float (*)[D]>(smem);
+    const int wave = threadIdx.x >> 6;
+    U16x8 (*const vs)[D / 8] =
+        reinterpret_cast<U16x8 (*)[D / 8]>(smem + GH * D * 4 + wave * KPC * D * 2);
+
+    const int lane = threadIdx.x & 63;
+    const int group = a.heads / a.kv_heads;
+    const int hpq = group >= GH ? GH : group;   // heads per query in a wave
+    const int qpw = group >= GH ? 1 : GH / group;  // queries per wave
+    const int chunks = (group + GH - 1) / GH;
+    const int64_t bx = blockIdx.x;
+    const int hc = int(bx % chunks);
+    const int64_t ik = bx / chunks;
+    const int kvh = int(ik % a.kv_heads);
+    const int64_t item = ik / a.kv_heads;
+    const int64_t q0 = int64_t(blockIdx.y) * qpw;
+
+    int64_t tok0, qlen;
+    if (a.rows) {
+        tok0 = a.rows[item];
+        qlen = 1;
+    } else {
+        tok0 = a.q_offsets[item];
+        qlen = a.q_offsets[item + 1] - tok0;
+        if (q0 >= qlen) return;  // uniform per workgroup
+        tok0 += q0;
+    }
+    const int64_t nq = min<int64_t>(qpw, qlen - q0);
+    const int g0 = hc * GH;
+    const int hw = min(hpq, group - g0);
+    const int nrows = int(nq) * hw;
+    const int64_t ctx = a.lengths[item];
+    const int64_t first_end = ctx - qlen + q0 + 1;  // causal bound of the wave's first query
+    const int64_t kv_max = first_end + nq - 1;       // ... and of its last
+    const float qscale = a.scale * kLog2eG * a.k_scale;
+    const T* const q = static_cast<const T*>(a.q);
+    T* const out = static_cast<T*>(a.out);
+    auto row_token = [&](int r) { return tok0 + r / hw; };
+    auto row_head = [&](int r) { return kvh * group + g0 + r % hw; };
+
+    for (int r = 0; r < nrows; ++r)
+        for (int d = threadIdx.x; d < D; d += 64 * NW)
+            qs[r][d] = to_f<T>(q[row_token(r) * a.qts + row_head(r) * a.qhs + d]) * qscale;
+    __syncthreads();
+
+    float m[GH], l[GH], acc[GH][DI];
+#pragma unroll
+    for (int r = 0; r < GH; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < DI; ++i) acc[r][i] = 0.f;
+    }
+    const int64_t table = a.offsets[item];
+    const int bs = a.block_size;
+    const int kp = lane / LPK;    // the lane's key within a chunk
+    const int part = lane % LPK;  // ... and its share of the dims
+    const int64_t lane_off = int64_t(kvh) * a.chs + part * EPL;
+
+    struct Chunk {
+        Piece k[NV], v[NV];
+    };
+    auto load_chunk = [&](int64_t t0) -> Chunk {
+        const int64_t t = max<int64_t>(min(t0 + kp, kv_max - 1), 0);  // a valid row
+        const int64_t page = t / bs;
+        const int64_t base = (a.blocks[table + page] * bs + (t - page * bs)) * a.css + lane_off;
+        Chunk c;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            if constexpr (F8) {
+                c.k[v] = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.k) + base + 8 * v);
+                c.v[v] = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.v) + base + 8 * v);
+            } else {
+                c.k[v] = *reinterpret_cast<const uint4*>(static_cast<const T*>(a.k) + base + 8 * v);
+                c.v[v] = *reinterpret_cast<const uint4*>(static_cast<const T*>(a.v) + base + 8 * v);
+            }
+        }
+        return c;
+    };
+
+    // Wave w takes chunks w, w + NW, ... of the keys.
+    Chunk cur = load_chunk(int64_t(wave) * KPC);
+    for (int64_t t0 = int64_t(wave) * KPC; t0 < kv_max; t0 += NW * KPC) {
+        // The chunk's V pieces into LDS, its K pieces unpacked to floats.
+        float x[NV][8];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            if constexpr (F8) {
+                vs[kp][(part * EPL) / 8 + v] = fp8x8_widen<T>(cur.v[v]);  // exact in T
+                fp8x8_unpack(cur.k[v], x[v]);
+            } else {
+                vs[kp][(part * EPL) / 8 + v] = __builtin_bit_cast(U16x8, cur.v[v]);
+                unpack8<T>(__builtin_bit_cast(U16x8, cur.k[v]), x[v]);
+            }
+        }
+        float s[GH];
+#pragma unroll
+        for (int r = 0; r < GH; ++r) {
+            s[r] = 0.f;
+            if (r < nrows) {  // uniform
+                float y = 0.f;
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    const int d = part * EPL + 8 * v;
+                    const float4 qa = *reinterpret_cast<const float4*>(&qs[r][d]);
+                    const float4 qb = *reinterpret_cast<const float4*>(&qs[r][d + 4]);
+                    y = fmaf(qa.x, x[v][0], y);
+                    y = fmaf(qa.y, x[v][1], y);
+                    y = fmaf(qa.z, x[v][2], y);
+                    y = fmaf(qa.w, x[v][3], y);
+                    y = fmaf(qb.x, x[v][4], y);
+                    y = fmaf(qb.y, x[v][5], y);
+                    y = fmaf(qb.z, x[v][6], y);
+                    y = fmaf(qb.w, x[v][7], y);
+                }
+                s[r] = y;
+            }
+        }
+        const int64_t key = t0 + kp;
+        float pr[GH];  // this lane's key's probability for each row
+#pragma unroll
+        for (int r = 0; r < GH; ++r) {
+            pr[r] = 0.f;
+            if (r >= nrows) continue;
+            float sr = s[r];
+            if constexpr (LPK > 1) sr += __shfl_xor(sr, 1, 64);
+            if constexpr (LPK > 2) sr += __shfl_xor(sr, 2, 64);
+            // Row r (query r / hw) sees keys below its own causal bound.
+            const float sg = key < first_end + r / hw ? sr : -INFINITY;
+            const float mn = fmaxf(m[r], wave_max(sg));
+            const float alpha = mn == -INFINITY ? 1.f : exp2f(m[r] - mn);
+            const float p = sg == -INFINITY ? 0.f : exp2f(sg - mn);
+            l[r] = l[r] * alpha + wave_sum(part == 0 ? p : 0.f);
+#pragma unroll
+            for (int i = 0; i < DI; ++i) acc[r][i] *= alpha;
+            m[r] = mn;
+            pr[r] = p;
+        }
+        wave_sync();  // the chunk's V rows are in LDS
+        // The next chunk's rows (past the end: clamped, valid rows, loaded
+        // unconditionally so the loaded registers are no loop-carried
+        // choice) are in flight during P.V.
+        cur = load_chunk(t0 + NW * KPC);
+        const int n = int(min<int64_t>(KPC, kv_max - t0));
+        const uint16_t* const vrow = reinterpret_cast<const uint16_t*>(&vs[0][0]);
+        // Eight keys at a time: their V elements are read from LDS together,
+        // and each key's probabilities come from the lanes that scored it
+        // (a register broadcast, no LDS round trip).
+        for (int j0 = 0; j0 < n; j0 += 8) {
+            float vv[8][DI];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+                for (int i = 0; i < DI; ++i) {
+                    const int d = lane + 64 * i;
+                    vv[jj][i] = (j0 + jj < n && d < D)
+                        ? to_f<T>(__builtin_bit_cast(T, vrow[(j0 + jj) * D + d])) : 0.f;
+                }
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                if (j0 + jj >= n) continue;  // uniform
+#pragma unroll
+                for (int r = 0; r < GH; ++r) {
+                    if (r >= nrows) continue;
+                    const float p = __builtin_bit_cast(
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr[r]),
+                                                         (j0 + jj) * LPK));
+#pragma unroll
+                    for (int i = 0; i < DI; ++i) acc[r][i] = fmaf(p, vv[jj][i], acc[r][i]);
+                }
+            }
+        }
+        wave_sync();  // the wave's V buffer is rewritten by the next chunk
+    }
+
+    // Merge the waves' partial results: out = sum_w 2^(m_w - M) acc_w /
+    // sum_w 2^(m_w - M) l_w per row (M the largest m_w); a row with no key
+    // in any wave gives zeros.
+    __syncthreads();  // every wave is past its last LDS read of qs and vs
+    float* const part_acc = reinterpret_cast<float*>(smem);          // [NW-1][GH][D]
+    float* const part_ml = part_acc + (NW - 1) * GH * D;             // [NW-1][GH][2]
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < GH; ++r) {
+            if (r >= nrows) continue;
+            float* const pa = part_acc + ((wave - 1) * GH + r) * D;
+#pragma unroll
+            for (int i = 0; i < DI; ++i) {
+                const int d = lane + 64 * i;
+                if (d < D) pa[d] = acc[r][i];
+            }
+            if (lane == 0) {
+                part_ml[((wave - 1) * GH + r) * 2] = m[r];
+                part_ml[((wave - 1) * GH + r) * 2 + 1] = l[r];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int r = 0; r < GH; ++r) {
+        if (r >= nrows) continue;
+        float mx = m[r];
+        for (int w = 1; w < NW; ++w) mx = fmaxf(mx, part_ml[((w - 1) * GH + r) * 2]);
+        float den = 0.f;
+        float num[DI];
+        const float w0 = mx == -INFINITY ? 0.f : exp2f(m[r] - mx);
+        den = w0 * l[r];
+#pragma unroll
+        for (int i = 0; i < DI; ++i) num[i] = w0 * acc[r][i];
+        for (int w = 1; w < NW; ++w) {
+            const float mw = part_ml[((w - 1) * GH + r) * 2];
+            const float ww = mx == -INFINITY ? 0.f : exp2f(mw - mx);
+            den += ww * part_ml[((w - 1) * GH + r) * 2 + 1];
+            const float* const pa = part_acc + ((w - 1) * GH + r) * D;
+#pragma unroll
+            for (int i = 0; i < DI; ++i) {
+                const int d = lane + 64 * i;
+                if (d < D) num[i] += ww * pa[d];
+            }
+        }
+        const float inv = den > 0.f ? a.v_scale / den : 0.f;
+        T* const o = out + row_token(r) * a.ots + row_head(r) * a.ohs;
+#pragma unroll
+        for (int i = 0; i < DI; ++i) {
+            const int d = lane + 64 * i;
+            if (d < D) o[d] = static_cast<T>(num[i] * inv);
         }
     }
 }
@@ -218,10 +484,25 @@ int launch_general_attention(const GeneralAttention& g, hipStream_t stream) {
     const bool f8 = g.cache_dtype == TVLLM_FP8_E4M3;
     const bool vec = g.head_dim % 8 == 0 && g.css % 8 == 0 && g.chs % 8 == 0 &&
                      (f8 ? aligned8(g.k) && aligned8(g.v) : aligned16(g.k) && aligned16(g.v));
-    const dim3 grid{static_cast<uint32_t>(gx), static_cast<uint32_t>(gy), 1u};
+    const int D = g.head_dim;
+    const bool rows_kernel = vec && (D == 32 || D == 64 || D == 128 || D == 256);
+    const int group = g.heads / g.kv_heads;
+    const int64_t qpw = rows_kernel && group < GH ? GH / group : 1;
+    const int64_t gy_rows = g.rows ? 1 : (g.max_query_len + qpw - 1) / qpw;
+    const dim3 grid{static_cast<uint32_t>(gx), static_cast<uint32_t>(rows_kernel ? gy_rows : gy),
+                    1u};
     return dispatch_half(g.dtype, [&]<int DT>() {
         using T = typename Elem<DT>::T;
-        if (f8 && vec) general_attention_kernel<T, true, true><<<grid, 64, 0, stream>>>(g);
+        if (rows_kernel) {
+            auto go = [&]<int DD>() {
+                if (f8) rows_attention_kernel<T, true, DD><<<grid, 64 * kRowWaves, 0, stream>>>(g);
+                else rows_attention_kernel<T, false, DD><<<grid, 64 * kRowWaves, 0, stream>>>(g);
+            };
+            if (D == 32) go.template operator()<32>();
+            else if (D == 64) go.template operator()<64>();
+            else if (D == 128) go.template operator()<128>();
+            else go.template operator()<256>();
+        } else if (f8 && vec) general_attention_kernel<T, true, true><<<grid, 64, 0, stream>>>(g);
         else if (f8) general_attention_kernel<T, true, false><<<grid, 64, 0, stream>>>(g);
         else if (vec) general_attention_kernel<T, false, true><<<grid, 64, 0, stream>>>(g);
         else general_attention_kernel<T, false, false><<<grid, 64, 0, stream>>>(g);
