@@ -413,10 +413,26 @@ def summarize_profile(directory: str, tail: int = 30) -> None:
         def dur(r):
             return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
 
-        decode = [dur(r) for r in trace if "paged_decode_d128" in r["Kernel_Name"]]
-        if len(decode) >= tail:
-            print(f"-- paged_decode_d128: mean of the last {tail} dispatches "
-                  f"(bench.py's roofline loop) = {sum(decode[-tail:]) / tail:.2f} us")
+        # bench.py's roofline loop: graph replays of the attention launch
+        # alone, i.e. the last run of >= `tail` paged_decode_d128 dispatches
+        # with no other kernel between them; its timed part is the last 7
+        # replays of `tail` launches each.
+        runs, cur = [], []
+        for r in trace:
+            if "paged_decode_d128" in r["Kernel_Name"]:
+                cur.append(dur(r))
+            else:
+                if len(cur) >= tail:
+                    runs.append(cur)
+                cur = []
+        if len(cur) >= tail:
+            runs.append(cur)
+        if runs:
+            timed = runs[-1][-7 * tail:]
+            print(f"-- paged_decode_d128: roofline loop of {len(runs[-1])} back-to-back "
+                  f"dispatches; mean of its last {len(timed)} (the timed replays) = "
+                  f"{sum(timed) / len(timed):.2f} us, median "
+                  f"{sorted(timed)[len(timed) // 2]:.2f} us")
         ends = [i for i, r in enumerate(trace) if "sample_kernel" in r["Kernel_Name"]]
         if len(ends) >= 2:
             step = trace[ends[-2] + 1:ends[-1] + 1]
