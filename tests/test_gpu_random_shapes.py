@@ -311,3 +311,39 @@ def test_sampling_random_configuration(device, seed):
                 assert int(drawn[i]) == int(greedy[i]), (step, i)
             else:
                 assert bool(kept[i][int(drawn[i])]), (step, i, int(drawn[i]))
+
+
+@pytest.mark.parametrize("head_dim,group", [(128, 4), (64, 4), (128, 32), (36, 2)],
+                         ids=["mfma", "rows-d64", "rows-group32", "scalar-d36"])
+def test_decode_padded_rows_with_one_past_the_end_offsets(device, head_dim, group):
+    """The engine's decode graphs pad a batch with rows of length 0 whose
+    table offset is one past the end of the block tables (the reference's
+    padding). Every decode kernel path must return zeros for them without
+    reading a table entry, and the real rows must still match the oracle."""
+    from tinyvllm.kernels.paged_decode import paged_decode_attention
+    from tinyvllm.runtime.contracts import SingleQueryMetadata
+
+    g = torch.Generator().manual_seed(77)
+    kv_heads, bs = 2, 16
+    lengths = [40, 0, 300, 0]
+    pool, blocks, csr = _tables(g, lengths, bs)
+    offsets = csr.clone()
+    for i, n in enumerate(lengths):
+        if n == 0:
+            offsets[i] = blocks.numel()  # one past the end
+    k = torch.randn(pool * bs, kv_heads, head_dim, generator=g).to(torch.bfloat16)
+    v = torch.randn(pool * bs, kv_heads, head_dim, generator=g).to(torch.bfloat16)
+    q = torch.randn(len(lengths), kv_heads * group, head_dim, generator=g).to(torch.bfloat16)
+    cache = _Cache(k.to(device), v.to(device), bs)
+    rows = torch.arange(len(lengths))
+    lens = torch.tensor(lengths)
+    meta = SingleQueryMetadata(rows.to(device), blocks.to(device), offsets.to(device),
+                               lens.to(device), 512)
+    out = torch.full(q.shape, 7.0, dtype=q.dtype, device=device)
+    paged_decode_attention(q.to(device), cache, 0, meta, out, scale=head_dim ** -0.5)
+    torch.cuda.synchronize()
+    expect = torch.zeros_like(q)
+    OA.decode_attention(q, k, v, rows, blocks, csr, lens, bs, head_dim ** -0.5, expect)
+    out = out.cpu()
+    assert (out[1] == 0).all() and (out[3] == 0).all()
+    assert_bf16_close(out, expect)

@@ -278,6 +278,13 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
     auto row_token = [&](int r) { return tok0 + r / hw; };
     auto row_head = [&](int r) { return kvh * group + g0 + r % hw; };
 
+    if (kv_max <= 0) {  // no key for any row (a padded decode row): zeros, and
+                        // no read of its block table, which may hold no entry
+        for (int r = 0; r < nrows; ++r)
+            for (int d = threadIdx.x; d < D; d += 64 * NW)
+                out[row_token(r) * a.ots + row_head(r) * a.ohs + d] = static_cast<T>(0.f);
+        return;  // uniform per workgroup
+    }
     for (int r = 0; r < nrows; ++r)
         for (int d = threadIdx.x; d < D; d += 64 * NW)
             qs[r][d] = to_f<T>(q[row_token(r) * a.qts + row_head(r) * a.qhs + d]) * qscale;
