@@ -186,6 +186,26 @@ __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);  // v_exp_f32; inputs here are <= 0
 }
 
+// The query's norm weights and RoPE angles (lane: dims c*32 + quad*8 + e),
+// loaded in the kernel prologue ahead of the first K/V rows.
+struct RopeIn {
+    U16x8 w[4], c[2], s[2];
+};
+
+template <typename T>
+__device__ __forceinline__ RopeIn load_rope_in(const T* __restrict__ w, const T* __restrict__ cs,
+                                               const T* __restrict__ sn, int quad) {
+    RopeIn in;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) in.w[c] = *reinterpret_cast<const U16x8*>(w + c * 32 + quad * 8);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        in.c[c] = *reinterpret_cast<const U16x8*>(cs + c * 32 + quad * 8);
+        in.s[c] = *reinterpret_cast<const U16x8*>(sn + c * 32 + quad * 8);
+    }
+    return in;
+}
+
 // Fused QK-norm + RoPE for the decode step (head_dim 128), with the
 // rounding points of the standalone kernel (reference pointwise.cu:325-450):
 //   n = round(round(x * rsqrt(mean(x^2) + eps)) * w);
@@ -193,9 +213,7 @@ __device__ __forceinline__ float fast_exp2(float x) {
 // Query: in place on the MFMA B operand (lane = head col, quad; dims c*32 +
 // quad*8 + e), the sum of squares reduced over the four quads.
 template <typename T>
-__device__ __forceinline__ void rope_query(U16x8 (&qb)[4], const T* __restrict__ w,
-                                           const T* __restrict__ cs,
-                                           const T* __restrict__ sn, float eps, int quad) {
+__device__ __forceinline__ void rope_query(U16x8 (&qb)[4], const RopeIn& in, float eps) {
     float x[4][8];
     float ss = 0.f;
 #pragma unroll
@@ -209,12 +227,11 @@ __device__ __forceinline__ void rope_query(U16x8 (&qb)[4], const T* __restrict__
     const float inv = rsqrtf(ss * (1.0f / 128.f) + eps);
     float wv[4][8], cv[2][8], sv[2][8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-        unpack8<T>(*reinterpret_cast<const U16x8*>(w + c * 32 + quad * 8), wv[c]);
+    for (int c = 0; c < 4; ++c) unpack8<T>(in.w[c], wv[c]);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        unpack8<T>(*reinterpret_cast<const U16x8*>(cs + c * 32 + quad * 8), cv[c]);
-        unpack8<T>(*reinterpret_cast<const U16x8*>(sn + c * 32 + quad * 8), sv[c]);
+        unpack8<T>(in.c[c], cv[c]);
+        unpack8<T>(in.s[c], sv[c]);
     }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -456,6 +473,9 @@ paged_decode_d128(DecodeArgs<T> a) {
                 for (int w = 0; w < 4; ++w) qb[c].w[w] = has ? qb[c].w[w] : 0u;
         };
         if constexpr (!PARTS) load_q();
+        RopeIn rope_in;
+        if constexpr (FUSED)
+            rope_in = load_rope_in<T>(a.qw, a.cos_t + row * 64, a.sin_t + row * 64, quad);
         // The wave's range is walked in groups of 64 * IDR pages. Lane p
         // holds the block ids of pages p, p + 64, ... of the group in
         // registers (fetched once per group; only the low word: ids < 2^32,
@@ -637,12 +657,16 @@ paged_decode_d128(DecodeArgs<T> a) {
             load_k(first);
             load_v(first);
         }
+        // The query's QK-norm + RoPE stays behind the first chunk's loads:
+        // without this barrier the scheduler hoists it, and the waits for its
+        // inputs, above them (0.5 us per launch at the 8B bs64 shape).
+        if constexpr (FUSED) __builtin_amdgcn_sched_barrier(0);
         if constexpr (FUSED) {
             // QK-norm + RoPE of the raw query while the first K/V rows are in
             // flight, in the B-operand layout: lane (head col, quad) holds dims
             // c*32 + quad*8 + e; the RoPE pair of dim d < 64 is d + 64, two
             // k-slices up in the same lane.
-            rope_query<T>(qb, a.qw, a.cos_t + row * 64, a.sin_t + row * 64, a.q_eps, quad);
+            rope_query<T>(qb, rope_in, a.q_eps);
         }
         // The first chunk's K words pass through an empty asm: otherwise the
         // compiler merges this load and the loop's load of the next chunk
