@@ -328,7 +328,8 @@ def engine_decode_step(model, cfg, batch: int, context: int, steps: int,
         raise RuntimeError(f"engine benchmark: {tokens} tokens in {steps} steps of {batch} rows")
     unfinished = engine.has_unfinished()
     engine.close()
-    assert unfinished  # no request ended inside the timed steps
+    if not unfinished:
+        raise RuntimeError("engine benchmark: requests ended inside the timed steps")
     return {"engine_ms_per_step": round(elapsed / steps * 1e3, 3),
             "engine_tok_s": round(tokens / elapsed, 1),
             "engine_steps": steps,
