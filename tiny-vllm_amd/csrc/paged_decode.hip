@@ -410,26 +410,21 @@ paged_decode_d128(DecodeArgs<T> a) {
     if (t_begin < t_end) {
         const int64_t table = a.offsets[r];
 
-        // Prologue loads go out together: the query, the new token's slot,
-        // then (below) the first group of block ids, ahead of the new
-        // token's K/V write - each would otherwise cost a memory round trip
-        // of its own at short contexts.
+        // The new token's slot (a scalar load, issued with the row's metadata).
         const int64_t new_slot = FUSED ? a.slots[row] : -1;
         NewKV<T> new_kv{};
-        if constexpr (PARTS) {
-            const float* prow = a.parts + row * a.pts;
-            new_kv = load_new_kv_parts<T>(prow + (a.heads + kvh) * D,
-                                          prow + (a.heads + a.kv_heads + kvh) * D, a.pss, a.kw,
-                                          a.cos_t + row * 64, a.sin_t + row * 64, lane);
-        } else if constexpr (FUSED) {
-            new_kv = load_new_kv<T>(a.kraw + row * a.krts + kvh * a.krhs,
-                                    a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
-                                    a.cos_t + row * 64, a.sin_t + row * 64, lane);
-        }
         // B operand: query head g = col (zero beyond the group), dims c*32 + quad*8.
         U16x8 qb[4];
-        // The query's B operand (the partial sums, PARTS, are loaded after
-        // the block ids so that the sums' wait does not hold those back).
+        // The query's B operand, loaded after the block ids (below). Lanes
+        // beyond the group hold zeros (fused: set after its QK-norm + RoPE,
+        // so that nothing ahead of the first K/V loads waits for the query).
+        auto mask_q = [&]() {
+            const bool has = col < a.group;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) qb[c].w[w] = has ? qb[c].w[w] : 0u;
+        };
         auto load_q = [&]() {
             const bool has = col < a.group;
             const int hq = h0 + (has ? col : 0);
@@ -467,15 +462,9 @@ paged_decode_d128(DecodeArgs<T> a) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) qb[c] = *reinterpret_cast<const U16x8*>(qrow + c * 32);
             }
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-#pragma unroll
-                for (int w = 0; w < 4; ++w) qb[c].w[w] = has ? qb[c].w[w] : 0u;
+            if constexpr (!FUSED) mask_q();
         };
-        if constexpr (!PARTS) load_q();
         RopeIn rope_in;
-        if constexpr (FUSED)
-            rope_in = load_rope_in<T>(a.qw, a.cos_t + row * 64, a.sin_t + row * 64, quad);
         // The wave's range is walked in groups of 64 * IDR pages. Lane p
         // holds the block ids of pages p, p + 64, ... of the group in
         // registers (fetched once per group; only the low word: ids < 2^32,
@@ -624,14 +613,30 @@ paged_decode_d128(DecodeArgs<T> a) {
         // every wave keeps HBM requests in flight while it computes. The
         // last chunk of a group loads clamped (cached) rows instead of
         // branching, so the loop's wait counts never cover a skipped path.
+        // Prologue order: the block ids first, then the query, its RoPE
+        // inputs and (fused) the new token's raw K/V row. Vector loads
+        // complete in issue order, so the wait for the ids - all the first
+        // K/V loads need - does not include the rest. In a decode step the
+        // query and the new row come from the qkv GEMM just written on other
+        // XCDs and miss this XCD's cache: issued before the ids they held
+        // the first K/V loads back (8B bs64 decode step 7.92 -> 7.85 ms).
+        // The new row's loads are used only by the wave that writes it, so
+        // the compiler issues them in that wave's branch.
         load_group();
-        if constexpr (PARTS) load_q();
+        load_q();
+        if constexpr (FUSED)
+            rope_in = load_rope_in<T>(a.qw, a.cos_t + row * 64, a.sin_t + row * 64, quad);
+        if constexpr (PARTS) {
+            const float* prow = a.parts + row * a.pts;
+            new_kv = load_new_kv_parts<T>(prow + (a.heads + kvh) * D,
+                                          prow + (a.heads + a.kv_heads + kvh) * D, a.pss, a.kw,
+                                          a.cos_t + row * 64, a.sin_t + row * 64, lane);
+        } else if constexpr (FUSED) {
+            new_kv = load_new_kv<T>(a.kraw + row * a.krts + kvh * a.krhs,
+                                    a.vraw + row * a.vrts + kvh * a.vrhs, a.kw,
+                                    a.cos_t + row * 64, a.sin_t + row * 64, lane);
+        }
         if constexpr (FUSED) {
-            // Keep the new row's loads here, in flight with the query and the
-            // block ids (the compiler would sink them into the writer's branch).
-            asm volatile("" : "+v"(new_kv.x1), "+v"(new_kv.x2), "+v"(new_kv.w1), "+v"(new_kv.w2),
-                         "+v"(new_kv.c), "+v"(new_kv.s));
-            asm volatile("" : "+v"(new_kv.v1), "+v"(new_kv.v2));
             // The row's new token (position length - 1) is written by the
             // wave whose page range holds it, before that wave reads it.
             if (t_begin <= length - 1 && length - 1 < t_end) {
@@ -667,6 +672,7 @@ paged_decode_d128(DecodeArgs<T> a) {
             // c*32 + quad*8 + e; the RoPE pair of dim d < 64 is d + 64, two
             // k-slices up in the same lane.
             rope_query<T>(qb, rope_in, a.q_eps);
+            mask_q();
         }
         // The first chunk's K words pass through an empty asm: otherwise the
         // compiler merges this load and the loop's load of the next chunk
