@@ -107,7 +107,9 @@ int64_t tvllm_paged_decode_workspace_size(int64_t num_rows, int64_t num_heads,
 
 /* The split-K decomposition tvllm_paged_decode uses for this geometry,
  * packed as (waves per KV head << 16) | (workgroups per row << 8) | (KV heads
- * per workgroup); 0 for the generic path. It depends on max_context_len, so a
+ * per workgroup) for the MFMA kernel, (1 << 32) | (workgroups per row, KV
+ * head and head chunk) for the general kernel (head_dim != 128 or groups
+ * above 16), 0 for invalid geometry. It depends on max_context_len, so a
  * caller that bakes launches (graph capture) can tell when a tighter context
  * bound would change it. No reference counterpart (the reference kernel has
  * no split-K). */
@@ -127,8 +129,10 @@ int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_heads,
  * workspace: >= tvllm_paged_decode_workspace_size(...) bytes (may be NULL
  * when that size is 0). head_dim 128 with group <= 16 and 16-byte aligned
  * rows runs the MFMA kernel; any other head_dim <= 256, group or alignment
- * runs the general kernel (one wave per row, KV head and group of up to 16
- * query heads, sharing each K/V load; fp32 arithmetic, no MFMA).
+ * runs the general kernel (a workgroup of four waves per row, KV head and
+ * group of up to 16 query heads, sharing each K/V load; when such units are
+ * few, each row's keys split over several workgroups and a second launch
+ * merges their partials; fp32 arithmetic, no MFMA).
  * cache_dtype: dtype (caches hold q's element type; k_scale = v_scale = 1)
  * or TVLLM_FP8_E4M3 (caches hold E4M3 bytes in the paged layout;
  * K = stored * k_scale, V = stored * v_scale).
@@ -155,8 +159,9 @@ int tvllm_paged_decode(const void* q, int64_t q_token_stride,
  * harnesses that forbid hipMalloc). No counterpart in the reference. The
  * split-K partials go to a static 8 MiB device array per GPU (held until
  * the process ends); a geometry whose tvllm_paged_decode_workspace_size
- * exceeds 8 MiB is rejected with TVLLM_EINVAL (the default split plan needs
- * at most ~6 MB). Allocates nothing. Calls that
+ * exceeds 8 MiB is rejected with TVLLM_EINVAL (the MFMA kernel's split plan
+ * needs at most ~6 MB; the general kernel's can need more at head_dim 256
+ * with groups of 16). Allocates nothing. Calls that
  * overlap on one GPU (different streams) share that array and race; calls
  * ordered on one stream are safe. The first call on a device looks up the
  * array's address (hipGetSymbolAddress): make it outside graph capture. */
@@ -348,7 +353,8 @@ int tvllm_resolve_tokens(int64_t* tokens, const int64_t* src, const int64_t* pre
  * cache_dtype / k_scale / v_scale as for tvllm_paged_decode.
  * head_dim 128 runs the MFMA kernel (16-byte aligned Q and cache rows, cache
  * strides in whole 8-element units); any other head_dim <= 256 runs the
- * general kernel of tvllm_paged_decode (fp32, one wave per query token).
+ * general kernel of tvllm_paged_decode (fp32; a workgroup per KV head and
+ * up to 16 (query token, query head) rows of one item).
  * workspace: >= tvllm_paged_prefill_workspace_size(dtype, cache_dtype)
  * bytes, 4-byte aligned, zero before the first call; every call leaves it
  * zero. (A bf16 cache's V is converted to fp16 for the P.V products; a call

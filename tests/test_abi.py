@@ -155,11 +155,20 @@ def test_decode_workspace_sizes():
     # 4 waves x 4 workgroups, two KV heads per workgroup.
     assert lib.tvllm_paged_decode_workspace_size(16, 64, 8, 128, 32768, 16) == \
         16 * 64 * 4 * 130 * 4
-    # Groups above 16 run the general kernel: no splits, no
-    # workspace (the no-alloc entry point then never rejects them).
-    assert lib.tvllm_paged_decode_workspace_size(63, 64, 2, 128, 16384, 16) == 0
-    assert lib.tvllm_paged_decode_workspace_size(1, 17, 1, 128, 32768, 16) == 0
+    # Groups above 16 and other head dims run the general kernel, which
+    # splits a context over workgroups (toward 512 of them) only when there
+    # are few (row, KV head, 16-head chunk) units: 63 rows x 2 KV heads x 2
+    # chunks = 252 units -> 3 splits; 2 units -> 64 splits.
+    assert lib.tvllm_paged_decode_workspace_size(63, 64, 2, 128, 16384, 16) == \
+        63 * 64 * 3 * 130 * 4
+    assert lib.tvllm_paged_decode_workspace_size(1, 17, 1, 128, 32768, 16) == \
+        17 * 64 * 130 * 4
     assert lib.tvllm_paged_decode_workspace_size(1, 16, 1, 128, 32768, 16) > 0
+    assert lib.tvllm_paged_decode_workspace_size(1, 32, 8, 64, 32768, 16) == 32 * 64 * 66 * 4
+    assert lib.tvllm_paged_decode_workspace_size(64, 32, 8, 64, 2048, 16) == 0  # 512 units
+    # A split keeps at least two 64-key chunks per wave of its four at head
+    # dim 64: a 1000-token context splits twice at most.
+    assert lib.tvllm_paged_decode_workspace_size(1, 8, 8, 64, 1000, 16) == 8 * 2 * 66 * 4
     # The largest request of any plan with group <= 16 fits the no-alloc
     # entry point's 8 MiB scratch.
     worst = max(lib.tvllm_paged_decode_workspace_size(rows, kv * g, kv, 128, ctx, 16)
@@ -197,7 +206,10 @@ def test_decode_split_plans():
                for ctx in (16, 512, 4096, 32768, 131072, 1 << 20)) <= 64
 
 
-def test_decode_workspace_at_the_longest_context_covers_shorter_ones():
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [
+    (64, 8, 128), (16, 8, 64), (8, 2, 256), (16, 4, 32), (40, 2, 128)])
+def test_decode_workspace_at_the_longest_context_covers_shorter_ones(heads, kv_heads,
+                                                                     head_dim):
     """The runner sizes the decode workspace once, at max_model_len, for every
     row count; a launch's plan follows its batch's longest context."""
     from tinyvllm.kernels._extension import load_kernels
@@ -205,9 +217,11 @@ def test_decode_workspace_at_the_longest_context_covers_shorter_ones():
     lib = load_kernels()
     for max_len in (2048, 8192, 40960):
         for rows in (1, 2, 3, 4, 8, 12, 16, 31, 32, 33, 64):
-            cap = lib.tvllm_paged_decode_workspace_size(rows, 64, 8, 128, max_len, 16)
+            cap = lib.tvllm_paged_decode_workspace_size(rows, heads, kv_heads, head_dim,
+                                                        max_len, 16)
             for ctx in range(16, max_len + 1, 16 * 37):
-                assert lib.tvllm_paged_decode_workspace_size(rows, 64, 8, 128, ctx, 16) <= cap
+                assert lib.tvllm_paged_decode_workspace_size(
+                    rows, heads, kv_heads, head_dim, ctx, 16) <= cap
 
 
 def test_decode_split_plan_under_tuning_override_keeps_the_merge_bound():

@@ -142,6 +142,24 @@ def test_decode_fp8_cache_matches_oracle(device, heads, kv_heads, lengths, max_c
     assert_bf16_close(out, expect)
 
 
+@pytest.mark.parametrize("head_dim,heads,kv_heads,lengths,scales", [
+    (64, 8, 2, [20000, 0, 300], (1.0, 0.25)),
+    (256, 4, 2, [9000, 1], (0.5, 2.0)),
+])
+def test_decode_fp8_general_kernel_splits(device, head_dim, heads, kv_heads, lengths, scales):
+    """The general kernel over an FP8 cache with its keys split over
+    workgroups (few rows, long contexts)."""
+    pool = sum(max(1, -(-n // 16)) for n in lengths) + 8
+    case = paged_decode_case(seed=head_dim, batch=len(lengths), heads=heads,
+                             kv_heads=kv_heads, head_dim=head_dim, pool_blocks=pool,
+                             lengths=lengths)
+    out, expect = _decode(case, device, *scales, max(lengths))
+    for r, n in enumerate(lengths):
+        if n == 0:
+            assert (out[r] == 0).all()
+    assert_bf16_close(out, expect)
+
+
 def test_decode_fp8_cache_fp16_queries(device):
     case = paged_decode_case(seed=5, batch=6, heads=32, kv_heads=8, pool_blocks=1024)
     out, expect = _decode(case, device, 1.0, 1.0, 1024, dtype=torch.float16)

@@ -153,6 +153,33 @@ def test_decode_generic_shapes(device, head_dim, block_size, layout):
     assert_bf16_close(out, expect)
 
 
+@pytest.mark.parametrize("head_dim,heads,kv_heads,lengths", [
+    (64, 8, 2, [0, 20000, 1, 4097]),   # 64 splits; an empty row and a 1-token row
+    (256, 4, 1, [12000, 300]),         # most splits of the short row hold no key
+    (32, 16, 4, [9000]),
+    (128, 64, 2, [15000, 0, 700]),     # GQA group 32: the general kernel at head dim 128
+])
+def test_decode_general_kernel_splits_long_contexts(device, head_dim, heads, kv_heads, lengths):
+    """Few rows with long contexts on the general kernel (head dims other
+    than 128, groups above 16): the keys split over workgroups, whose
+    partials a second launch merges."""
+    from tinyvllm.kernels.paged_decode import decode_split_plan, decode_workspace_bytes
+
+    pool = sum(-(-n // 16) for n in lengths) + 8
+    case = paged_decode_case(seed=head_dim + heads, batch=len(lengths), heads=heads,
+                             kv_heads=kv_heads, head_dim=head_dim, pool_blocks=pool,
+                             lengths=lengths)
+    max_ctx = max(lengths)
+    plan = decode_split_plan(len(lengths), heads, kv_heads, head_dim, max_ctx, 16)
+    assert plan >> 32 == 1 and plan & 0xFFFF > 1, plan  # general kernel, split
+    assert decode_workspace_bytes(len(lengths), heads, kv_heads, head_dim, max_ctx, 16) > 0
+    out, expect = _run_decode(case, device, max_context_len=max_ctx)
+    for r, n in enumerate(lengths):
+        if n == 0:
+            assert (out[r] == 0).all()
+    assert_bf16_close(out, expect)
+
+
 def test_decode_fp16(device):
     case = paged_decode_case(seed=21, batch=6, heads=32, kv_heads=8, pool_blocks=512,
                              dtype=torch.float16)

@@ -30,10 +30,34 @@ struct GeneralAttention {
     int dtype, cache_dtype;
     float scale;             // softmax scale
     float k_scale, v_scale;  // FP8 cache dequantisation scales (1 otherwise)
+    // Decode only: the bound on lengths[] that sizes the launch, and the
+    // workspace that holds the partials of contexts split over several
+    // workgroups (general_decode_workspace bytes; may be null when that is 0).
+    int64_t max_context;
+    void* workspace;
+    int64_t workspace_bytes;
+    // Filled in by the launcher: the split plan and the partials' arrays.
+    int64_t splits, split_keys;
+    float* part_o;   // [num_items][heads][splits][head_dim]
+    float* part_ml;  // [num_items][heads][splits][2]: (max, sum) in base 2
 };
 
+// Grid-level key splits of a decode launch of the general kernel (1: none):
+// enough workgroups to fill the chip when there are few (row, KV head) units,
+// each split keeping at least two rounds of chunks for each of its waves.
+struct GeneralSplits {
+    int64_t splits;  // workgroups per (row, KV head, head chunk)
+    int64_t keys;    // keys per split (a multiple of the kernel's chunk)
+};
+GeneralSplits general_decode_splits(int64_t rows, int64_t heads, int64_t kv_heads,
+                                    int64_t head_dim, int64_t max_context);
+// Workspace bytes a decode launch of this geometry needs (0 when unsplit).
+int64_t general_decode_workspace(int64_t rows, int64_t heads, int64_t kv_heads,
+                                 int64_t head_dim, int64_t max_context);
+
 // Validated by the caller (geometry, dtypes, cache layout); enqueues one
-// launch on `stream`.
+// launch on `stream` (two for a split decode: the split workgroups, then
+// the merge of their partials).
 int launch_general_attention(const GeneralAttention& g, hipStream_t stream);
 
 }  // namespace tvllm

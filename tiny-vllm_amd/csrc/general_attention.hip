@@ -253,7 +253,10 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
     const int64_t ik = bx / chunks;
     const int kvh = int(ik % a.kv_heads);
     const int64_t item = ik / a.kv_heads;
-    const int64_t q0 = int64_t(blockIdx.y) * qpw;
+    // Prefill: y is the workgroup's tile of queries. Decode: its split of
+    // the row's keys (one query).
+    const int64_t q0 = a.rows ? 0 : int64_t(blockIdx.y) * qpw;
+    const int64_t split = a.rows ? int64_t(blockIdx.y) : 0;
 
     int64_t tok0, qlen;
     if (a.rows) {
@@ -277,6 +280,18 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
     T* const out = static_cast<T*>(a.out);
     auto row_token = [&](int r) { return tok0 + r / hw; };
     auto row_head = [&](int r) { return kvh * group + g0 + r % hw; };
+    // Keys [k_begin, k_end) of this split (all of them when unsplit).
+    const int64_t k_begin = split * a.split_keys;
+    const int64_t k_end = a.splits > 1 ? min(kv_max, k_begin + a.split_keys) : kv_max;
+    auto part_index = [&](int r) { return (item * a.heads + row_head(r)) * a.splits + split; };
+
+    if (a.splits > 1 && k_begin >= k_end) {  // no key of the row in this split
+        for (int r = threadIdx.x; r < nrows; r += 64 * NW) {
+            a.part_ml[2 * part_index(r)] = -INFINITY;  // the merge skips it
+            a.part_ml[2 * part_index(r) + 1] = 0.f;
+        }
+        return;  // uniform per workgroup
+    }
 
     if (kv_max <= 0) {  // no key for any row (a padded decode row): zeros, and
                         // no read of its block table, which may hold no entry
@@ -326,8 +341,8 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
     };
 
     // Wave w takes chunks w, w + NW, ... of the keys.
-    Chunk cur = load_chunk(int64_t(wave) * KPC);
-    for (int64_t t0 = int64_t(wave) * KPC; t0 < kv_max; t0 += NW * KPC) {
+    Chunk cur = load_chunk(k_begin + int64_t(wave) * KPC);
+    for (int64_t t0 = k_begin + int64_t(wave) * KPC; t0 < k_end; t0 += NW * KPC) {
         // The chunk's V pieces into LDS, its K pieces unpacked to floats.
         float x[NV][8];
 #pragma unroll
@@ -373,7 +388,7 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
             if constexpr (LPK > 1) sr += __shfl_xor(sr, 1, 64);
             if constexpr (LPK > 2) sr += __shfl_xor(sr, 2, 64);
             // Row r (query r / hw) sees keys below its own causal bound.
-            const float sg = key < first_end + r / hw ? sr : -INFINITY;
+            const float sg = key < first_end + r / hw && key < k_end ? sr : -INFINITY;
             const float mn = fmaxf(m[r], wave_max(sg));
             const float alpha = mn == -INFINITY ? 1.f : exp2f(m[r] - mn);
             const float p = sg == -INFINITY ? 0.f : exp2f(sg - mn);
@@ -388,7 +403,7 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
         // unconditionally so the loaded registers are no loop-carried
         // choice) are in flight during P.V.
         cur = load_chunk(t0 + NW * KPC);
-        const int n = int(min<int64_t>(KPC, kv_max - t0));
+        const int n = int(min<int64_t>(KPC, k_end - t0));
         const uint16_t* const vrow = reinterpret_cast<const uint16_t*>(&vs[0][0]);
         // Eight keys at a time: their V elements are read from LDS together,
         // and each key's probabilities come from the lanes that scored it
@@ -466,6 +481,19 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
                 if (d < D) num[i] += ww * pa[d];
             }
         }
+        if (a.splits > 1) {  // the split's partials, merged by general_merge
+            float* const po = a.part_o + part_index(r) * D;
+#pragma unroll
+            for (int i = 0; i < DI; ++i) {
+                const int d = lane + 64 * i;
+                if (d < D) po[d] = num[i];
+            }
+            if (lane == 0) {
+                a.part_ml[2 * part_index(r)] = mx;
+                a.part_ml[2 * part_index(r) + 1] = den;
+            }
+            continue;
+        }
         const float inv = den > 0.f ? a.v_scale / den : 0.f;
         T* const o = out + row_token(r) * a.ots + row_head(r) * a.ohs;
 #pragma unroll
@@ -476,9 +504,91 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
     }
 }
 
+// Merge a split decode: out = v_scale * sum_s 2^(m_s - M) o_s / sum_s
+// 2^(m_s - M) l_s, M the largest m_s; splits with no key (m_s = -inf) are
+// skipped, so their o_s is never read, and a row with none gives zeros. One
+// wave per (row, query head): lane s holds split s's (max, sum) (splits <=
+// 64), lane l the output dims l, l + 64, ...
+template <typename T, int D>
+__global__ void __launch_bounds__(64)
+general_merge(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+              T* __restrict__ out, const int64_t* __restrict__ rows, int64_t ots, int64_t ohs,
+              int heads, int splits, float v_scale) {
+    constexpr int DI = (D + 63) / 64;
+    const int id = blockIdx.x;
+    const int r = id / heads;
+    const int h = id - r * heads;
+    const int lane = threadIdx.x;
+    const int64_t base = (int64_t(r) * heads + h) * splits;
+    float m = -INFINITY, l = 0.f;
+    if (lane < splits) {
+        m = part_ml[2 * (base + lane)];
+        l = part_ml[2 * (base + lane) + 1];
+    }
+    const float mx = wave_max(m);
+    T* const o = out + rows[r] * ots + h * ohs;
+    float acc[DI];
+#pragma unroll
+    for (int i = 0; i < DI; ++i) acc[i] = 0.f;
+    float inv = 0.f;
+    if (mx != -INFINITY) {  // uniform
+        const float w = m == -INFINITY ? 0.f : exp2f(m - mx);
+        inv = v_scale / wave_sum(w * l);
+        for (int s0 = 0; s0 < splits; ++s0) {
+            const float ws = __shfl(w, s0, 64);
+            if (ws == 0.f) continue;  // uniform: an empty split (or a negligible one)
+            const float* const po = part_o + (base + s0) * D;
+#pragma unroll
+            for (int i = 0; i < DI; ++i) {
+                const int d = lane + 64 * i;
+                if (d < D) acc[i] = fmaf(ws, po[d], acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < DI; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) o[d] = static_cast<T>(acc[i] * inv);
+    }
+}
+
+// Keys per chunk of the row-tiled kernel at head dim D (LPK lanes per key).
+int64_t keys_per_chunk(int64_t D) { return D > 64 ? 64 / (D / 64) : 64; }
+
+bool rows_kernel_dim(int64_t D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+
 }  // namespace
 
-int launch_general_attention(const GeneralAttention& g, hipStream_t stream) {
+GeneralSplits general_decode_splits(int64_t rows, int64_t heads, int64_t kv_heads,
+                                    int64_t head_dim, int64_t max_context) {
+    GeneralSplits p{1, max_context};
+    if (rows <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_context <= 0 ||
+        !rows_kernel_dim(head_dim))
+        return p;
+    // Aim for 512 workgroups (two of four waves per CU); a split keeps at
+    // least two rounds of chunks per wave, and one merge lane per split.
+    constexpr int64_t kTarget = 512, kMaxSplits = 64;
+    const int64_t units = rows * kv_heads * ((heads / kv_heads + GH - 1) / GH);
+    const int64_t kpc = keys_per_chunk(head_dim);
+    const int64_t min_keys = 2 * kRowWaves * kpc;
+    int64_t s = std::min((kTarget + units - 1) / units, kMaxSplits);
+    s = std::min(s, (max_context + min_keys - 1) / min_keys);
+    if (s <= 1) return p;
+    // Exactly s splits (a trailing one may hold no key: it writes an empty
+    // partial), so the workspace never shrinks as max_context grows.
+    p.splits = s;
+    p.keys = ((max_context + s - 1) / s + kpc - 1) / kpc * kpc;
+    return p;
+}
+
+int64_t general_decode_workspace(int64_t rows, int64_t heads, int64_t kv_heads,
+                                 int64_t head_dim, int64_t max_context) {
+    const GeneralSplits p = general_decode_splits(rows, heads, kv_heads, head_dim, max_context);
+    return p.splits > 1 ? rows * heads * p.splits * (head_dim + 2) * int64_t(sizeof(float)) : 0;
+}
+
+int launch_general_attention(const GeneralAttention& g_in, hipStream_t stream) {
+    GeneralAttention g = g_in;
     TVLLM_CHECK(g.head_dim > 0 && g.head_dim <= DMAX, "attention: head_dim must be in 1..256");
     TVLLM_CHECK(g.heads > 0 && g.kv_heads > 0 && g.heads % g.kv_heads == 0,
                 "attention: query heads must be a multiple of the KV heads");
@@ -492,10 +602,29 @@ int launch_general_attention(const GeneralAttention& g, hipStream_t stream) {
     const bool vec = g.head_dim % 8 == 0 && g.css % 8 == 0 && g.chs % 8 == 0 &&
                      (f8 ? aligned8(g.k) && aligned8(g.v) : aligned16(g.k) && aligned16(g.v));
     const int D = g.head_dim;
-    const bool rows_kernel = vec && (D == 32 || D == 64 || D == 128 || D == 256);
+    const bool rows_kernel = vec && rows_kernel_dim(D);
     const int group = g.heads / g.kv_heads;
     const int64_t qpw = rows_kernel && group < GH ? GH / group : 1;
-    const int64_t gy_rows = g.rows ? 1 : (g.max_query_len + qpw - 1) / qpw;
+    g.splits = 1;
+    g.split_keys = 0;
+    g.part_o = g.part_ml = nullptr;
+    if (g.rows && rows_kernel) {
+        TVLLM_CHECK(g.max_context > 0, "attention: decode needs a positive max_context");
+        const GeneralSplits p = general_decode_splits(g.num_items, g.heads, g.kv_heads, D,
+                                                      g.max_context);
+        if (p.splits > 1) {
+            const int64_t need = g.num_items * g.heads * p.splits * (D + 2) * int64_t(sizeof(float));
+            TVLLM_CHECK(g.workspace_bytes >= need && g.workspace != nullptr,
+                        "paged_decode: workspace of %lld bytes required, %lld given",
+                        (long long)need, (long long)g.workspace_bytes);
+            TVLLM_CHECK(aligned16(g.workspace), "paged_decode: workspace must be 16-byte aligned");
+            g.splits = p.splits;
+            g.split_keys = p.keys;
+            g.part_o = static_cast<float*>(g.workspace);
+            g.part_ml = g.part_o + g.num_items * g.heads * p.splits * D;
+        }
+    }
+    const int64_t gy_rows = g.rows ? g.splits : (g.max_query_len + qpw - 1) / qpw;
     const dim3 grid{static_cast<uint32_t>(gx), static_cast<uint32_t>(rows_kernel ? gy_rows : gy),
                     1u};
     return dispatch_half(g.dtype, [&]<int DT>() {
@@ -509,6 +638,20 @@ int launch_general_attention(const GeneralAttention& g, hipStream_t stream) {
             else if (D == 64) go.template operator()<64>();
             else if (D == 128) go.template operator()<128>();
             else go.template operator()<256>();
+            if (g.splits > 1) {
+                const int st = launch_status("attention (general head dims)");
+                if (st != TVLLM_OK) return st;
+                auto merge = [&]<int DD>() {
+                    general_merge<T, DD><<<int(g.num_items * g.heads), 64, 0, stream>>>(
+                        g.part_o, g.part_ml, static_cast<T*>(g.out), g.rows, g.ots, g.ohs,
+                        g.heads, int(g.splits), g.v_scale);
+                };
+                if (D == 32) merge.template operator()<32>();
+                else if (D == 64) merge.template operator()<64>();
+                else if (D == 128) merge.template operator()<128>();
+                else merge.template operator()<256>();
+                return launch_status("attention merge (general head dims)");
+            }
         } else if (f8 && vec) general_attention_kernel<T, true, true><<<grid, 64, 0, stream>>>(g);
         else if (f8) general_attention_kernel<T, true, false><<<grid, 64, 0, stream>>>(g);
         else if (vec) general_attention_kernel<T, false, true><<<grid, 64, 0, stream>>>(g);

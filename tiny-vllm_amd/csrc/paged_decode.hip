@@ -1069,10 +1069,15 @@ extern "C" int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_h
                                                  int64_t num_kv_heads, int64_t head_dim,
                                                  int64_t max_context_len,
                                                  int64_t block_size) {
-    (void)num_heads;
-    if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || head_dim != 128 ||
-        max_context_len <= 0)
+    if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || max_context_len <= 0 ||
+        num_heads % num_kv_heads != 0)
         return 0;
+    if (head_dim != 128 || num_heads / num_kv_heads > 16) {
+        // The general kernel: its workgroup-level split count, tagged.
+        const GeneralSplits g = general_decode_splits(num_rows, num_heads, num_kv_heads,
+                                                      head_dim, max_context_len);
+        return (int64_t(1) << 32) | g.splits;
+    }
     const SplitPlan p = plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
     return (p.waves << 16) | (p.grid << 8) | int64_t(p.heads);
 }
@@ -1085,14 +1090,19 @@ extern "C" int64_t tvllm_paged_decode_workspace_size(int64_t num_rows,
                                                      int64_t block_size) {
     // Partials of the waves of one workgroup merge in LDS; only contexts
     // split over several workgroups (few rows, long contexts) need HBM
-    // partials for the merge kernel. Groups above 16 take the general kernel,
-    // which splits nothing (as do head dims other than 128).
-    if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || head_dim != 128 ||
-        num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > 16)
+    // partials for a merge kernel. Other head dims and groups above 16 take
+    // the general kernel; so do head-dim-128 calls with unaligned rows,
+    // which is why those sizes cover both plans.
+    if (num_rows <= 0 || num_kv_heads <= 0 || block_size <= 0 || max_context_len <= 0 ||
+        num_heads % num_kv_heads != 0)
         return 0;
+    const int64_t general = general_decode_workspace(num_rows, num_heads, num_kv_heads,
+                                                     head_dim, max_context_len);
+    if (head_dim != 128 || num_heads / num_kv_heads > 16) return general;
     const SplitPlan p = plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
-    if (p.grid <= 1) return 0;
-    return num_rows * num_heads * p.grid * (head_dim + 2) * int64_t(sizeof(float));
+    const int64_t mfma = p.grid > 1
+        ? num_rows * num_heads * p.grid * (head_dim + 2) * int64_t(sizeof(float)) : 0;
+    return std::max(mfma, general);
 }
 
 namespace tvllm {
@@ -1158,8 +1168,9 @@ int paged_decode_impl(
                     "16-byte aligned rows");
         if (!fast) {
             // Other head dims, GQA groups above 16 or unaligned rows: the
-            // general kernel (one wave per row, KV head and group of up to 16
-            // query heads; fp32 arithmetic).
+            // general kernel (a workgroup per row, KV head and group of up to
+            // 16 query heads, and split of the keys when there are few of
+            // those; fp32 arithmetic).
             GeneralAttention g{};
             g.q = q;
             g.qts = q_token_stride;
@@ -1187,6 +1198,9 @@ int paged_decode_impl(
             g.scale = scale;
             g.k_scale = k_scale;
             g.v_scale = v_scale;
+            g.max_context = max_context_len;
+            g.workspace = workspace;
+            g.workspace_bytes = workspace_bytes;
             return launch_general_attention(g, s);
         }
         const SplitPlan plan =
