@@ -180,6 +180,18 @@ def test_decode_general_kernel_splits_long_contexts(device, head_dim, heads, kv_
     assert_bf16_close(out, expect)
 
 
+@pytest.mark.parametrize("head_dim,heads", [(128, 32), (64, 32), (256, 8)])
+def test_decode_rows_longer_than_max_context_len(device, head_dim, heads):
+    """max_context_len only sizes the split plan: rows longer than it still
+    attend all their keys (both kernels)."""
+    lengths = [9000, 300, 4100]
+    case = paged_decode_case(seed=head_dim + 1, batch=3, heads=heads, kv_heads=8,
+                             head_dim=head_dim, pool_blocks=sum(-(-n // 16) for n in lengths) + 4,
+                             lengths=lengths)
+    out, expect = _run_decode(case, device, max_context_len=1024)
+    assert_bf16_close(out, expect)
+
+
 def test_decode_fp16(device):
     case = paged_decode_case(seed=21, batch=6, heads=32, kv_heads=8, pool_blocks=512,
                              dtype=torch.float16)

@@ -280,9 +280,12 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
     T* const out = static_cast<T*>(a.out);
     auto row_token = [&](int r) { return tok0 + r / hw; };
     auto row_head = [&](int r) { return kvh * group + g0 + r % hw; };
-    // Keys [k_begin, k_end) of this split (all of them when unsplit).
+    // Keys [k_begin, k_end) of this split (all of them when unsplit). The
+    // last split also takes any keys past splits * split_keys (a row longer
+    // than the max_context the plan was sized for): slow, never wrong.
     const int64_t k_begin = split * a.split_keys;
-    const int64_t k_end = a.splits > 1 ? min(kv_max, k_begin + a.split_keys) : kv_max;
+    const int64_t k_end = a.splits > 1 && split + 1 < a.splits
+        ? min(kv_max, k_begin + a.split_keys) : kv_max;
     auto part_index = [&](int r) { return (item * a.heads + row_head(r)) * a.splits + split; };
 
     if (a.splits > 1 && k_begin >= k_end) {  // no key of the row in this split
