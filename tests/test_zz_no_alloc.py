@@ -101,8 +101,8 @@ def test_noalloc_rejects_geometry_beyond_scratch():
 @pytest.mark.gpu
 def test_noalloc_decode_random_sequence(device):
     """Eight seeded geometries in a row on the same static scratch (row
-    counts, GQA groups up to 32 - above 16 the general kernel,
-    which needs no scratch - long and short contexts, either cache
+    counts, GQA groups up to 32 - above 16 the general kernel, whose
+    split partials use the same scratch - long and short contexts, either cache
     nesting), each bit-identical to the workspace entry point."""
     import random
 
