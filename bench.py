@@ -356,12 +356,19 @@ def kernel_only(args) -> None:
     hq, hkv, d = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     pages = math.ceil(ctx / bs)
     layers = 8  # visited in turn: no launch finds its KV in the memory-side cache
+    fp8 = args.kv_cache_dtype == "fp8_e4m3"
     cache = PagedKVCache(num_layers=layers, num_blocks=rows * pages, block_size=bs,
-                         num_kv_heads=hkv, head_dim=d, device=device, dtype=torch.bfloat16,
+                         num_kv_heads=hkv, head_dim=d, device=device,
+                         dtype=torch.float8_e4m3fn if fp8 else torch.bfloat16,
                          layout=resolve_layout(args.kv_layout, rows, hkv))
     gen = torch.Generator(device=device).manual_seed(1)
-    cache.key.normal_(generator=gen)
-    cache.value.normal_(generator=gen)
+    if fp8:  # N(0, 1) values quantised layer by layer (scales 1)
+        for layer in range(layers):
+            for t in (cache.key[layer], cache.value[layer]):
+                t.copy_(torch.randn(t.shape, generator=gen, device=device))
+    else:
+        cache.key.normal_(generator=gen)
+        cache.value.normal_(generator=gen)
     perm = torch.randperm(rows * pages, device=device, generator=gen)
     max_len = 4096
     meta = SingleQueryMetadata(torch.arange(rows, device=device), perm,
@@ -388,6 +395,7 @@ def kernel_only(args) -> None:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"kernel_only": True, "rows": rows, "context": ctx,
+                      "kv_cache_dtype": "fp8_e4m3" if fp8 else "bf16",
                       "decode_launches": args.steps, "copy_bytes": src.numel() * 2}))
 
 
@@ -1020,7 +1028,7 @@ def main() -> None:
     if fp8:  # N(0, 1) values quantised layer by layer
         for layer in range(cache.num_layers):
             for t in (cache.key[layer], cache.value[layer]):
-                t.copy_(torch.randn(t.shape, generator=gen, device=device).to(t.dtype))
+                t.copy_(torch.randn(t.shape, generator=gen, device=device))
     else:
         cache.key.normal_(generator=gen)
         cache.value.normal_(generator=gen)
