@@ -201,11 +201,15 @@ def test_decode_split_plans():
     assert _plan(lib, 2, 32, 8, 128, 32768, 16) == (8, 16, 1)
     assert _plan(lib, 1, 64, 8, 128, 131072, 16) == (4, 64, 2)
     # Context bounds up to 256: page ranges of at least 64 tokens (four at
-    # 256); past 256, 32-token ranges again.
+    # 256); up to 512: at least 128 (four at 512); past 512, 32-token ranges
+    # again.
     assert _plan(lib, 1, 16, 8, 128, 256, 16) == (4, 1, 1)
     assert _plan(lib, 16, 16, 8, 128, 256, 16) == (4, 1, 1)
     assert _plan(lib, 1, 16, 8, 128, 128, 16) == (2, 1, 2)
-    assert _plan(lib, 1, 16, 8, 128, 257, 16) == (8, 2, 1)
+    assert _plan(lib, 1, 16, 8, 128, 257, 16) == (3, 1, 1)
+    assert _plan(lib, 1, 16, 8, 128, 512, 16) == (4, 1, 1)
+    assert _plan(lib, 16, 16, 8, 128, 512, 16) == (4, 1, 1)
+    assert _plan(lib, 1, 16, 8, 128, 513, 16) == (8, 3, 1)
     # The merge launch holds one workgroup-level split per lane.
     assert max(_plan(lib, rows, 4 * kv, kv, 128, ctx, 16)[1]
                for rows in range(1, 80) for kv in (1, 2, 4, 8)

@@ -998,12 +998,14 @@ int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
     int64_t s = (target + units - 1) / units;
     const int64_t max_pages = (max_context + block_size - 1) / block_size;
     // Each split should own at least one full 32-token iteration; at context
-    // bounds up to 256 two (the short ranges' launch, prologue and merge cost
-    // more than the parallelism returns, and a graph captured for the bound
-    // runs shorter contexts with some ranges empty: Qwen3-0.6B decode steps
-    // at contexts 64 / 200 and 1-16 rows 4-6 % faster, e.g. 1 row x 64
-    // tokens 1.407 -> 1.328 ms; longer bounds measured slower with 64).
-    const int64_t min_tokens = max_context <= 256 ? 64 : 32;
+    // bounds up to 256 two, up to 512 four (short ranges' prologue and merge -
+    // a second launch once the splits outgrow one workgroup - cost more than
+    // the parallelism returns; Qwen3-0.6B decode steps at contexts 64 / 200
+    // and 1-16 rows 4-6 % faster, e.g. 1 row x 64 tokens 1.407 -> 1.328 ms;
+    // the decode launch at 300 / 500 tokens and 1-16 rows 9.2-13.9 us with 4
+    // splits against 11.8-15.5 us with 16-32; at bounds past 512 the 32-token
+    // ranges measured faster).
+    const int64_t min_tokens = max_context <= 256 ? 64 : max_context <= 512 ? 128 : 32;
     const int64_t by_tokens = (max_context + min_tokens - 1) / min_tokens;
     s = std::min(s, std::min(max_pages, by_tokens));
     s = std::min<int64_t>(s, kMaxSplits);

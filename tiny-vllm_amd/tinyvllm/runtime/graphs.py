@@ -27,7 +27,7 @@ def context_buckets(max_model_len: int) -> tuple[int, ...]:
     split-K plan depends on the bound, and a graph baked for max_model_len
     over-splits short contexts (few rows at 64 tokens would run 64 splits
     and a merge launch per layer)."""
-    return tuple(sorted({b for b in (256, 1024, 4096) if b < max_model_len} | {max_model_len}))
+    return tuple(sorted({b for b in (256, 512, 1024, 4096) if b < max_model_len} | {max_model_len}))
 
 
 def bucket_sizes(limit: int) -> tuple[int, ...]:
