@@ -11,8 +11,10 @@ rows exact, temperature / top-k / top-p draws inside the oracle's kept set)
 over vocab sizes around the scan spans, three logit dtypes and tied maxima.
 Each configuration comes from its own seed and is printed in
 the test id; the bar is the one every attention test uses (max abs 2e-2,
-mean relative 1e-3), with empty rows exactly zero."""
+mean relative 1e-3), with empty rows exactly zero. TVLLM_RANDOM_CASES=k
+multiplies every case count by k for a longer sweep."""
 import math
+import os
 import random
 
 import pytest
@@ -25,8 +27,9 @@ from test_gpu_kernels import _Cache
 
 pytestmark = pytest.mark.gpu
 
-DECODE_CASES = 36
-PREFILL_CASES = 26
+_SCALE = max(1, int(os.environ.get("TVLLM_RANDOM_CASES", "1")))
+DECODE_CASES = 36 * _SCALE
+PREFILL_CASES = 26 * _SCALE
 
 
 def _decode_config(seed: int) -> dict:
@@ -163,7 +166,7 @@ def test_prefill_random_configuration(device, seed):
     assert_bf16_close(out.cpu(), expect)
 
 
-FUSED_CASES = 12
+FUSED_CASES = 12 * _SCALE
 
 
 def _fused_config(seed: int) -> dict:
@@ -259,7 +262,7 @@ def test_fused_decode_step_random_configuration(device, seed):
             assert (out[r].cpu() == 0).all()
 
 
-SAMPLING_CASES = 16
+SAMPLING_CASES = 16 * _SCALE
 
 
 def _sampling_config(seed: int) -> dict:
