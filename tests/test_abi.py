@@ -200,6 +200,13 @@ def test_decode_split_plans():
     assert _plan(lib, 1, 32, 8, 128, 32768, 16) == (8, 32, 1)
     assert _plan(lib, 2, 32, 8, 128, 32768, 16) == (8, 16, 1)
     assert _plan(lib, 1, 64, 8, 128, 131072, 16) == (4, 64, 2)
+    # 256+ (row, KV head) units: the largest power-of-two split count with at
+    # most 1024 waves, in four-wave workgroups (one per CU at most).
+    assert _plan(lib, 32, 32, 8, 128, 4096, 16) == (4, 1, 1)
+    assert _plan(lib, 40, 32, 8, 128, 4096, 16) == (2, 1, 2)
+    assert _plan(lib, 56, 32, 8, 128, 4096, 16) == (2, 1, 2)
+    assert _plan(lib, 72, 32, 8, 128, 4096, 16) == (1, 1, 4)
+    assert _plan(lib, 128, 32, 8, 128, 4096, 16) == (1, 1, 4)
     # Context bounds up to 256: page ranges of at least 64 tokens (four at
     # 256); up to 512: at least 128 (four at 512); past 512, 32-token ranges
     # again.

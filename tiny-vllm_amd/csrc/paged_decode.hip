@@ -996,6 +996,17 @@ int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
     const int64_t target = tuning().target ? tuning().target
                                            : (units >= 256 ? 1024 : 2048);
     int64_t s = (target + units - 1) / units;
+    if (!tuning().target && units >= 256) {
+        // One wave per SIMD at most, in whole four-wave workgroups: the
+        // largest power of two with units * s <= 1024. Three ranges make
+        // three-wave workgroups, and past 1024 waves some CUs take two
+        // workgroups while others idle (Qwen3-8B shape, 2048 tokens: 40 / 48
+        // / 56 rows 66 / 71 / 79 us with 2 ranges against 78 / 83 / 90 us
+        // with 4 / 3 / 3; 72 / 80 / 96 rows 121 / 122 / 128 us with 1 against
+        // 135 / 139 / 146 us with 2).
+        s = 1;
+        while (units * s * 2 <= 1024) s *= 2;
+    }
     const int64_t max_pages = (max_context + block_size - 1) / block_size;
     // Each split should own at least one full 32-token iteration; at context
     // bounds up to 256 two, up to 512 four (short ranges' prologue and merge -
