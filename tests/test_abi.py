@@ -200,6 +200,13 @@ def test_decode_split_plans():
     assert _plan(lib, 1, 32, 8, 128, 32768, 16) == (8, 32, 1)
     assert _plan(lib, 2, 32, 8, 128, 32768, 16) == (8, 16, 1)
     assert _plan(lib, 1, 64, 8, 128, 131072, 16) == (4, 64, 2)
+    # Fewer units: at most 256 workgroups - eight ranges times a power-of-two
+    # grid per unit, or one four-wave workgroup per unit past 128 units
+    # (heads not paired there).
+    assert _plan(lib, 8, 32, 8, 128, 4096, 16) == (8, 4, 1)
+    assert _plan(lib, 12, 32, 8, 128, 4096, 16) == (8, 2, 1)
+    assert _plan(lib, 20, 32, 8, 128, 4096, 16) == (4, 1, 1)
+    assert _plan(lib, 28, 32, 8, 128, 4096, 16) == (4, 1, 1)
     # 256+ (row, KV head) units: the largest power-of-two split count with at
     # most 1024 waves, in four-wave workgroups (one per CU at most).
     assert _plan(lib, 32, 32, 8, 128, 4096, 16) == (4, 1, 1)

@@ -996,6 +996,17 @@ int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
     const int64_t target = tuning().target ? tuning().target
                                            : (units >= 256 ? 1024 : 2048);
     int64_t s = (target + units - 1) / units;
+    if (!tuning().target && units < 256) {
+        // At most one workgroup per CU: units * grid <= 256 workgroups of
+        // eight page ranges (grid a power of two), or, when not even two
+        // fit per unit, one four-wave workgroup per unit (Qwen3-8B shape,
+        // 2048 tokens: 12 rows 30 us with 16 ranges against 41 us with 22
+        // (24); 20 / 24 / 28 rows 38 / 41 / 45 us with 4 against 54 / 56 /
+        // 59 us with 13 / 11 / 10 (16)).
+        int64_t g = 1;
+        while (units * g * 2 <= 256) g *= 2;
+        s = g >= 2 || units * 2 <= 256 ? 8 * g : 4;
+    }
     if (!tuning().target && units >= 256) {
         // One wave per SIMD at most, in whole four-wave workgroups: the
         // largest power of two with units * s <= 1024. Three ranges make
@@ -1042,8 +1053,13 @@ SplitPlan plan_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
     // token's cache row at about the same time, which the DRAM serves better
     // than one head's 256-byte pieces alone (C5 decode shape, cold cache:
     // 276 -> 257 us). Short ranges keep one head per workgroup: the extra
-    // grid-level partials would cost more than the locality gains.
-    if (!tuning().overridden && rows * kv_heads < 256 && max_context >= 512 * total) {
+    // grid-level partials would cost more than the locality gains. So do
+    // plans of four ranges (128-255 units, one workgroup each): pairing
+    // heads there halves the workgroups to far fewer than the CUs (20-28
+    // rows of the Qwen3-8B shape at a 4096 bound: 97-106 us against 59-71 us
+    // at 3500 tokens).
+    if (!tuning().overridden && rows * kv_heads < 256 && total >= 8 &&
+        max_context >= 512 * total) {
         split_waves = 4;
         waves = 8;
     }
