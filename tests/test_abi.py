@@ -207,6 +207,11 @@ def test_decode_split_plans():
     assert _plan(lib, 12, 32, 8, 128, 4096, 16) == (8, 2, 1)
     assert _plan(lib, 20, 32, 8, 128, 4096, 16) == (4, 1, 1)
     assert _plan(lib, 28, 32, 8, 128, 4096, 16) == (4, 1, 1)
+    # Groups above 4 (a 16-bit cache's kernel runs 16-token iterations): one
+    # eight-range workgroup per unit past 128 units, and a 2048-wave budget
+    # from 256 units.
+    assert _plan(lib, 24, 64, 8, 128, 4096, 16) == (8, 1, 1)
+    assert _plan(lib, 48, 64, 8, 128, 4096, 16) == (4, 1, 1)
     # 256+ (row, KV head) units: the largest power-of-two split count with at
     # most 1024 waves, in four-wave workgroups (one per CU at most).
     assert _plan(lib, 32, 32, 8, 128, 4096, 16) == (4, 1, 1)

@@ -987,7 +987,10 @@ const Tuning& tuning() {
     return t;
 }
 
-int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
+// narrow: the kernel variant runs one 16-token tile per iteration (a 16-bit
+// cache at GQA groups above 4, an FP8 cache above 8): half the bytes in
+// flight per wave of the other variants, so it wants about twice the waves.
+int64_t choose_splits(int64_t rows, int64_t kv_heads, bool narrow, int64_t max_context,
                       int64_t block_size) {
     const int64_t units = rows * kv_heads;
     if (units <= 0) return 1;
@@ -1003,9 +1006,12 @@ int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
         // 2048 tokens: 12 rows 30 us with 16 ranges against 41 us with 22
         // (24); 20 / 24 / 28 rows 38 / 41 / 45 us with 4 against 54 / 56 /
         // 59 us with 13 / 11 / 10 (16)).
+        // Narrow variants: one eight-wave workgroup per unit there (Qwen3-32B
+        // shape, bf16, 24 rows x 2048 tokens: 43 us with 8 ranges against 52
+        // us with 4).
         int64_t g = 1;
         while (units * g * 2 <= 256) g *= 2;
-        s = g >= 2 || units * 2 <= 256 ? 8 * g : 4;
+        s = g >= 2 || units * 2 <= 256 || narrow ? 8 * g : 4;
     }
     if (!tuning().target && units >= 256) {
         // One wave per SIMD at most, in whole four-wave workgroups: the
@@ -1015,8 +1021,13 @@ int64_t choose_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
         // / 56 rows 66 / 71 / 79 us with 2 ranges against 78 / 83 / 90 us
         // with 4 / 3 / 3; 72 / 80 / 96 rows 121 / 122 / 128 us with 1 against
         // 135 / 139 / 146 us with 2).
+        // Narrow variants: two waves per SIMD, 2048 (Qwen3-32B shape, bf16, 48
+        // rows x 2048 tokens: 80 us with 4 ranges against 93 us with 2; its
+        // FP8 variant, 64 tokens per iteration, keeps 1024: 47 us with 2
+        // against 55 us with 4).
+        const int64_t waves = narrow ? 2048 : 1024;
         s = 1;
-        while (units * s * 2 <= 1024) s *= 2;
+        while (units * s * 2 <= waves) s *= 2;
     }
     const int64_t max_pages = (max_context + block_size - 1) / block_size;
     // Each split should own at least one full 32-token iteration; at context
@@ -1043,9 +1054,10 @@ struct SplitPlan {
 
 int heads_per_group(int64_t kv_heads, int64_t splits, int64_t waves);
 
-SplitPlan plan_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
-                      int64_t block_size) {
-    const int64_t total = choose_splits(rows, kv_heads, max_context, block_size);
+SplitPlan plan_splits(int64_t rows, int64_t kv_heads, int64_t group, bool f8,
+                      int64_t max_context, int64_t block_size) {
+    const bool narrow = group > (f8 ? 8 : 4);
+    const int64_t total = choose_splits(rows, kv_heads, narrow, max_context, block_size);
     int split_waves = tuning().split_waves, waves = tuning().waves;
     // Few (row, KV head) units with long page ranges per split (small batch,
     // long context): workgroups of two KV heads x four page ranges. The two
@@ -1054,12 +1066,10 @@ SplitPlan plan_splits(int64_t rows, int64_t kv_heads, int64_t max_context,
     // than one head's 256-byte pieces alone (C5 decode shape, cold cache:
     // 276 -> 257 us). Short ranges keep one head per workgroup: the extra
     // grid-level partials would cost more than the locality gains. So do
-    // plans of four ranges (128-255 units, one workgroup each): pairing
-    // heads there halves the workgroups to far fewer than the CUs (20-28
-    // rows of the Qwen3-8B shape at a 4096 bound: 97-106 us against 59-71 us
-    // at 3500 tokens).
-    if (!tuning().overridden && rows * kv_heads < 256 && total >= 8 &&
-        max_context >= 512 * total) {
+    // plans past 128 units (one workgroup each): pairing heads there halves
+    // the workgroups to far fewer than the CUs (20-28 rows of the Qwen3-8B
+    // shape at a 4096 bound: 97-106 us against 59-71 us at 3500 tokens).
+    if (!tuning().overridden && rows * kv_heads <= 128 && max_context >= 512 * total) {
         split_waves = 4;
         waves = 8;
     }
@@ -1113,7 +1123,10 @@ extern "C" int64_t tvllm_paged_decode_split_plan(int64_t num_rows, int64_t num_h
                                                       head_dim, max_context_len);
         return (int64_t(1) << 32) | g.splits;
     }
-    const SplitPlan p = plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
+    // The plan of a 16-bit cache (an FP8 cache's can differ where the grid
+    // is 1: the id only groups context bounds into graphs).
+    const SplitPlan p = plan_splits(num_rows, num_kv_heads, num_heads / num_kv_heads, false,
+                                    max_context_len, block_size);
     return (p.waves << 16) | (p.grid << 8) | int64_t(p.heads);
 }
 
@@ -1134,9 +1147,14 @@ extern "C" int64_t tvllm_paged_decode_workspace_size(int64_t num_rows,
     const int64_t general = general_decode_workspace(num_rows, num_heads, num_kv_heads,
                                                      head_dim, max_context_len);
     if (head_dim != 128 || num_heads / num_kv_heads > 16) return general;
-    const SplitPlan p = plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
-    const int64_t mfma = p.grid > 1
-        ? num_rows * num_heads * p.grid * (head_dim + 2) * int64_t(sizeof(float)) : 0;
+    int64_t mfma = 0;
+    for (const bool f8 : {false, true}) {  // the cache dtype is not an argument: cover both
+        const SplitPlan p = plan_splits(num_rows, num_kv_heads, num_heads / num_kv_heads, f8,
+                                        max_context_len, block_size);
+        if (p.grid > 1)
+            mfma = std::max(mfma, num_rows * num_heads * p.grid * (head_dim + 2) *
+                                      int64_t(sizeof(float)));
+    }
     return std::max(mfma, general);
 }
 
@@ -1239,7 +1257,7 @@ int paged_decode_impl(
             return launch_general_attention(g, s);
         }
         const SplitPlan plan =
-            plan_splits(num_rows, num_kv_heads, max_context_len, block_size);
+            plan_splits(num_rows, num_kv_heads, group, f8, max_context_len, block_size);
         const int hpg = plan.heads;
         const int64_t grid = num_rows * (num_kv_heads / hpg) * plan.grid;
         TVLLM_CHECK(grid <= INT32_MAX, "paged_decode: decode grid is too large");
