@@ -994,12 +994,14 @@ int64_t choose_splits(int64_t rows, int64_t kv_heads, bool narrow, int64_t max_c
                       int64_t block_size) {
     const int64_t units = rows * kv_heads;
     if (units <= 0) return 1;
-    // Many (row, KV head) units: few splits; few units (long context, small
-    // batch): split deeper so that the waves still cover all 256 CUs.
-    const int64_t target = tuning().target ? tuning().target
-                                           : (units >= 256 ? 1024 : 2048);
-    int64_t s = (target + units - 1) / units;
-    if (!tuning().target && units < 256) {
+    // Page ranges per (row, KV head): enough waves to cover the 256 CUs, at
+    // most one workgroup per CU (measured over 1-128 rows of the Qwen3-8B and
+    // -32B shapes at 1500-3500 tokens). A tuning override sets the wave
+    // target directly.
+    int64_t s;
+    if (tuning().target) {
+        s = (tuning().target + units - 1) / units;
+    } else if (units < 256) {
         // At most one workgroup per CU: units * grid <= 256 workgroups of
         // eight page ranges (grid a power of two), or, when not even two
         // fit per unit, one four-wave workgroup per unit (Qwen3-8B shape,
@@ -1012,8 +1014,7 @@ int64_t choose_splits(int64_t rows, int64_t kv_heads, bool narrow, int64_t max_c
         int64_t g = 1;
         while (units * g * 2 <= 256) g *= 2;
         s = g >= 2 || units * 2 <= 256 || narrow ? 8 * g : 4;
-    }
-    if (!tuning().target && units >= 256) {
+    } else {
         // One wave per SIMD at most, in whole four-wave workgroups: the
         // largest power of two with units * s <= 1024. Three ranges make
         // three-wave workgroups, and past 1024 waves some CUs take two
