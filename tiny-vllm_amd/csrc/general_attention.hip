@@ -235,13 +235,16 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
     constexpr int NW = kRowWaves;
     // LDS: the rows' queries and each wave's staged V chunk; after the key
     // loop the same bytes hold waves 1..NW-1's partial results for the merge.
-    constexpr int kMain = GH * D * 4 + NW * KPC * D * 2;
+    // Staged V rows are padded by 16 bytes, so the lanes' 16-byte row writes
+    // (one key per lane, rows D * 2 bytes apart) spread over the LDS banks.
+    constexpr int VS = D + 8;  // staged V row stride (elements)
+    constexpr int kMain = GH * D * 4 + NW * KPC * VS * 2;
     constexpr int kMerge = (NW - 1) * GH * (D + 2) * 4;
     __shared__ __align__(16) unsigned char smem[kMain > kMerge ? kMain : kMerge];
     float (*const qs)[D] = reinterpret_cast<float (*)[D]>(smem);
     const int wave = threadIdx.x >> 6;
-    U16x8 (*const vs)[D / 8] =
-        reinterpret_cast<U16x8 (*)[D / 8]>(smem + GH * D * 4 + wave * KPC * D * 2);
+    U16x8 (*const vs)[VS / 8] =
+        reinterpret_cast<U16x8 (*)[VS / 8]>(smem + GH * D * 4 + wave * KPC * VS * 2);
 
     const int lane = threadIdx.x & 63;
     const int group = a.heads / a.kv_heads;
@@ -419,7 +422,7 @@ __global__ void __launch_bounds__(64 * kRowWaves) rows_attention_kernel(GeneralA
                 for (int i = 0; i < DI; ++i) {
                     const int d = lane + 64 * i;
                     vv[jj][i] = (j0 + jj < n && d < D)
-                        ? to_f<T>(__builtin_bit_cast(T, vrow[(j0 + jj) * D + d])) : 0.f;
+                        ? to_f<T>(__builtin_bit_cast(T, vrow[(j0 + jj) * VS + d])) : 0.f;
                 }
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj) {
